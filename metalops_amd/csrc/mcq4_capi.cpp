@@ -1,0 +1,155 @@
+// C ABI of the gfx950 q4_0 path: argument validation, status codes and
+// dispatch to the kernel launchers.  No allocation, no exceptions; everything
+// is enqueued on the caller's stream.
+//
+// Reference boundary replaced: metalcore's pybind11 binding
+// matmul_ggml_q4_0_metal (native/core_mps.mm:5917-5975): shape/dtype checks
+// (core_mps.mm:5923-5938) become status codes, the Metal encode on the current
+// MPS stream (core_mps.mm:5947-5969) becomes a launch on the given HIP stream.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/mcq4.h"
+
+namespace mcq4 {
+hipError_t launch_quantize(bool llama_rule, const float *W, int64_t ldw, int nb, int N,
+                           uint8_t *out, hipStream_t s);
+hipError_t launch_dequant(const uint8_t *blocks, int nb, int N, void *out, int64_t ldo,
+                          bool f16, hipStream_t s);
+size_t skinny_workspace_bytes(int64_t M, int64_t K, int64_t N);
+hipError_t launch_skinny(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                         int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
+size_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N);
+hipError_t launch_gemm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                       int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
+}  // namespace mcq4
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_status(hipError_t e, const char *what) {
+    if (e == hipSuccess) return MCQ4_OK;
+    return fail(MCQ4_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr int64_t kMaxBlocksK = 65535;        // grid.y limit of the conversion kernels
+constexpr int64_t kMaxDim = (int64_t)1 << 30;  // keeps 32-bit lane offsets safe
+
+bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+int check_kn(int64_t K, int64_t N) {
+    if (K <= 0 || N <= 0) return fail(MCQ4_ERR_SHAPE, "K (%lld) and N (%lld) must be positive",
+                                      (long long)K, (long long)N);
+    if (K % 32 != 0) return fail(MCQ4_ERR_SHAPE, "K (%lld) must be divisible by 32", (long long)K);
+    if (K / 32 > kMaxBlocksK || N > kMaxDim || (K / 32) * N * 18 > ((int64_t)1 << 40))
+        return fail(MCQ4_ERR_SHAPE, "shape K=%lld N=%lld exceeds the supported size",
+                    (long long)K, (long long)N);
+    return MCQ4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mcq4_version(void) { return 1 * 10000 + 0 * 100 + 0; }
+
+const char *mcq4_status_string(int status) {
+    switch (status) {
+        case MCQ4_OK: return "ok";
+        case MCQ4_ERR_INVALID_ARG: return "invalid argument";
+        case MCQ4_ERR_SHAPE: return "unsupported shape";
+        case MCQ4_ERR_ALIGNMENT: return "misaligned pointer or leading dimension";
+        case MCQ4_ERR_WORKSPACE: return "workspace missing or too small";
+        case MCQ4_ERR_HIP: return "HIP runtime error";
+        default: return "unknown status";
+    }
+}
+
+const char *mcq4_last_error(void) { return g_err; }
+
+static int quantize_common(bool llama, const float *W, int64_t ldw, int64_t K, int64_t N,
+                           uint8_t *blocks, void *stream) {
+    g_err[0] = 0;
+    if (!W || !blocks) return fail(MCQ4_ERR_INVALID_ARG, "null pointer");
+    if (int st = check_kn(K, N)) return st;
+    if (ldw < N) return fail(MCQ4_ERR_SHAPE, "ldw (%lld) < N (%lld)", (long long)ldw, (long long)N);
+    if (!aligned(W, 4)) return fail(MCQ4_ERR_ALIGNMENT, "W must be 4-byte aligned");
+    if (!aligned(blocks, 2)) return fail(MCQ4_ERR_ALIGNMENT, "blocks must be 2-byte aligned");
+    return hip_status(mcq4::launch_quantize(llama, W, ldw, (int)(K / 32), (int)N, blocks,
+                                            (hipStream_t)stream),
+                      "quantize launch");
+}
+
+int mcq4_quantize_q4_0(const float *W, int64_t ldw, int64_t K, int64_t N, uint8_t *blocks,
+                       void *stream) {
+    return quantize_common(false, W, ldw, K, N, blocks, stream);
+}
+
+int mcq4_quantize_q4_0_llama(const float *W, int64_t ldw, int64_t K, int64_t N,
+                             uint8_t *blocks, void *stream) {
+    return quantize_common(true, W, ldw, K, N, blocks, stream);
+}
+
+int mcq4_dequantize_q4_0(const uint8_t *blocks, int64_t K, int64_t N, void *out, int64_t ldo,
+                         int out_dtype, void *stream) {
+    g_err[0] = 0;
+    if (!blocks || !out) return fail(MCQ4_ERR_INVALID_ARG, "null pointer");
+    if (out_dtype != MCQ4_DTYPE_F32 && out_dtype != MCQ4_DTYPE_F16)
+        return fail(MCQ4_ERR_INVALID_ARG, "out_dtype must be MCQ4_DTYPE_F32 or MCQ4_DTYPE_F16");
+    if (int st = check_kn(K, N)) return st;
+    if (ldo < N) return fail(MCQ4_ERR_SHAPE, "ldo (%lld) < N (%lld)", (long long)ldo, (long long)N);
+    if (!aligned(blocks, 2)) return fail(MCQ4_ERR_ALIGNMENT, "blocks must be 2-byte aligned");
+    if (!aligned(out, out_dtype == MCQ4_DTYPE_F32 ? 4 : 2))
+        return fail(MCQ4_ERR_ALIGNMENT, "out is misaligned for its dtype");
+    return hip_status(mcq4::launch_dequant(blocks, (int)(K / 32), (int)N, out, ldo,
+                                           out_dtype == MCQ4_DTYPE_F16, (hipStream_t)stream),
+                      "dequantize launch");
+}
+
+size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    if (M <= 0 || K <= 0 || N <= 0 || K % 32) return 0;
+    if (M <= 64) return mcq4::skinny_workspace_bytes(M, K, N);
+    return mcq4::gemm_workspace_bytes(M, K, N);
+}
+
+int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, int64_t ldy,
+                         int64_t M, int64_t K, int64_t N, void *workspace,
+                         size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    if (!X || !W || !Y) return fail(MCQ4_ERR_INVALID_ARG, "null pointer");
+    if (M <= 0) return fail(MCQ4_ERR_SHAPE, "M (%lld) must be positive", (long long)M);
+    if (int st = check_kn(K, N)) return st;
+    if (M > kMaxDim) return fail(MCQ4_ERR_SHAPE, "M (%lld) too large", (long long)M);
+    if (ldx < K) return fail(MCQ4_ERR_SHAPE, "ldx (%lld) < K (%lld)", (long long)ldx, (long long)K);
+    if (ldy < N) return fail(MCQ4_ERR_SHAPE, "ldy (%lld) < N (%lld)", (long long)ldy, (long long)N);
+    if (!aligned(X, 16) || ldx % 8)
+        return fail(MCQ4_ERR_ALIGNMENT, "X must be 16-byte aligned with ldx %% 8 == 0");
+    if (!aligned(W, 2)) return fail(MCQ4_ERR_ALIGNMENT, "W must be 2-byte aligned");
+    if (!aligned(Y, 2)) return fail(MCQ4_ERR_ALIGNMENT, "Y must be 2-byte aligned");
+    const size_t need = mcq4_matmul_workspace_bytes(M, K, N);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail(MCQ4_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                    workspace ? workspace_bytes : (size_t)0);
+    if (need && !aligned(workspace, 16))
+        return fail(MCQ4_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
+    hipError_t e;
+    if (M <= 64)
+        e = mcq4::launch_skinny((const _Float16 *)X, ldx, W, (_Float16 *)Y, ldy, (int)M, (int)K,
+                                (int)N, workspace, (hipStream_t)stream);
+    else
+        e = mcq4::launch_gemm((const _Float16 *)X, ldx, W, (_Float16 *)Y, ldy, (int)M, (int)K,
+                              (int)N, workspace, (hipStream_t)stream);
+    return hip_status(e, "matmul launch");
+}
+
+}  // extern "C"

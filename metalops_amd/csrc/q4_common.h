@@ -1,0 +1,76 @@
+// Shared definitions for the gfx950 block_q4_0 kernels.
+//
+// Block format (metalcore quantization.py:296-304, native/quant_kernels.metal:1703-1710):
+// 18 bytes = fp16 scale d + 16 bytes of nibbles; byte i holds element 2i (low
+// nibble) and element 2i+1 (high nibble).  Tensor layout [K/32][N][18]: the
+// blocks of adjacent output columns are contiguous.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mcq4 {
+
+constexpr int QK = 32;       // weights per block
+constexpr int BLOCK_BYTES = 18;
+
+// Split-K workspace layout shared by both matmul kernels: a fixed area of
+// per-tile arrival counters at offset 0 (zero on first use, left zero by every
+// call), then the fp32 partials.  Fixing the counter area's place and size keeps
+// a call's partials from ever landing where a later call, of any shape, looks
+// for its counters.
+constexpr int64_t COUNTER_SLOTS = 65536;
+constexpr size_t COUNTER_BYTES = COUNTER_SLOTS * sizeof(uint32_t);
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
+
+template <typename To, typename From>
+__device__ __forceinline__ To bitcast(const From &f) {
+    static_assert(sizeof(To) == sizeof(From), "size mismatch");
+    return __builtin_bit_cast(To, f);
+}
+
+// Eight nibbles (elements e0..e7 at bits 4e..4e+3 of `w`, i.e. byte i holds
+// e_{2i} low and e_{2i+1} high) and the fp16 bits of d -> eight fp16 weights
+// (q-8)*d in the slot order [e0,e2,e4,e6,e1,e3,e5,e7].
+//
+// lo/hi isolate the even/odd nibbles one per byte; v_perm_b32 against a word
+// of 0x64 bytes then builds fp16 halves 0x64qq = 1024 + q directly (one op per
+// pair).  Subtracting 1032 gives q - 8 exactly, and one fp16 multiply by d
+// gives the single nearest-even rounding of the exact product -- the value the
+// reference's fp16 dequant produces (quantization.py:417-419: exact fp32
+// product cast to fp16).
+__device__ __forceinline__ half8_t dequant8_perm(uint32_t w, uint32_t dbits) {
+#pragma clang fp contract(off)
+    const uint32_t C64 = 0x64646464u;
+    const uint32_t lo = w & 0x0F0F0F0Fu;          // bytes e0 e2 e4 e6
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;   // bytes e1 e3 e5 e7
+    const half2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
+    const half2_t d2 = bitcast<half2_t>(__builtin_amdgcn_perm(dbits, dbits, 0x01000100u));
+    half2_t p0 = (bitcast<half2_t>(__builtin_amdgcn_perm(C64, lo, 0x04010400u)) - off) * d2;
+    half2_t p1 = (bitcast<half2_t>(__builtin_amdgcn_perm(C64, lo, 0x04030402u)) - off) * d2;
+    half2_t p2 = (bitcast<half2_t>(__builtin_amdgcn_perm(C64, hi, 0x04010400u)) - off) * d2;
+    half2_t p3 = (bitcast<half2_t>(__builtin_amdgcn_perm(C64, hi, 0x04030402u)) - off) * d2;
+    half8_t r;
+    r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
+    r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
+    return r;
+}
+
+// Eight consecutive fp16 activations x0..x7 (as four dwords) reordered to the
+// dequant8_perm slot order [x0,x2,x4,x6,x1,x3,x5,x7].
+__device__ __forceinline__ half8_t perm_act8(uint4_t v) {
+    uint4_t r;
+    r[0] = __builtin_amdgcn_perm(v[1], v[0], 0x05040100u);  // x0, x2
+    r[1] = __builtin_amdgcn_perm(v[3], v[2], 0x05040100u);  // x4, x6
+    r[2] = __builtin_amdgcn_perm(v[1], v[0], 0x07060302u);  // x1, x3
+    r[3] = __builtin_amdgcn_perm(v[3], v[2], 0x07060302u);  // x5, x7
+    return bitcast<half8_t>(r);
+}
+
+}  // namespace mcq4

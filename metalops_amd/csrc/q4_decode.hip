@@ -1,0 +1,329 @@
+// Decode-shaped q4_0 matmul (M <= 64), LDS-staged strip variant (the default
+// decode path when N % 8 == 0 and W is 16-byte aligned).
+//
+// Why: in the [K/32][N][18] layout a 16-column tile is a strip of 288-byte row
+// segments 18*N bytes apart.  Fetching it with per-lane 2/4-byte loads (one
+// wave instruction = 144 useful bytes) starves the memory pipeline; the same
+// bytes fetched as 16-byte coalesced loads (1 KiB per wave instruction) stream
+// at close to the plain-copy rate.
+//
+// Structure.  A workgroup has WAVES waves in TPW = WAVES/KS tile slots of KS
+// waves each.  A slot's KS waves split the K-block rows of one column tile of
+// 16*NT columns; the workgroup walks tile groups (blockIdx.x, +gridDim.x, ...)
+// so that a small grid stays resident and streams continuously.
+//   * Rows are streamed in batches of B.  A batch's strip bytes (B rows of
+//     288*NT contiguous bytes) and its activations (M rows x B*64 bytes) are
+//     fetched with 16-byte coalesced loads into registers.  The next batch --
+//     possibly of the next tile -- is issued before the current one is
+//     computed, so memory latency overlaps the math and the tile epilogue.
+//   * Each wave bounces its batch through a private LDS slice (no workgroup
+//     barrier: a wave's LDS accesses are ordered) to regroup bytes into the
+//     MFMA layout: lane (column c = l%16, k-group g = l/16) reads the fp16 scale
+//     and qs bytes 4g..4g+3 of its block, dequant8_perm turns them into fp16
+//     (q-8)*d, and one v_mfma_f32_16x16x32_f16 per 16-row M tile accumulates in
+//     fp32.  The kernel covers whole column tiles only; the launcher sends the
+//     remaining N % (16*NT) columns to the generic decode kernel.
+//   * KS > 1: the slot's partial tiles are summed through LDS in a fixed order
+//     (one barrier pair per 16x16 fragment); KS == 1: each wave stores its own
+//     tile.  Results are written as fp16.
+#include <algorithm>
+#include <atomic>
+
+#include "q4_common.h"
+
+namespace mcq4 {
+
+struct DecodeArgs {
+    const _Float16 *X;
+    int64_t ldx;
+    const uint8_t *W;
+    _Float16 *Y;
+    int64_t ldy;
+    int M, nb, N;
+    int ntiles;
+};
+
+template <int MR, int NT>
+struct DecodeShape {
+    static constexpr int MT = (MR + 15) / 16;           // 16-row M tiles
+    static constexpr int B = (MR <= 4) ? 8 : 4;         // rows (K blocks) per batch
+    static constexpr int ROW_BYTES = 288 * NT;          // strip bytes per row
+    static constexpr int CPR = 18 * NT;                 // 16-byte strip chunks per row
+    static constexpr int CH = B * CPR;                  // strip chunks per batch
+    static constexpr int LPL = (CH + 63) / 64;          // strip loads per lane per batch
+    static constexpr int XROW = B * 64 + 16;            // LDS bytes per activation row (+pad)
+    static constexpr int XCPR = B * 4;                  // 16-byte activation chunks per row
+    static constexpr int XL = (MR * XCPR + 63) / 64;    // activation loads per lane
+    static constexpr int W_LDS = B * ROW_BYTES;
+    // Per-wave LDS slice for `mrows` activation rows (the launch sizes it for M).
+    static constexpr int wave_lds(int mrows) { return W_LDS + mrows * XROW; }
+};
+
+// MR: compile-time bound on the activation rows M (1, 4, 16, 32, 48 or 64).
+template <int MR, int NT, int WAVES, int KS>
+__global__ void __launch_bounds__(WAVES * 64)
+q4_decode_lds_kernel(DecodeArgs a) {
+    using S = DecodeShape<MR, NT>;
+    constexpr int MT = S::MT;
+    constexpr int B = S::B, CPR = S::CPR, LPL = S::LPL, ROW_BYTES = S::ROW_BYTES;
+    constexpr int XROW = S::XROW, XCPR = S::XCPR, XL = S::XL;
+    constexpr int NFRAG = MT * NT;
+    constexpr int TPW = WAVES / KS;
+    static_assert(WAVES % KS == 0, "KS must divide WAVES");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int slot = wave / KS, kp = wave % KS;
+    const int c = lane & 15;
+    const int g = lane >> 4;
+    const int mrows = min(a.M, MR);
+    const uint32_t grow = (uint32_t)a.N * BLOCK_BYTES;
+    uint8_t *wlds = smem + wave * S::wave_lds(mrows);
+    uint8_t *xlds = wlds + S::W_LDS;
+    float *red = (float *)(smem + WAVES * S::wave_lds(mrows));  // [WAVES][256] when KS > 1
+
+    // Per-lane chunk geometry of one batch: global byte offsets relative to the
+    // batch's first row, LDS offsets, and the batch row each chunk belongs to.
+    uint32_t soff[LPL], slds[LPL];
+    int srow[LPL];
+#pragma unroll
+    for (int i = 0; i < LPL; ++i) {
+        const int q = lane + 64 * i;
+        const int r = q / CPR, k = q - r * CPR;
+        srow[i] = q < S::CH ? r : B;            // B = never valid
+        soff[i] = (uint32_t)r * grow + 16u * k;
+        slds[i] = (uint32_t)(r * ROW_BYTES + 16 * k);
+    }
+    uint32_t xoff[XL], xlo[XL];
+    int xrw[XL];
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+        const int q = lane + 64 * i;
+        const int m = q / XCPR, k = q - m * XCPR;
+        xrw[i] = m < mrows ? (k >> 2) : B;      // batch row of this chunk (B = none)
+        xoff[i] = (uint32_t)(m * a.ldx * 2 + 16 * k);
+        xlo[i] = (uint32_t)(m * XROW + 16 * k);
+    }
+    bool xvalid[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xvalid[mt] = mt * 16 + c < mrows;
+
+    // This wave's K rows (identical for every tile) and its batch count.
+    const int rpp = (a.nb + KS - 1) / KS;
+    const int rbeg = min(a.nb, kp * rpp);
+    const int rend = min(a.nb, rbeg + rpp);
+    const int nbatch = (rend - rbeg + B - 1) / B;
+    // Tile groups walked by this workgroup (uniform across its waves).
+    const int ngroups_total = (a.ntiles + TPW - 1) / TPW;
+    const int ngroups = (ngroups_total - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const uint8_t *xbase = (const uint8_t *)a.X;
+
+    uint4_t wv[LPL], xr[XL];
+    auto issue = [&](int tile, int row0) {
+        const int rows = min(B, rend - row0);
+        const uint8_t *gb = a.W + (int64_t)tile * (16 * NT * BLOCK_BYTES) + (int64_t)row0 * grow;
+#pragma unroll
+        for (int i = 0; i < LPL; ++i)
+            if (srow[i] < rows) wv[i] = __builtin_nontemporal_load((const uint4_t *)(gb + soff[i]));
+        const uint8_t *xb = xbase + (int64_t)row0 * (QK * 2);
+#pragma unroll
+        for (int i = 0; i < XL; ++i)
+            if (xrw[i] < rows) xr[i] = *(const uint4_t *)(xb + xoff[i]);
+    };
+    auto tile_of = [&](int j) { return ((int)blockIdx.x + j * (int)gridDim.x) * TPW + slot; };
+
+    float4_t acc[MT][NT];
+    if (nbatch > 0 && ngroups > 0 && tile_of(0) < a.ntiles) issue(tile_of(0), rbeg);
+    for (int j = 0; j < ngroups; ++j) {
+        const int tile = tile_of(j);
+        const bool tile_ok = tile < a.ntiles;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[mt][t] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+        for (int b = 0; b < nbatch; ++b) {
+            const int row0 = rbeg + b * B;
+            const int rows = min(B, rend - row0);
+            if (tile_ok) {
+                // Stage into this wave's LDS slice (a wave's LDS accesses are ordered).
+#pragma unroll
+                for (int i = 0; i < LPL; ++i)
+                    if (srow[i] < rows) *(uint4_t *)(wlds + slds[i]) = wv[i];
+#pragma unroll
+                for (int i = 0; i < XL; ++i)
+                    if (xrw[i] < rows) *(uint4_t *)(xlds + xlo[i]) = xr[i];
+            }
+            // Prefetch the next batch (of this tile or of the next group's tile).
+            if (b + 1 < nbatch) {
+                if (tile_ok) issue(tile, row0 + B);
+            } else if (j + 1 < ngroups && tile_of(j + 1) < a.ntiles) {
+                issue(tile_of(j + 1), rbeg);
+            }
+            if (!tile_ok) continue;
+            for (int u = 0; u < rows; ++u) {
+                half8_t av[MT];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    av[mt] = xvalid[mt] ? perm_act8(*(const uint4_t *)(xlds + (mt * 16 + c) * XROW +
+                                                                      u * 64 + 16 * g))
+                                        : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const uint16_t *bp =
+                        (const uint16_t *)(wlds + u * ROW_BYTES + t * 288 + c * BLOCK_BYTES);
+                    const uint32_t w = (uint32_t)bp[1 + 2 * g] | ((uint32_t)bp[2 + 2 * g] << 16);
+                    const half8_t bv = dequant8_perm(w, bp[0]);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mt], bv, acc[mt][t],
+                                                                            0, 0, 0);
+                }
+            }
+        }
+
+        // ---- tile epilogue ---------------------------------------------------
+        const int n0 = tile * 16 * NT;
+        if constexpr (KS == 1) {
+            if (tile_ok) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int t = 0; t < NT; ++t)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int m = mt * 16 + 4 * g + i;
+                            if (m < a.M)
+                                a.Y[(int64_t)m * a.ldy + n0 + t * 16 + c] = (_Float16)acc[mt][t][i];
+                        }
+            }
+        } else {
+#pragma unroll
+            for (int f = 0; f < NFRAG; ++f) {
+                const int mt = f / NT, t = f % NT;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[wave * 256 + lane * 4 + i] = acc[mt][t][i];
+                __syncthreads();
+                // The slot's KS*64 threads finish its 256 values, summing waves in order.
+                for (int vi = tid - slot * KS * 64; vi < 256; vi += KS * 64) {
+                    float s = 0.f;
+#pragma unroll
+                    for (int w = 0; w < KS; ++w) s += red[(slot * KS + w) * 256 + vi];
+                    const int l = vi >> 2, i = vi & 3;
+                    const int m = mt * 16 + 4 * (l >> 4) + i;
+                    if (tile_ok && m < a.M)
+                        a.Y[(int64_t)m * a.ldy + n0 + t * 16 + (l & 15)] = (_Float16)s;
+                }
+                __syncthreads();
+            }
+        }
+    }
+}
+
+// ---- launch -----------------------------------------------------------------
+
+struct DecodeCfg {
+    int NT, WAVES, KS, grid_cap;
+};
+
+// Small N (few column tiles): all waves of a 16-wave workgroup split K of one
+// tile.  Large N: 4-wave workgroups whose waves each own a whole tile (no
+// reduction); the grid is capped so workgroups stay resident and pipeline
+// across the tiles they walk.
+static DecodeCfg decode_config(int64_t M, int64_t K, int64_t N) {
+    (void)K;
+    DecodeCfg c{1, 16, 16, 256};                  // one resident 16-wave workgroup per CU
+    if (M > 4 && N >= 8192) c = DecodeCfg{2, 16, 16, 0};
+    if (M <= 16 && N / 16 >= 4096) c = DecodeCfg{2, 4, 1, 1024};  // lm_head-sized N
+    if (const char *env = getenv("MCQ4_DECODE_CFG")) {  // "NT,WAVES,KS,GRIDCAP" (tuning aid)
+        int nt, w, ks, cap;
+        if (sscanf(env, "%d,%d,%d,%d", &nt, &w, &ks, &cap) == 4 && (nt == 1 || nt == 2) &&
+            (w == 4 || w == 8 || w == 16) && (ks == 1 || ks == 4 || ks == w) && cap >= 0)
+            c = DecodeCfg{nt, w, ks, cap};
+    }
+    return c;
+}
+
+template <int MR, int NT, int WAVES, int KS>
+static hipError_t launch_dec_t(const DecodeArgs &a, int grid_cap, hipStream_t s) {
+    using S = DecodeShape<MR, NT>;
+    const int mrows = std::min(a.M, MR);
+    size_t lds = (size_t)WAVES * S::wave_lds(mrows);
+    if (KS > 1) lds += (size_t)WAVES * 256 * sizeof(float);
+    if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
+    // Raise the dynamic-LDS limit once per device (bit d of `done`).
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(done.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void *)q4_decode_lds_kernel<MR, NT, WAVES, KS>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        done.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    constexpr int TPW = WAVES / KS;
+    int grid = (a.ntiles + TPW - 1) / TPW;
+    if (grid_cap > 0) grid = std::min(grid, grid_cap);
+    hipLaunchKernelGGL((q4_decode_lds_kernel<MR, NT, WAVES, KS>), dim3(grid), dim3(WAVES * 64),
+                       lds, s, a);
+    return hipGetLastError();
+}
+
+template <int MR, int NT>
+static hipError_t launch_dec_nt(const DecodeArgs &a, const DecodeCfg &c, hipStream_t s) {
+    if (c.KS == 1) {
+        if (c.WAVES == 4) return launch_dec_t<MR, NT, 4, 1>(a, c.grid_cap, s);
+        return launch_dec_t<MR, NT, 8, 1>(a, c.grid_cap, s);
+    }
+    if (c.KS == 4) return launch_dec_t<MR, NT, 8, 4>(a, c.grid_cap, s);
+    // K split by all waves; fall back to fewer waves when the LDS slices do not fit.
+    if (c.WAVES == 16 && MR <= 32) {
+        hipError_t e = launch_dec_t<MR, NT, 16, 16>(a, c.grid_cap, s);
+        if (e != hipErrorInvalidConfiguration) return e;
+    }
+    if (c.WAVES >= 8) {
+        hipError_t e = launch_dec_t<MR, NT, 8, 8>(a, c.grid_cap, s);
+        if (e != hipErrorInvalidConfiguration) return e;
+    }
+    return launch_dec_t<MR, NT, 4, 4>(a, c.grid_cap, s);
+}
+
+template <int MR>
+static hipError_t launch_dec_mr(const DecodeArgs &a, const DecodeCfg &c, hipStream_t s) {
+    if (c.NT == 1) return launch_dec_nt<MR, 1>(a, c, s);
+    return launch_dec_nt<MR, 2>(a, c, s);
+}
+
+// True when the LDS-staged decode kernel applies: 16-byte loads of strip rows
+// need 18*N to be a multiple of 16 (N % 8 == 0; 18*8 = 144 = 9*16), a 16-byte
+// aligned weight base, activation rows 16-byte aligned, and the strip row
+// offsets of one batch within 32 bits.
+bool decode_lds_supported(const uint8_t *W, int64_t N, int64_t ldx) {
+    return N % 8 == 0 && ((uintptr_t)W % 16) == 0 && N * 18 * 8 < ((int64_t)1 << 31) &&
+           ldx * 2 * 64 < ((int64_t)1 << 31);
+}
+
+// Launches the LDS-staged kernel over the whole column tiles of 16*NT columns;
+// returns through *n_done how many leading columns it covers (a multiple of 16*NT).
+hipError_t launch_decode_lds(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                             int64_t ldy, int M, int K, int N, int *n_done, hipStream_t s) {
+    const DecodeCfg c = decode_config(M, K, N);
+    DecodeArgs a;
+    a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
+    a.M = M; a.nb = K / QK; a.N = N;
+    a.ntiles = N / (16 * c.NT);
+    *n_done = a.ntiles * 16 * c.NT;
+    if (a.ntiles == 0) return hipSuccess;
+    if (M == 1) return launch_dec_mr<1>(a, c, s);
+    if (M <= 4) return launch_dec_mr<4>(a, c, s);
+    if (M <= 16) return launch_dec_mr<16>(a, c, s);
+    if (M <= 32) return launch_dec_mr<32>(a, c, s);
+    if (M <= 48) return launch_dec_mr<48>(a, c, s);
+    return launch_dec_mr<64>(a, c, s);
+}
+
+}  // namespace mcq4

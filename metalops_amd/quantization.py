@@ -1,0 +1,192 @@
+"""GGML block_q4_0 quantize / dequantize / matmul on MI355X.
+
+Mirrors metalcore's q4_0 API (``packages/metalcore/src/metalcore/quantization.py``):
+
+* ``quantize_ggml_q4_0(weight)``            -- quantization.py:307-371
+* ``dequantize_ggml_q4_0(blocks, dtype)``   -- quantization.py:374-419
+* ``matmul_ggml_q4_0(X, W_blocks)``         -- quantization.py:422-454
+
+Same names, argument order, defaults (dequant defaults to float16), block tensor
+``[K/32, N, 18]`` uint8 and ``AssertionError`` messages for the K checks
+(quantization.py:329, :443).  Every computation runs in the HIP kernels of
+``libmcq4.so``; tensors must live on a ROCm device (``device.type == "cuda"``) --
+there is deliberately no CPU fallback.  Work is enqueued on the current stream
+and returns without synchronising, like the reference's Metal binding
+(core_mps.mm:5947-5971).
+"""
+from __future__ import annotations
+
+import threading
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+QK4_0 = 32                         # quantization.py:303
+BLOCK_Q4_0_SIZE = 2 + QK4_0 // 2   # quantization.py:304 (18 bytes)
+
+__all__ = [
+    "QK4_0",
+    "BLOCK_Q4_0_SIZE",
+    "quantize_ggml_q4_0",
+    "quantize_ggml_q4_0_llama",
+    "dequantize_ggml_q4_0",
+    "matmul_ggml_q4_0",
+]
+
+
+def _require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "metalops_amd q4_0 ops run only on a ROCm GPU (torch device 'cuda'); "
+                f"got a tensor on '{t.device}'. There is no CPU fallback.")
+    dev = tensors[0].device
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"all tensors must be on one device, got {dev} and {t.device}")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _quantize(weight: torch.Tensor, llama_rule: bool) -> torch.Tensor:
+    K, N = weight.shape
+    assert K % QK4_0 == 0, f"K ({K}) must be divisible by {QK4_0}"   # quantization.py:329
+    _require_device(weight)
+    w = weight if weight.dtype == torch.float32 else weight.float()
+    if w.stride(1) != 1 or w.stride(0) < N or w.data_ptr() % 4:
+        w = w.contiguous()
+    blocks = torch.empty((K // QK4_0, N, BLOCK_Q4_0_SIZE), dtype=torch.uint8, device=w.device)
+    if K == 0 or N == 0:
+        return blocks
+    fn = _lib.lib.mcq4_quantize_q4_0_llama if llama_rule else _lib.lib.mcq4_quantize_q4_0
+    with torch.cuda.device(w.device):
+        _lib.check(fn(w.data_ptr(), w.stride(0), K, N, blocks.data_ptr(), _stream(w.device)),
+                   fn.__name__)
+    return blocks
+
+
+def quantize_ggml_q4_0(weight: torch.Tensor) -> torch.Tensor:
+    """Quantize ``weight[K, N]`` to ``[K/32, N, 18]`` uint8 blocks (reference rule).
+
+    Per block of 32 rows of a column: ``d = amax/7`` (1 when amax is 0),
+    ``q = round_half_even(x/d + 8)`` clamped to [0, 15]; bytes 0..1 hold fp16(d),
+    byte ``2+i`` holds ``q[2i] | q[2i+1] << 4`` (quantization.py:333-369).
+    fp32 weights reproduce the reference bit for bit; other float dtypes are
+    quantized from their exact fp32 upcast (the reference rounds each step in
+    the weight's own dtype instead).
+    """
+    return _quantize(weight, llama_rule=False)
+
+
+def quantize_ggml_q4_0_llama(weight: torch.Tensor) -> torch.Tensor:
+    """llama.cpp ``quantize_row_q4_0_ref`` rule in metalcore's layout (benchmark generator).
+
+    ``d = max_signed/-8``, ``q = min(15, trunc(x/d + 8.5))``; produces negative
+    scales and ``q = 0``, which the reference rule never does.  Not part of the
+    reference API.
+    """
+    return _quantize(weight, llama_rule=True)
+
+
+def dequantize_ggml_q4_0(blocks: torch.Tensor, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``[K/32, N, 18]`` blocks -> ``W[K, N] = (q - 8) * d`` in ``dtype`` (default float16).
+
+    The product is exact in fp32; other dtypes receive one rounding of it, as
+    the reference's ``.to(dtype)`` does (quantization.py:414-419).
+    """
+    if dtype is None:
+        dtype = torch.float16
+    num_blocks, N, bs = blocks.shape
+    assert bs == BLOCK_Q4_0_SIZE, f"blocks last dim must be {BLOCK_Q4_0_SIZE}"
+    K = num_blocks * QK4_0
+    _require_device(blocks)
+    if blocks.dtype != torch.uint8:
+        raise RuntimeError("blocks must be uint8")
+    b = blocks if (blocks.is_contiguous() and blocks.data_ptr() % 2 == 0) else blocks.contiguous()
+    if b.data_ptr() % 2:
+        b = b.clone()
+    kernel_dtype = torch.float16 if dtype == torch.float16 else torch.float32
+    out = torch.empty((K, N), dtype=kernel_dtype, device=b.device)
+    if K and N:
+        code = _lib.MCQ4_DTYPE_F16 if kernel_dtype == torch.float16 else _lib.MCQ4_DTYPE_F32
+        with torch.cuda.device(b.device):
+            _lib.check(_lib.lib.mcq4_dequantize_q4_0(b.data_ptr(), K, N, out.data_ptr(), N, code,
+                                                     _stream(b.device)),
+                       "mcq4_dequantize_q4_0")
+    return out if out.dtype == dtype else out.to(dtype)
+
+
+class _Workspace:
+    """Per-device, zero-initialised split-K workspace reused across calls.
+
+    The kernels leave the arrival counters at zero after every call, so the
+    buffer is zero-filled once when (re)allocated and never cleared again.
+    One buffer per (device, stream), so concurrent streams never share one; a
+    larger request allocates a new buffer through PyTorch's stream-ordered
+    caching allocator.
+    """
+
+    def __init__(self):
+        self._bufs: dict = {}
+        self._lock = threading.Lock()
+
+    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+        key = (device, stream)   # one buffer per stream: calls on one stream never overlap
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                size = max(nbytes, 1 << 20)
+                buf = torch.zeros(size, dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+            return buf
+
+
+_workspace = _Workspace()
+
+
+def matmul_ggml_q4_0(X: torch.Tensor, W_blocks: torch.Tensor) -> torch.Tensor:
+    """``Y[M, N] = X[M, K] @ dequant(W_blocks)`` with fp16 inputs and fp32 accumulation.
+
+    ``X`` is used as fp16 (as the reference's GPU binding does, quantization.py:448);
+    the result is returned in ``X.dtype`` (quantization.py:452-454).  M <= 64 runs
+    the decode kernel, larger M the prefill MFMA GEMM.
+    """
+    num_blocks_per_col, N, _ = W_blocks.shape
+    K = num_blocks_per_col * QK4_0
+    assert X.shape[1] == K, f"X K dim ({X.shape[1]}) must match weight K ({K})"  # :443
+    _require_device(X, W_blocks)
+    if X.dim() != 2:
+        raise RuntimeError(f"X must be 2-D [M, K], got shape {tuple(X.shape)}")
+    if W_blocks.dtype != torch.uint8 or W_blocks.shape[2] != BLOCK_Q4_0_SIZE:
+        raise RuntimeError("W_blocks must be uint8 [K/32, N, 18]")
+    M = X.shape[0]
+    out_dtype = X.dtype
+    x = X if X.dtype == torch.float16 else X.half()
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.stride(0) < K or x.data_ptr() % 16:
+        x = x.contiguous()
+        if x.data_ptr() % 16:
+            x = x.clone()
+    w = W_blocks if W_blocks.is_contiguous() else W_blocks.contiguous()
+    if w.data_ptr() % 2:
+        w = w.clone()
+    Y = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    if M == 0 or N == 0:
+        return Y.to(out_dtype)
+    if K == 0:
+        return Y.zero_().to(out_dtype)
+    need = int(_lib.lib.mcq4_matmul_workspace_bytes(M, K, N))
+    stream = _stream(x.device)
+    ws_ptr, ws_bytes = None, 0
+    if need:
+        ws = _workspace.get(x.device, stream, need)
+        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.lib.mcq4_matmul_q4_0_f16(x.data_ptr(), x.stride(0), w.data_ptr(),
+                                                 Y.data_ptr(), N, M, K, N, ws_ptr, ws_bytes,
+                                                 stream),
+                   "mcq4_matmul_q4_0_f16")
+    return Y if out_dtype == torch.float16 else Y.to(out_dtype)

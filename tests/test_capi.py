@@ -1,0 +1,90 @@
+"""CPU tests of the C ABI surface (include/mcq4.h <-> metalops_amd/_lib/libmcq4.so).
+
+No kernel is launched: every call here fails validation before touching the GPU.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+from metalops_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mcq4.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(mcq4_[a-z0-9_]+)\s*\(", src)))
+
+
+def test_header_declares_what_binding_knows():
+    assert _declared() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_status_strings():
+    L = _lib.lib
+    assert L.mcq4_version() >= 10000
+    assert _lib.status_string(_lib.MCQ4_OK) == "ok"
+    assert "workspace" in _lib.status_string(_lib.MCQ4_ERR_WORKSPACE)
+    assert _lib.status_string(99) == "unknown status"
+
+
+def _err():
+    return _lib.lib.mcq4_last_error().decode()
+
+
+def test_matmul_validation_codes():
+    L = _lib.lib
+    X, W, Y = 0x10000, 0x20000, 0x30000   # never dereferenced: validation fails first
+    assert L.mcq4_matmul_q4_0_f16(None, 32, W, Y, 8, 1, 32, 8, None, 0, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert "null" in _err()
+    assert L.mcq4_matmul_q4_0_f16(X, 48, W, Y, 8, 1, 48, 8, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert "divisible by 32" in _err()
+    assert L.mcq4_matmul_q4_0_f16(X, 32, W, Y, 8, 0, 32, 8, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert L.mcq4_matmul_q4_0_f16(X, 16, W, Y, 8, 1, 32, 8, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert L.mcq4_matmul_q4_0_f16(X, 32, W, Y, 4, 1, 32, 8, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert L.mcq4_matmul_q4_0_f16(X + 8, 32, W, Y, 8, 1, 32, 8, None, 0, None) == _lib.MCQ4_ERR_ALIGNMENT
+    assert L.mcq4_matmul_q4_0_f16(X, 36, W, Y, 8, 1, 32, 8, None, 0, None) == _lib.MCQ4_ERR_ALIGNMENT
+    assert L.mcq4_matmul_q4_0_f16(X, 32, W + 1, Y, 8, 1, 32, 8, None, 0, None) == _lib.MCQ4_ERR_ALIGNMENT
+    assert L.mcq4_matmul_q4_0_f16(X, 32, W, Y + 1, 8, 1, 32, 8, None, 0, None) == _lib.MCQ4_ERR_ALIGNMENT
+
+
+def test_workspace_query_and_check():
+    L = _lib.lib
+    assert L.mcq4_matmul_workspace_bytes(1, 4096, 4096) == 0   # decode: no split-K
+    need = L.mcq4_matmul_workspace_bytes(128, 8192, 128)       # one GEMM tile: split-K
+    assert need >= 256 * 1024                                  # counter area + partials
+    assert L.mcq4_matmul_workspace_bytes(1, 48, 8) == 0        # invalid K
+    assert L.mcq4_matmul_workspace_bytes(0, 4096, 8) == 0
+    rc = L.mcq4_matmul_q4_0_f16(0x10000, 8192, 0x20000, 0x30000, 128, 128, 8192, 128, None, 0, None)
+    assert rc == _lib.MCQ4_ERR_WORKSPACE and "required" in _err()
+    rc = L.mcq4_matmul_q4_0_f16(0x10000, 8192, 0x20000, 0x30000, 128, 128, 8192, 128,
+                                0x40000, need - 1, None)
+    assert rc == _lib.MCQ4_ERR_WORKSPACE
+
+
+def test_quantize_dequant_validation_codes():
+    L = _lib.lib
+    assert L.mcq4_quantize_q4_0(None, 8, 32, 8, 0x20000, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert L.mcq4_quantize_q4_0(0x10000, 8, 33, 8, 0x20000, None) == _lib.MCQ4_ERR_SHAPE
+    assert L.mcq4_quantize_q4_0(0x10000, 4, 32, 8, 0x20000, None) == _lib.MCQ4_ERR_SHAPE
+    assert L.mcq4_quantize_q4_0_llama(0x10002, 8, 32, 8, 0x20000, None) == _lib.MCQ4_ERR_ALIGNMENT
+    assert L.mcq4_quantize_q4_0(0x10000, 8, 32, 8, 0x20001, None) == _lib.MCQ4_ERR_ALIGNMENT
+    assert L.mcq4_dequantize_q4_0(0x20000, 32, 8, 0x30000, 8, 7, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert L.mcq4_dequantize_q4_0(0x20000, 32, 8, 0x30002, 8, _lib.MCQ4_DTYPE_F32, None) == _lib.MCQ4_ERR_ALIGNMENT
+    assert L.mcq4_dequantize_q4_0(0x20000, 32, 8, 0x30000, 4, _lib.MCQ4_DTYPE_F16, None) == _lib.MCQ4_ERR_SHAPE
+    assert L.mcq4_dequantize_q4_0(0x20000, 32 * 70000, 8, 0x30000, 8, 0, None) == _lib.MCQ4_ERR_SHAPE
+
+
+def test_error_raises_runtime_error_subclass():
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        _lib.check(_lib.lib.mcq4_quantize_q4_0(None, 8, 32, 8, None, None), "mcq4_quantize_q4_0")

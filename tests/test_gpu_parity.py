@@ -1,0 +1,174 @@
+"""GPU parity: the HIP kernels of libmcq4.so against the CPU oracle.
+
+Bars (from the reference semantics, quantization.py:307-454):
+  * quantize (both rules): bit-exact bytes.
+  * dequantize: bit-exact fp32 and fp16.
+  * matmul: max|err| <= 1e-2 * ||Y_ref[m, :]||_inf per row, Y_ref = X.float() @ dequant_f32(W)
+    (TOL below); in practice the kernels sit orders of magnitude inside it.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import q4_0_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _mo():
+    import metalops_amd as mo
+    return mo
+
+
+def _weights(K, N, seed, outliers=False):
+    g = torch.Generator().manual_seed(seed)
+    W = torch.randn(K, N, generator=g) * 0.02
+    if outliers:
+        n = max(1, W.numel() // 100)
+        idx = torch.randperm(W.numel(), generator=g)[:n]
+        W.view(-1)[idx] = torch.randn(n, generator=g) * 0.2
+    return W
+
+
+def _acts(M, K, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(M, K, generator=g).half()
+
+
+def _check_rows(Y, Yref, tol=TOL):
+    Y = np.asarray(Y, dtype=np.float64)
+    Yref = np.asarray(Yref, dtype=np.float64)
+    err = np.abs(Y - Yref).max(axis=1)
+    bound = tol * np.abs(Yref).max(axis=1)
+    bad = np.nonzero(err > bound)[0]
+    assert bad.size == 0, f"rows {bad[:8]} exceed tolerance: err={err[bad[:4]]} bound={bound[bad[:4]]}"
+    return float((err / np.maximum(bound, 1e-30)).max())
+
+
+@pytest.mark.parametrize("K,N", [(32, 1), (32, 7), (64, 33), (352, 257), (4096, 96)])
+@pytest.mark.parametrize("rule", ["ref", "llama"])
+def test_quantize_bit_exact(dev, K, N, rule):
+    mo = _mo()
+    W = _weights(K, N, seed=K * 7 + N, outliers=True)
+    W[:32, 0] = 0.0  # an all-zero block
+    if rule == "ref":
+        got = mo.quantize_ggml_q4_0(W.to(dev)).cpu().numpy()
+        want = ref.quantize_ref_rule(W.numpy())
+    else:
+        got = mo.quantize_ggml_q4_0_llama(W.to(dev)).cpu().numpy()
+        want = ref.quantize_llama_rule(W.numpy())
+    assert got.shape == (K // 32, N, 18)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_quantize_ties_and_specials(dev):
+    mo = _mo()
+    # Column 0: amax = 7 -> d = 1 exactly, so x + 8 lands on .5 ties: half-to-even.
+    col = np.zeros(32, np.float32)
+    col[:8] = [7.0, 0.5, 1.5, -0.5, -1.5, 2.5, -2.5, 6.5]
+    W = np.zeros((32, 4), np.float32)
+    W[:, 0] = col
+    W[5, 1] = -3.0          # single-hot negative
+    W[:, 2] = np.linspace(-1, 1, 32, dtype=np.float32)
+    got = mo.quantize_ggml_q4_0(torch.from_numpy(W).to(dev)).cpu().numpy()
+    np.testing.assert_array_equal(got, ref.quantize_ref_rule(W))
+    q, d = ref.unpack_nibbles(got)
+    assert list(q[0, 0, :8]) == [15, 8, 10, 8, 6, 10, 6, 14]
+    assert d[0, 3] == np.float16(1.0) and (q[0, 3] == 8).all()   # zero block: d = 1, q = 8
+
+
+@pytest.mark.parametrize("K,N", [(32, 1), (64, 33), (352, 257), (1024, 640)])
+def test_dequant_bit_exact(dev, K, N):
+    mo = _mo()
+    rng = np.random.default_rng(K + N)
+    blocks = rng.integers(0, 256, size=(K // 32, N, 18), dtype=np.uint8)
+    # keep scales finite: random fp16 in a sane exponent range, both signs, some subnormals
+    d = (rng.standard_normal((K // 32, N)) * 0.01).astype(np.float16)
+    d.reshape(-1)[:5] = np.array([0.0, -0.0, 6e-8, -6e-8, 65504.0], np.float16)[: min(5, d.size)]
+    blocks[:, :, 0:2] = d.view(np.uint8).reshape(K // 32, N, 2)
+    tb = torch.from_numpy(blocks).to(dev)
+    got32 = mo.dequantize_ggml_q4_0(tb, torch.float32).cpu().numpy()
+    np.testing.assert_array_equal(got32.view(np.uint32), ref.dequantize(blocks, np.float32).view(np.uint32))
+    got16 = mo.dequantize_ggml_q4_0(tb).cpu().numpy()
+    assert got16.dtype == np.float16
+    np.testing.assert_array_equal(got16.view(np.uint16), ref.dequantize(blocks, np.float16).view(np.uint16))
+
+
+SMALL_SHAPES = [
+    (1, 32, 1), (1, 64, 33), (1, 352, 257), (2, 256, 100), (5, 352, 33), (16, 1024, 48),
+    (17, 352, 40), (33, 512, 130), (64, 256, 64), (1, 4096, 96), (4, 14336, 64),
+    (65, 352, 70), (100, 512, 300), (128, 1024, 256), (257, 352, 130), (300, 2048, 520),
+]
+
+
+@pytest.mark.parametrize("M,K,N", SMALL_SHAPES)
+def test_matmul_small_vs_oracle(dev, M, K, N):
+    mo = _mo()
+    W = _weights(K, N, seed=M + K + N, outliers=True)
+    X = _acts(M, K, seed=M * 3 + 1)
+    blocks = ref.quantize_llama_rule(W.numpy())
+    Y = mo.matmul_ggml_q4_0(X.to(dev), torch.from_numpy(blocks).to(dev))
+    assert Y.dtype == torch.float16 and Y.shape == (M, N)
+    _check_rows(Y.float().cpu().numpy(), ref.matmul_f32(X.numpy(), blocks))
+
+
+def test_matmul_matches_f64_bruteforce(dev):
+    mo = _mo()
+    W = _weights(96, 9, seed=5)
+    X = _acts(3, 96, seed=6)
+    blocks = ref.quantize_ref_rule(W.numpy())
+    Y = mo.matmul_ggml_q4_0(X.to(dev), torch.from_numpy(blocks).to(dev)).float().cpu().numpy()
+    _check_rows(Y, ref.matmul_f64(X.numpy(), blocks), tol=2e-3)
+
+
+def test_matmul_deterministic_and_dtype(dev):
+    mo = _mo()
+    W = _weights(2048, 384, seed=1)
+    X = _acts(8, 2048, seed=2)
+    b = mo.quantize_ggml_q4_0(W.to(dev))
+    y1 = mo.matmul_ggml_q4_0(X.to(dev), b)
+    y2 = mo.matmul_ggml_q4_0(X.to(dev), b)
+    assert torch.equal(y1, y2)
+    y32 = mo.matmul_ggml_q4_0(X.float().to(dev), b)
+    assert y32.dtype == torch.float32
+    assert torch.equal(y32, y1.float())
+
+
+def _full_size_check(dev, M, K, N, outliers=False):
+    """Full-size config: GPU quantize (llama rule), kernel vs fp32 torch GEMM of the
+    bit-exact GPU dequant (dequant itself is pinned bit-exact against the oracle above)."""
+    mo = _mo()
+    g = torch.Generator(device=dev).manual_seed(M + K + N)
+    W = torch.randn(K, N, generator=g, device=dev) * 0.02
+    if outliers:
+        n = W.numel() // 100
+        idx = torch.randperm(W.numel(), generator=g, device=dev)[:n]
+        W.view(-1)[idx] = torch.randn(n, generator=g, device=dev) * 0.2
+    X = torch.randn(M, K, generator=g, device=dev).half()
+    b = mo.quantize_ggml_q4_0_llama(W)
+    del W
+    Y = mo.matmul_ggml_q4_0(X, b).float()
+    Yref = X.float() @ mo.dequantize_ggml_q4_0(b, torch.float32)
+    err = (Y - Yref).abs().amax(dim=1)
+    bound = TOL * Yref.abs().amax(dim=1)
+    assert bool((err <= bound).all()), f"max err/bound {(err / bound).max().item()}"
+
+
+@pytest.mark.parametrize("M,K,N", [
+    (1, 4096, 12288), (1, 4096, 4096), (1, 4096, 11008), (1, 11008, 4096),
+    (4, 4096, 14336), (8, 14336, 4096), (16, 4096, 14336), (16, 14336, 4096),
+])
+def test_matmul_decode_configs(dev, M, K, N):
+    _full_size_check(dev, M, K, N)
+
+
+@pytest.mark.parametrize("M,K,N", [(2048, 4096, 14336), (2048, 14336, 4096), (512, 11008, 4096)])
+def test_matmul_prefill_configs(dev, M, K, N):
+    _full_size_check(dev, M, K, N, outliers=True)
+
+
+def test_matmul_lm_head(dev):
+    _full_size_check(dev, 1, 4096, 128256)
+    _full_size_check(dev, 512, 4096, 128256)
