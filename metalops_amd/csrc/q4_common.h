@@ -29,6 +29,20 @@ typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t uint4_t __attribute__((ext_vector_type(4)));
 
+// Explicit LDS (address space 3) views: a 32-bit LDS address kept in a VGPR
+// and dereferenced through these types compiles to ds_read with immediate
+// offsets.
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef __attribute__((address_space(3))) uint16_t lds_u16;
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+typedef __attribute__((address_space(3))) half8_t lds_half8;
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const lds_u8 *)p;
+}
+__device__ __forceinline__ const lds_u8 *lds_ptr(uint32_t addr) {
+    return (const lds_u8 *)(uintptr_t)addr;
+}
+
 template <typename To, typename From>
 __device__ __forceinline__ To bitcast(const From &f) {
     static_assert(sizeof(To) == sizeof(From), "size mismatch");
@@ -60,6 +74,20 @@ __device__ __forceinline__ half8_t dequant8_perm(uint32_t w, uint32_t dbits) {
     r[0] = p0[0]; r[1] = p0[1]; r[2] = p1[0]; r[3] = p1[1];
     r[4] = p2[0]; r[5] = p2[1]; r[6] = p3[0]; r[7] = p3[1];
     return r;
+}
+
+// Eight nibbles -> fp16 halves 1024 + q (exact) in the dequant8_perm slot order.
+// Used where the -8 offset and the scale d are applied after the MFMA.
+__device__ __forceinline__ half8_t unpack8_1024(uint32_t w) {
+    const uint32_t C64 = 0x64646464u;
+    const uint32_t lo = w & 0x0F0F0F0Fu;
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+    uint4_t r;
+    r[0] = __builtin_amdgcn_perm(C64, lo, 0x04010400u);
+    r[1] = __builtin_amdgcn_perm(C64, lo, 0x04030402u);
+    r[2] = __builtin_amdgcn_perm(C64, hi, 0x04010400u);
+    r[3] = __builtin_amdgcn_perm(C64, hi, 0x04030402u);
+    return bitcast<half8_t>(r);
 }
 
 // Eight consecutive fp16 activations x0..x7 (as four dwords) reordered to the

@@ -54,12 +54,14 @@ struct DecodeShape {
     static constexpr int XROW = B * 64 + 16;            // LDS bytes per activation row (+pad)
     static constexpr int XCPR = B * 4;                  // 16-byte activation chunks per row
     static constexpr int XL = (MR * XCPR + 63) / 64;    // activation loads per lane
-    static constexpr int W_LDS = B * ROW_BYTES;
+    static constexpr int W_LDS = B * ROW_BYTES + 16;    // +16: the last row's qs read2 overhang
+    static constexpr int ZERO_LDS = B * 64;             // zero activations for rows m >= M
     // Per-wave LDS slice for `mrows` activation rows (the launch sizes it for M).
     static constexpr int wave_lds(int mrows) { return W_LDS + mrows * XROW; }
+    // Batch row r is complete once strip load (r*CPR + CPR - 1) / 64 has landed.
+    static constexpr int last_load_of_row(int r) { return (r * CPR + CPR - 1) / 64; }
 };
 
-// MR: compile-time bound on the activation rows M (1, 4, 16, 32, 48 or 64).
 template <int MR, int NT, int WAVES, int KS>
 __global__ void __launch_bounds__(WAVES * 64)
 q4_decode_lds_kernel(DecodeArgs a) {
@@ -74,18 +76,20 @@ q4_decode_lds_kernel(DecodeArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int slot = wave / KS, kp = wave % KS;
     const int c = lane & 15;
     const int g = lane >> 4;
     const int mrows = min(a.M, MR);
     const uint32_t grow = (uint32_t)a.N * BLOCK_BYTES;
-    uint8_t *wlds = smem + wave * S::wave_lds(mrows);
+    // LDS: [zero activations][WAVES x per-wave slice][reduction scratch when KS > 1]
+    uint8_t *zero = smem;
+    uint8_t *wlds = smem + S::ZERO_LDS + wave * S::wave_lds(mrows);
     uint8_t *xlds = wlds + S::W_LDS;
-    float *red = (float *)(smem + WAVES * S::wave_lds(mrows));  // [WAVES][256] when KS > 1
+    float *red = (float *)(smem + S::ZERO_LDS + WAVES * S::wave_lds(mrows));
 
-    // Per-lane chunk geometry of one batch: global byte offsets relative to the
-    // batch's first row, LDS offsets, and the batch row each chunk belongs to.
+    // Strip chunk geometry of one batch (global offset from the batch's first row,
+    // LDS offset, batch row).  Chunk q = lane + 64*i.
     uint32_t soff[LPL], slds[LPL];
     int srow[LPL];
 #pragma unroll
@@ -96,6 +100,7 @@ q4_decode_lds_kernel(DecodeArgs a) {
         soff[i] = (uint32_t)r * grow + 16u * k;
         slds[i] = (uint32_t)(r * ROW_BYTES + 16 * k);
     }
+    // Activation chunk geometry: row m, 16-byte chunk k of the batch's B*32 halves.
     uint32_t xoff[XL], xlo[XL];
     int xrw[XL];
 #pragma unroll
@@ -106,36 +111,114 @@ q4_decode_lds_kernel(DecodeArgs a) {
         xoff[i] = (uint32_t)(m * a.ldx * 2 + 16 * k);
         xlo[i] = (uint32_t)(m * XROW + 16 * k);
     }
-    bool xvalid[MT];
+    // A-operand read base per M tile (row u adds u*64): lanes past M read zeros.
+    const uint8_t *abase[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xvalid[mt] = mt * 16 + c < mrows;
+    for (int mt = 0; mt < MT; ++mt)
+        abase[mt] = (mt * 16 + c < mrows) ? xlds + (mt * 16 + c) * XROW + 16 * g : zero + 16 * g;
+    // B-operand reads: d at c*18, qs bytes 4g..4g+3 at c*18 + 2 + 4g, fetched as the
+    // aligned dword pair around them and funnel-shifted.
+    const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
+    const uint32_t qal = (uint32_t)(qoff & ~3), qsh = (uint32_t)(qoff & 3) * 8;
+    const uint32_t doff = (uint32_t)(c * BLOCK_BYTES);
+
+    // Zero activations for lanes past M (written once, read-only afterwards).
+    for (int i = tid; i < S::ZERO_LDS / 16; i += WAVES * 64)
+        *(uint4_t *)(zero + 16 * i) = uint4_t{0u, 0u, 0u, 0u};
+    __syncthreads();
 
     // This wave's K rows (identical for every tile) and its batch count.
     const int rpp = (a.nb + KS - 1) / KS;
     const int rbeg = min(a.nb, kp * rpp);
     const int rend = min(a.nb, rbeg + rpp);
     const int nbatch = (rend - rbeg + B - 1) / B;
-    // Tile groups walked by this workgroup (uniform across its waves).
     const int ngroups_total = (a.ntiles + TPW - 1) / TPW;
     const int ngroups = (ngroups_total - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
     const uint8_t *xbase = (const uint8_t *)a.X;
+    auto tile_of = [&](int j) { return ((int)blockIdx.x + j * (int)gridDim.x) * TPW + slot; };
 
     uint4_t wv[LPL], xr[XL];
-    auto issue = [&](int tile, int row0) {
+    auto issue_w = [&](int i, int tile, int row0) {
         const int rows = min(B, rend - row0);
         const uint8_t *gb = a.W + (int64_t)tile * (16 * NT * BLOCK_BYTES) + (int64_t)row0 * grow;
-#pragma unroll
-        for (int i = 0; i < LPL; ++i)
-            if (srow[i] < rows) wv[i] = __builtin_nontemporal_load((const uint4_t *)(gb + soff[i]));
+        if (srow[i] < rows) wv[i] = __builtin_nontemporal_load((const uint4_t *)(gb + soff[i]));
+    };
+    auto issue_x = [&](int row0) {
+        const int rows = min(B, rend - row0);
         const uint8_t *xb = xbase + (int64_t)row0 * (QK * 2);
 #pragma unroll
         for (int i = 0; i < XL; ++i)
             if (xrw[i] < rows) xr[i] = *(const uint4_t *)(xb + xoff[i]);
     };
-    auto tile_of = [&](int j) { return ((int)blockIdx.x + j * (int)gridDim.x) * TPW + slot; };
+    auto issue_all = [&](int tile, int row0) {
+        issue_x(row0);
+#pragma unroll
+        for (int i = 0; i < LPL; ++i) issue_w(i, tile, row0);
+    };
+
+    // Per-lane LDS read bases, materialized once so that rows and column tiles
+    // become immediate offsets of the ds_read instructions.
+    uint32_t qo = lds_addr(wlds + qal);
+    uint32_t dof = lds_addr(wlds + doff);
+    uint32_t ao[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) ao[mt] = lds_addr(abase[mt]);
+    asm volatile("" : "+v"(qo), "+v"(dof));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) asm volatile("" : "+v"(ao[mt]));
 
     float4_t acc[MT][NT];
-    if (nbatch > 0 && ngroups > 0 && tile_of(0) < a.ntiles) issue(tile_of(0), rbeg);
+    // Operands of one batch row read from LDS: activations (per M tile), the qs
+    // dword pair and the scale of each column tile.
+    struct RowOps {
+        half8_t av[MT];
+        uint32_t q0[NT], q1[NT], d[NT];
+    };
+    auto row_read = [&](int u) {
+        RowOps o;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) o.av[mt] = *(const lds_half8 *)(lds_ptr(ao[mt]) + u * 64);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const lds_u32 *qp = (const lds_u32 *)(lds_ptr(qo) + u * ROW_BYTES + t * 288);
+            o.q0[t] = qp[0];
+            o.q1[t] = qp[1];
+            o.d[t] = *(const lds_u16 *)(lds_ptr(dof) + u * ROW_BYTES + t * 288);
+        }
+        return o;
+    };
+    auto row_math = [&](const RowOps &o) {
+        if constexpr (MR == 1) {
+            // Single activation row: B holds the exact halves 1024 + q, a second
+            // MFMA against ones gives sum(x) of the block, and the -8 offset and
+            // scale are applied in fp32 on the one output lane that matters
+            // (D[0][c], i = 0 of lanes 0..15):
+            //   y += d * (sum x*(1024+q) - 1032 * sum x) = d * sum x*(q-8).
+            const half8_t ones = {(_Float16)1, (_Float16)1, (_Float16)1, (_Float16)1,
+                                  (_Float16)1, (_Float16)1, (_Float16)1, (_Float16)1};
+            const float4_t z = {0.f, 0.f, 0.f, 0.f};
+            const float4_t sx = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.av[0], ones, z, 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const uint32_t w = __builtin_amdgcn_alignbit(o.q1[t], o.q0[t], qsh);
+                const float d = (float)bitcast<_Float16>((uint16_t)o.d[t]);
+                const float4_t blk =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(o.av[0], unpack8_1024(w), z, 0, 0, 0);
+                acc[0][t][0] = __builtin_fmaf(d, __builtin_fmaf(-1032.f, sx[0], blk[0]), acc[0][t][0]);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const uint32_t w = __builtin_amdgcn_alignbit(o.q1[t], o.q0[t], qsh);
+                const half8_t bv = dequant8_perm(w, o.d[t]);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+                    acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(o.av[mt], bv, acc[mt][t], 0, 0, 0);
+            }
+        }
+    };
+
+    if (nbatch > 0 && ngroups > 0 && tile_of(0) < a.ntiles) issue_all(tile_of(0), rbeg);
     for (int j = 0; j < ngroups; ++j) {
         const int tile = tile_of(j);
         const bool tile_ok = tile < a.ntiles;
@@ -147,39 +230,31 @@ q4_decode_lds_kernel(DecodeArgs a) {
         for (int b = 0; b < nbatch; ++b) {
             const int row0 = rbeg + b * B;
             const int rows = min(B, rend - row0);
+            // Next batch: this tile's, or the next group's tile's first.
+            int ntile = tile, nrow0 = row0 + B;
+            bool more = b + 1 < nbatch && tile_ok;
+            if (b + 1 >= nbatch && j + 1 < ngroups && tile_of(j + 1) < a.ntiles) {
+                ntile = tile_of(j + 1);
+                nrow0 = rbeg;
+                more = true;
+            }
+            // Activations: stage (permuted to the dequant slot order), then prefetch.
             if (tile_ok) {
-                // Stage into this wave's LDS slice (a wave's LDS accesses are ordered).
-#pragma unroll
-                for (int i = 0; i < LPL; ++i)
-                    if (srow[i] < rows) *(uint4_t *)(wlds + slds[i]) = wv[i];
 #pragma unroll
                 for (int i = 0; i < XL; ++i)
-                    if (xrw[i] < rows) *(uint4_t *)(xlds + xlo[i]) = xr[i];
+                    if (xrw[i] < rows)
+                        *(half8_t *)(xlds + xlo[i]) = perm_act8(xr[i]);
             }
-            // Prefetch the next batch (of this tile or of the next group's tile).
-            if (b + 1 < nbatch) {
-                if (tile_ok) issue(tile, row0 + B);
-            } else if (j + 1 < ngroups && tile_of(j + 1) < a.ntiles) {
-                issue(tile_of(j + 1), rbeg);
-            }
-            if (!tile_ok) continue;
-            for (int u = 0; u < rows; ++u) {
-                half8_t av[MT];
+            if (more) issue_x(nrow0);
+            // Strip: stage load i, prefetch its successor, then run the rows it completed.
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-                    av[mt] = xvalid[mt] ? perm_act8(*(const uint4_t *)(xlds + (mt * 16 + c) * XROW +
-                                                                      u * 64 + 16 * g))
-                                        : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+            for (int i = 0; i < LPL; ++i) {
+                if (tile_ok && srow[i] < rows) *(uint4_t *)(wlds + slds[i]) = wv[i];
+                if (more) issue_w(i, ntile, nrow0);
+                if (tile_ok) {
 #pragma unroll
-                for (int t = 0; t < NT; ++t) {
-                    const uint16_t *bp =
-                        (const uint16_t *)(wlds + u * ROW_BYTES + t * 288 + c * BLOCK_BYTES);
-                    const uint32_t w = (uint32_t)bp[1 + 2 * g] | ((uint32_t)bp[2 + 2 * g] << 16);
-                    const half8_t bv = dequant8_perm(w, bp[0]);
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt)
-                        acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[mt], bv, acc[mt][t],
-                                                                            0, 0, 0);
+                    for (int u = 0; u < B; ++u)
+                        if (S::last_load_of_row(u) == i && u < rows) row_math(row_read(u));
                 }
             }
         }
@@ -250,7 +325,7 @@ template <int MR, int NT, int WAVES, int KS>
 static hipError_t launch_dec_t(const DecodeArgs &a, int grid_cap, hipStream_t s) {
     using S = DecodeShape<MR, NT>;
     const int mrows = std::min(a.M, MR);
-    size_t lds = (size_t)WAVES * S::wave_lds(mrows);
+    size_t lds = S::ZERO_LDS + (size_t)WAVES * S::wave_lds(mrows);
     if (KS > 1) lds += (size_t)WAVES * 256 * sizeof(float);
     if (lds > 160 * 1024) return hipErrorInvalidConfiguration;
     // Raise the dynamic-LDS limit once per device (bit d of `done`).
