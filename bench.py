@@ -259,7 +259,7 @@ def main():
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "q4_skinny_kernel (decode GEMV, MFMA 16x16x32 f16)",
+            "kernel": "q4_decode_lds_kernel (decode GEMV, M=1)",
             "avg_launch_us": round(t_launch * 1e6, 3),
         },
         "prefill": {
@@ -272,7 +272,7 @@ def main():
                 "unit": "TFLOP/s",
                 "frac": round(pre_up["tflops"] / FP16_PEAK_TFLOPS, 4),
                 "traffic": None,
-                "kernel": "q4_gemm_kernel (M=2048 K=4096 N=14336)",
+                "kernel": "q4_gemm2_kernel (M=2048 K=4096 N=14336)",
             },
         },
         "cpu_baseline": cpu,

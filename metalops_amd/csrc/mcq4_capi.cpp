@@ -23,6 +23,9 @@ hipError_t launch_skinny(const _Float16 *X, int64_t ldx, const uint8_t *W, _Floa
 size_t gemm_workspace_bytes(int64_t M, int64_t K, int64_t N);
 hipError_t launch_gemm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
+bool gemm2_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
+hipError_t launch_gemm2(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, hipStream_t s);
 }  // namespace mcq4
 
 namespace {
@@ -46,6 +49,20 @@ constexpr int64_t kMaxBlocksK = 65535;        // grid.y limit of the conversion 
 constexpr int64_t kMaxDim = (int64_t)1 << 30;  // keeps 32-bit lane offsets safe
 
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+// Prefill kernel choice: the async-copy GEMM when its alignment needs hold and
+// the output has at least 128 tiles of 128x256 (about half the CUs); smaller
+// outputs go to the register-staged kernel, whose split-K fills the chip.
+// MCQ4_GEMM_PATH=sync / =async force one kernel.
+bool use_gemm2(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
+               int64_t N) {
+    if (!mcq4::gemm2_supported(X, ldx, W, K, N)) return false;
+    if (const char *env = getenv("MCQ4_GEMM_PATH")) {
+        if (env[0] == 's') return false;
+        if (env[0] == 'a') return true;
+    }
+    return ((M + 127) / 128) * ((N + 255) / 256) >= 128;
+}
 
 int check_kn(int64_t K, int64_t N) {
     if (K <= 0 || N <= 0) return fail(MCQ4_ERR_SHAPE, "K (%lld) and N (%lld) must be positive",
@@ -119,7 +136,7 @@ int mcq4_dequantize_q4_0(const uint8_t *blocks, int64_t K, int64_t N, void *out,
 size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M <= 0 || K <= 0 || N <= 0 || K % 32) return 0;
     if (M <= 64) return mcq4::skinny_workspace_bytes(M, K, N);
-    return mcq4::gemm_workspace_bytes(M, K, N);
+    return mcq4::gemm_workspace_bytes(M, K, N);  // an upper bound for either prefill kernel
 }
 
 int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, int64_t ldy,
@@ -146,6 +163,9 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
     if (M <= 64)
         e = mcq4::launch_skinny((const _Float16 *)X, ldx, W, (_Float16 *)Y, ldy, (int)M, (int)K,
                                 (int)N, workspace, (hipStream_t)stream);
+    else if (use_gemm2((const _Float16 *)X, ldx, W, M, K, N))
+        e = mcq4::launch_gemm2((const _Float16 *)X, ldx, W, (_Float16 *)Y, ldy, (int)M, (int)K,
+                               (int)N, (hipStream_t)stream);
     else
         e = mcq4::launch_gemm((const _Float16 *)X, ldx, W, (_Float16 *)Y, ldy, (int)M, (int)K,
                               (int)N, workspace, (hipStream_t)stream);

@@ -172,3 +172,35 @@ def test_matmul_prefill_configs(dev, M, K, N):
 def test_matmul_lm_head(dev):
     _full_size_check(dev, 1, 4096, 128256)
     _full_size_check(dev, 512, 4096, 128256)
+
+
+# Every kernel variant on ragged and full shapes: the launchers read these
+# environment variables on each call, so a test can pin the variant it checks.
+PATHS = {
+    "decode_lds": {},
+    "decode_direct": {"MCQ4_DECODE_PATH": "direct"},
+    "gemm_sync": {"MCQ4_GEMM_PATH": "sync"},
+    "gemm_async_bm256": {"MCQ4_GEMM_PATH": "async", "MCQ4_GEMM2_BM": "256"},
+    "gemm_async_bm128": {"MCQ4_GEMM_PATH": "async", "MCQ4_GEMM2_BM": "128"},
+}
+PATH_SHAPES = {
+    "decode_lds": [(1, 352, 264), (3, 1024, 520), (16, 4096, 1032), (40, 2048, 96), (64, 256, 64)],
+    "decode_direct": [(1, 352, 257), (7, 1024, 520), (16, 4096, 1000), (64, 512, 72)],
+    "gemm_sync": [(65, 352, 70), (200, 1024, 264), (300, 2048, 520)],
+    "gemm_async_bm256": [(65, 352, 72), (257, 1024, 264), (300, 2048, 520), (512, 4096, 776)],
+    "gemm_async_bm128": [(65, 352, 72), (129, 1024, 264), (300, 2048, 520), (384, 4096, 776)],
+}
+
+
+@pytest.mark.parametrize("path,M,K,N", [(p, *s) for p, shapes in PATH_SHAPES.items() for s in shapes])
+def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
+    for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM"):
+        monkeypatch.delenv(k, raising=False)
+    for k, v in PATHS[path].items():
+        monkeypatch.setenv(k, v)
+    mo = _mo()
+    W = _weights(K, N, seed=M * 7 + K + N, outliers=True)
+    X = _acts(M, K, seed=M + 11)
+    blocks = ref.quantize_llama_rule(W.numpy())
+    Y = mo.matmul_ggml_q4_0(X.to(dev), torch.from_numpy(blocks).to(dev))
+    _check_rows(Y.float().cpu().numpy(), ref.matmul_f32(X.numpy(), blocks))
