@@ -33,6 +33,13 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
 
+# HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the same
+# workloads (bench.py --part decode|prefill), each counter scaled by what it reads
+# for a plain 256 MiB device copy (FETCH_SIZE x 2, WRITE_SIZE x 1).  Figures and
+# commands: profiles/decode_lds_llama7b_m1.md, profiles/gemm2_llama7b_m2048.md.
+DECODE_TRAFFIC_BYTES = 22945155       # average over the five projections
+PREFILL_UP_TRAFFIC_BYTES = 360800000  # 302.0 MB read + 58.8 MB written
+
 DECODE_LAYER = [  # (name, K, N) -- Llama-2-7B projections, configs[1]
     ("qkv", 4096, 12288),
     ("o_proj", 4096, 4096),
@@ -56,8 +63,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
-    p.add_argument("--sweep", action="store_true",
-                   help="also print one JSON line per BASELINE config to stderr")
+    p.add_argument("--part", choices=["all", "decode", "prefill", "copy"], default="all",
+                   help="run one part only (for profiler passes); 'copy' runs a plain 256 MiB "
+                        "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters")
     return p.parse_args()
 
 
@@ -200,6 +208,27 @@ def cpu_baseline(seconds_budget):
     }
 
 
+def run_part(mo, torch, dev, args):
+    """One part of the benchmark, printing its own JSON line (profiler passes)."""
+    if args.part == "copy":
+        a = torch.ones(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"part": "copy", "bytes_read": a.numel(), "bytes_written": b.numel(),
+                          "launches": 5}), flush=True)
+    elif args.part == "decode":
+        dec = decode_bench(mo, torch, dev, args)
+        t = dec["seconds"] / dec["steps"]
+        print(json.dumps({"part": "decode", "GB/s": round(dec["bytes_step"] / t / 1e9, 1),
+                          "us_per_launch": round(t / dec["launches_step"] * 1e6, 3),
+                          "weight_bytes_per_launch": dec["bytes_step"] / dec["launches_step"]}),
+              flush=True)
+    else:
+        print(json.dumps({"part": "prefill", "configs": prefill_bench(mo, torch, dev)}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -216,6 +245,10 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+
+    if args.part != "all":
+        run_part(mo, torch, dev, args)
+        return
 
     dec = decode_bench(mo, torch, dev, args)
     t_step = dec["seconds"] / dec["steps"]
@@ -258,7 +291,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": DECODE_TRAFFIC_BYTES,
+            "algorithmic_bytes_per_launch": dec["bytes_step"] // dec["launches_step"],
             "kernel": "q4_decode_lds_kernel (decode GEMV, M=1)",
             "avg_launch_us": round(t_launch * 1e6, 3),
         },
@@ -271,7 +305,7 @@ def main():
                 "peak": FP16_PEAK_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": round(pre_up["tflops"] / FP16_PEAK_TFLOPS, 4),
-                "traffic": None,
+                "traffic": PREFILL_UP_TRAFFIC_BYTES,
                 "kernel": "q4_gemm2_kernel (M=2048 K=4096 N=14336)",
             },
         },

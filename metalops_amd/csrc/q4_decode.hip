@@ -132,10 +132,17 @@ q4_decode_lds_kernel(DecodeArgs a) {
     const int rbeg = min(a.nb, kp * rpp);
     const int rend = min(a.nb, rbeg + rpp);
     const int nbatch = (rend - rbeg + B - 1) / B;
+    // XCD-aware numbering: workgroups are dispatched round-robin over the 8 XCDs,
+    // so workgroup b runs on XCD b % 8.  Neighbouring tile groups share 128-byte
+    // lines (a 16-column strip row is 288 bytes), so consecutive groups go to
+    // workgroups of one XCD, whose L2 then fetches each shared line once.
+    const int G = (int)gridDim.x, G8 = G & ~7;
+    int wg = (int)blockIdx.x;
+    if (wg < G8) wg = (wg & 7) * (G8 >> 3) + (wg >> 3);
     const int ngroups_total = (a.ntiles + TPW - 1) / TPW;
-    const int ngroups = (ngroups_total - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int ngroups = (ngroups_total - wg + G - 1) / G;
     const uint8_t *xbase = (const uint8_t *)a.X;
-    auto tile_of = [&](int j) { return ((int)blockIdx.x + j * (int)gridDim.x) * TPW + slot; };
+    auto tile_of = [&](int j) { return (wg + j * G) * TPW + slot; };
 
     uint4_t wv[LPL], xr[XL];
     auto issue_w = [&](int i, int tile, int row0) {
