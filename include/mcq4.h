@@ -10,8 +10,8 @@
  *   - enqueues asynchronously on the given stream and returns a status code (no
  *     exceptions cross the ABI); mcq4_last_error() gives a message for the last
  *     failure on the calling thread;
- *   - is re-entrant (no global mutable state apart from the one-time device
- *     property query).
+ *   - is re-entrant: the only global state is a once-per-device raise of the
+ *     kernels' dynamic-LDS limit (hipFuncSetAttribute), guarded by an atomic.
  *
  * Weight format (quantization.py:296-304): blocks[K/32][N][18] uint8; bytes 0..1
  * of a block are the fp16 scale d (little endian), byte 2+i holds element 2i in
@@ -81,8 +81,8 @@ size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N);
 /*
  * matmul_ggml_q4_0 (quantization.py:422-454; Metal host binding
  * native/core_mps.mm:5917-5975): Y[M][ldy] = X[M][ldx] @ dequant(W), fp16 in,
- * fp32 accumulation, fp16 out.  M <= 64 runs the decode (skinny MFMA) kernel,
- * larger M the prefill MFMA GEMM.
+ * fp32 accumulation, fp16 out.  M <= 64 runs the decode GEMV kernels, larger M
+ * the prefill MFMA GEMM kernels.
  * Requirements: K % 32 == 0; X 16-byte aligned with ldx % 8 == 0; W 2-byte
  * aligned; Y 2-byte aligned; ldx >= K, ldy >= N.
  */
