@@ -36,8 +36,8 @@ FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
 # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the same
 # workloads (bench.py --part decode|prefill), each counter scaled by what it reads
 # for a plain 256 MiB device copy (FETCH_SIZE x 2, WRITE_SIZE x 1).  Figures and
-# commands: profiles/decode_lds_llama7b_m1.md, profiles/gemm2_llama7b_m2048.md.
-DECODE_TRAFFIC_BYTES = 22945155       # average over the five projections
+# commands: profiles/gemv_dma_llama7b_m1.md, profiles/gemm2_llama7b_m2048.md.
+DECODE_TRAFFIC_BYTES = 22985587       # average over the five projections
 PREFILL_UP_TRAFFIC_BYTES = 360800000  # 302.0 MB read + 58.8 MB written
 
 DECODE_LAYER = [  # (name, K, N) -- Llama-2-7B projections, configs[1]
@@ -293,7 +293,7 @@ def main():
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": DECODE_TRAFFIC_BYTES,
             "algorithmic_bytes_per_launch": dec["bytes_step"] // dec["launches_step"],
-            "kernel": "q4_decode_lds_kernel (decode GEMV, M=1)",
+            "kernel": "q4_gemv_dma_kernel (decode GEMV, M=1)",
             "avg_launch_us": round(t_launch * 1e6, 3),
         },
         "prefill": {

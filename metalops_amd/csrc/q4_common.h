@@ -49,6 +49,58 @@ __device__ __forceinline__ To bitcast(const From &f) {
     return __builtin_bit_cast(To, f);
 }
 
+__device__ __forceinline__ int64_t imin64(int64_t x, int64_t y) { return x < y ? x : y; }
+
+// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Workgroup barrier that waits only for this wave's LDS traffic.  (__syncthreads
+// also waits for all outstanding vector-memory operations, which would drain the
+// async copies that are meant to stay in flight across the barrier; the explicit
+// wait_vmcnt calls establish that the data consumed next has landed.)
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// (x & mask) | bits.  With `mask` in an SGPR and `bits` in a VGPR (see
+// opaque_sgpr / opaque_vgpr) this selects one v_and_or_b32; with literal
+// constants gfx9 needs a separate v_and and v_or (VOP3 encodes no literal).
+// Plain C on purpose: instructions written in inline asm are invisible to the
+// compiler's MFMA hazard tracking, so an asm VALU write to a register that an
+// in-flight MFMA will write gets clobbered.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t bits) {
+    return (x & mask) | bits;
+}
+__device__ __forceinline__ uint32_t opaque_sgpr(uint32_t v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+__device__ __forceinline__ uint32_t opaque_vgpr(uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+// Eight nibbles (elements e0..e7 at bits 4e..4e+3 of `w`) -> fp16 halves
+// 1024 + q in natural element order [e0..e7]: the even/odd nibble bytes are
+// interleaved first, then each byte pair gets the 0x64 exponent byte.
+__device__ __forceinline__ half8_t unpack8_1024_nat(uint32_t w) {
+    const uint32_t C64 = 0x64646464u;
+    const uint32_t lo = w & 0x0F0F0F0Fu;
+    const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
+    const uint32_t e03 = __builtin_amdgcn_perm(hi, lo, 0x05010400u);   // e0 e1 e2 e3
+    const uint32_t e47 = __builtin_amdgcn_perm(hi, lo, 0x07030602u);   // e4 e5 e6 e7
+    uint4_t r;
+    r[0] = __builtin_amdgcn_perm(C64, e03, 0x04010400u);
+    r[1] = __builtin_amdgcn_perm(C64, e03, 0x04030402u);
+    r[2] = __builtin_amdgcn_perm(C64, e47, 0x04010400u);
+    r[3] = __builtin_amdgcn_perm(C64, e47, 0x04030402u);
+    return bitcast<half8_t>(r);
+}
+
 // Eight nibbles (elements e0..e7 at bits 4e..4e+3 of `w`, i.e. byte i holds
 // e_{2i} low and e_{2i+1} high) and the fp16 bits of d -> eight fp16 weights
 // (q-8)*d in the slot order [e0,e2,e4,e6,e1,e3,e5,e7].

@@ -56,23 +56,6 @@ struct G2Layout {
     static constexpr int A_LOADS = BM * 4 / 64 / 4;   // 1 KiB copies per wave per step
 };
 
-__device__ __forceinline__ int64_t imin64(int64_t x, int64_t y) { return x < y ? x : y; }
-
-// s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | [15:14]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
-}
-
-// Workgroup barrier that waits only for this wave's LDS traffic.  (__syncthreads
-// also waits for all outstanding vector-memory operations, which would drain the
-// async copies that are meant to stay in flight across the barrier; the explicit
-// wait_vmcnt calls establish that the data consumed next has landed.)
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 template <int BM>
 __global__ void __launch_bounds__(G2_THREADS, 1)
 q4_gemm2_kernel(Gemm2Args a) {

@@ -1,0 +1,302 @@
+// Single-row (M == 1) q4_0 GEMV on gfx950.
+//
+// A decode projection reads 9-30 MB of q4_0 weights once; at that size the
+// launch latency and every serial step of a workgroup matter as much as the
+// bandwidth.  The kernel keeps the weight stream in asynchronous
+// global->LDS copies (no VGPR staging, exact vmcnt accounting) and keeps the
+// per-row math to one MFMA, two LDS reads and seven VALU instructions.
+//
+// Work decomposition
+//   * Column tile = 16 columns (a 288-byte strip row per K block).  Item = one
+//     tile's batch of B = 8 consecutive K blocks (8 strip rows, 2304 bytes).
+//   * Workgroup = 16 waves owning TPW tiles: wg, wg+G, ... (wg renumbered so
+//     consecutive tiles, which share 128-byte lines, run on one XCD).  Wave w
+//     owns batches b = w, w+16, ... of every one of those tiles and walks them
+//     batch-major: for each of its batches, the TPW tiles in turn.  The
+//     batch's activations therefore stay in registers across the tiles.
+//   * Copies: per item exactly three global_load_lds_dwordx4 (1 KiB each; 144
+//     chunks, lanes 16..63 of the last masked) into a per-wave ring of R LDS
+//     slots; item k+R-1 is issued (into the slot item k-1 freed) before the wave
+//     waits for item k.  Rows past K re-copy row 0, so every item issues the same number of
+//     copies and the vmcnt waits are exact.
+//   * Activations: lane (c = l%16, g = l/16) loads elements 8g..8g+7 of each of
+//     the batch's 8 K blocks straight from global memory (all 16 lanes of a
+//     group load the same 16 bytes) and rearranges them to
+//     x' = [x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16] (4 v_perm, 2 v_pk_mul).
+//   * Weights: lane (c, g) reads the qs dword w of elements 8g..8g+7 of column
+//     c.  Four v_and_or_b32 build the fp16 operand
+//     [1024+q0, 1024+q4, 1024+16q1, 1024+16q5, 1024+q2, 1024+q6, 1024+16q3,
+//     1024+16q7] (low nibbles as is, high nibbles in place = times 16, which x'
+//     divides out).  Against the constant operand C = [1032, 1032, 1152, 1152,
+//     1032, 1032, 1152, 1152] the same x' gives S = 1024 sum(x') + 8 sum(x), so
+//     one MFMA per K block and batch, mfma(x', -C), yields -S; it is the
+//     accumulator input of the per-item MFMA:
+//     mfma(x', B, -S)[0] = sum x*(q - 8), exact products, fp32 sums.
+//   * acc_tile += d * that, in fp32.
+//   * Epilogue: partials of the 16 waves per column summed through LDS in wave
+//     order (deterministic), stored as fp16.
+#include <algorithm>
+#include <atomic>
+
+#include "q4_common.h"
+
+
+
+namespace mcq4 {
+
+constexpr int GV_WAVES = 16;
+constexpr int GV_B = 8;                      // K blocks per item
+constexpr int GV_ROW = 288;                  // strip bytes per K block (16 columns)
+constexpr int GV_WCH = GV_B * 18;            // 144 strip chunks of 16 bytes per item
+constexpr int GV_LOADS = 3;                  // copies per item (chunks 0..143 of 192)
+constexpr int GV_SLOT = GV_WCH * 16 + 64;    // 2304 strip bytes + read overhang
+constexpr int GV_TPW_MAX = 4;                // tiles per workgroup
+constexpr int GV_XB_MAX = 4;                 // batches per wave (K <= 16*4*8*32 = 16384)
+constexpr int GV_XW = GV_XB_MAX * GV_B * 64; // activation bytes per wave in LDS
+constexpr int GV_NT = 2;                     // cache policy of the weight copies: non-temporal
+
+struct GemvArgs {
+    const _Float16 *X;
+    const uint8_t *W;
+    _Float16 *Y;
+    int nb, N, ntiles, nbt;                  // nbt = batches per tile
+};
+
+template <int R>
+__device__ __forceinline__ void gv_wait(int pending) {
+    // Wait until at most `pending` items (LOADS copies each) are still in flight.
+    if (R > 3 && pending >= 3) { wait_vmcnt<3 * GV_LOADS>(); return; }
+    if (R > 2 && pending >= 2) { wait_vmcnt<2 * GV_LOADS>(); return; }
+    if (R > 1 && pending >= 1) { wait_vmcnt<1 * GV_LOADS>(); return; }
+    wait_vmcnt<0>();
+}
+
+template <int R, int TPW>
+__global__ void __launch_bounds__(GV_WAVES * 64)
+q4_gemv_dma_kernel(GemvArgs a) {
+    static_assert(R >= 1 && R <= 3 && TPW >= 1 && TPW <= GV_TPW_MAX, "config");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const uint32_t grow = (uint32_t)a.N * BLOCK_BYTES;
+
+    // LDS: [16 waves x R slots][16 waves x activations][partials: TPW x 16 waves x 16]
+    uint8_t *ring = smem + wave * (R * GV_SLOT);
+    uint8_t *xs = smem + GV_WAVES * R * GV_SLOT + wave * GV_XW;
+    float *red = (float *)(smem + GV_WAVES * (R * GV_SLOT + GV_XW));
+
+    const int G = (int)gridDim.x, G8 = G & ~7;
+    int wg = (int)blockIdx.x;
+    if (wg < G8) wg = (wg & 7) * (G8 >> 3) + (wg >> 3);
+    const int ntl = min(TPW, (a.ntiles - wg + G - 1) / G);         // >= 1 (grid <= ntiles)
+    const int nbm = a.nbt > wave ? (a.nbt - wave + GV_WAVES - 1) / GV_WAVES : 0;  // my batches
+    const int nmine = nbm * ntl;
+
+    // Copy geometry per lane and copy i: strip chunk q = lane + 64 i of an item
+    // (row q/18, 16-byte piece q%18); q >= 144 is masked off.
+    int crow[GV_LOADS];
+    uint32_t coff[GV_LOADS];
+#pragma unroll
+    for (int i = 0; i < GV_LOADS; ++i) {
+        const int q = lane + 64 * i;
+        crow[i] = q < GV_WCH ? q / 18 : 0;
+        coff[i] = q < GV_WCH ? (uint32_t)(q / 18) * grow + 16u * (uint32_t)(q % 18) : 0u;
+    }
+    // Item (batch index m of this wave, tile j) into ring slot `slot`.
+    auto issue = [&](int m, int j, int slot) {
+        const int row0 = (wave + GV_WAVES * m) * GV_B;
+        const int rows = min(GV_B, a.nb - row0);
+        const uint8_t *wb = a.W + (int64_t)(wg + j * G) * GV_ROW + (int64_t)row0 * grow;
+#pragma unroll
+        for (int i = 0; i < GV_LOADS; ++i) {
+            // Rows past K re-copy row 0 (valid memory, never read back).
+            const uint32_t off = crow[i] < rows ? coff[i] : coff[i] - (uint32_t)crow[i] * grow;
+            if (i < GV_LOADS - 1 || lane < GV_WCH - 64 * (GV_LOADS - 1))
+                __builtin_amdgcn_global_load_lds(
+                    (void *)(wb + off),
+                    (__attribute__((address_space(3))) void *)(ring + slot * GV_SLOT + 1024 * i),
+                    16, 0, GV_NT);
+        }
+    };
+
+    // Prologue: the first R items in flight (issue cursor im, ij, islot).
+    int im = 0, ij = 0, islot = 0;
+    auto issue_next = [&]() {
+        issue(im, ij, islot);
+        islot = islot + 1 == R ? 0 : islot + 1;
+        if (++ij == ntl) { ij = 0; ++im; }
+    };
+    // Activations of all my batches first (512 bytes each: lanes 0..31 copy row
+    // lane/4, piece lane%4; rows past K clamp to the last row), so they are
+    // older than every weight copy and land before the first item does.
+    for (int m = 0; m < nbm; ++m) {
+        const int r = min((wave + GV_WAVES * m) * GV_B + (lane >> 2), a.nb - 1);
+        if (lane < 32)
+            __builtin_amdgcn_global_load_lds(
+                (void *)((const uint8_t *)a.X + (int64_t)r * (QK * 2) + 16 * (lane & 3)),
+                (__attribute__((address_space(3))) void *)(xs + m * (GV_B * 64)), 16, 0, 0);
+    }
+    // R-1 items ahead; each iteration issues one more before it waits, into the
+    // slot the previous item freed.
+    const int npro = min(R - 1, nmine);
+    for (int k = 0; k < npro; ++k) issue_next();
+
+    const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
+    const uint32_t qal = (uint32_t)(qoff & ~3), qsh = (uint32_t)(qoff & 3) * 8;
+    const uint32_t doff = (uint32_t)(c * BLOCK_BYTES);
+    const uint32_t c64 = opaque_vgpr(0x64006400u);
+    const uint32_t mlo = opaque_sgpr(0x000F000Fu), mhi = opaque_sgpr(0x00F000F0u);
+    // -C as the fp16 operand: (-1032, -1032) and (-1152, -1152) pairs.
+    const uint32_t nlo = 0xE408E408u, nhi = 0xE480E480u;
+    const half8_t negc = bitcast<half8_t>(uint4_t{nlo, nhi, nlo, nhi});
+    const float4_t z = {0.f, 0.f, 0.f, 0.f};
+    const half2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+
+    float acc[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) acc[j] = 0.f;
+
+    int k = 0, slot = 0;
+    for (int m = 0; m < nbm; ++m) {
+        const int row0 = (wave + GV_WAVES * m) * GV_B;
+        const int rows = min(GV_B, a.nb - row0);
+        half8_t xq[GV_B];
+        float4_t negs[GV_B];
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) {
+            if (j < ntl) {
+                if (k + R - 1 < nmine) issue_next();
+                gv_wait<R>(min(R - 1, nmine - 1 - k));
+                if (j == 0) {
+                    // The batch's activations (copied before any weights, so landed).
+                    const uint32_t xa = lds_addr(xs + m * (GV_B * 64) + 16 * g);
+#pragma unroll
+                    for (int u = 0; u < GV_B; ++u) {
+                        const uint4_t x = bitcast<uint4_t>(*(const lds_half8 *)(lds_ptr(xa) + u * 64));
+                        const uint32_t h15 = __builtin_amdgcn_perm(x[2], x[0], 0x07060302u);   // x1, x5
+                        const uint32_t h37 = __builtin_amdgcn_perm(x[3], x[1], 0x07060302u);   // x3, x7
+                        const uint4_t v = {__builtin_amdgcn_perm(x[2], x[0], 0x05040100u),     // x0, x4
+                                           bitcast<uint32_t>(bitcast<half2_t>(h15) * s16),
+                                           __builtin_amdgcn_perm(x[3], x[1], 0x05040100u),     // x2, x6
+                                           bitcast<uint32_t>(bitcast<half2_t>(h37) * s16)};
+                        xq[u] = bitcast<half8_t>(v);
+                        negs[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], negc, z, 0, 0, 0);
+                    }
+                }
+                const uint32_t base = lds_addr(ring + slot * GV_SLOT);
+                const uint32_t qa = base + qal, da = base + doff;
+                auto row = [&](int u) {
+                    const lds_u32 *qp = (const lds_u32 *)(lds_ptr(qa) + u * GV_ROW);
+                    const uint32_t q0 = qp[0], q1 = qp[1];
+                    const uint32_t w = __builtin_amdgcn_alignbit(q1, q0, qsh);
+                    const uint32_t w8 = __builtin_amdgcn_alignbit(q1, q0, qsh + 8);
+                    const float d = (float)bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(da) + u * GV_ROW));
+                    const uint4_t bq = {and_or(w, mlo, c64), and_or(w, mhi, c64),
+                                        and_or(w8, mlo, c64), and_or(w8, mhi, c64)};
+                    const float4_t blk =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], bitcast<half8_t>(bq), negs[u], 0, 0, 0);
+                    return d * blk[0];
+                };
+                if (rows == GV_B) {
+                    float part[GV_B];
+#pragma unroll
+                    for (int u = 0; u < GV_B; ++u) part[u] = row(u);
+#pragma unroll
+                    for (int u = 0; u < GV_B; ++u) acc[j] += part[u];
+                } else {
+#pragma unroll
+                    for (int u = 0; u < GV_B; ++u)
+                        if (u < rows) acc[j] += row(u);
+                }
+                // All reads of this slot are done before the next iteration refills it.
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                slot = slot + 1 == R ? 0 : slot + 1;
+                ++k;
+            }
+        }
+    }
+
+    // Partials (lanes 0..15 hold column c = lane), then the ordered wave sum.
+    if (lane < 16) {
+#pragma unroll
+        for (int j = 0; j < TPW; ++j)
+            if (j < ntl) red[(j * GV_WAVES + wave) * 16 + lane] = nbm > 0 ? acc[j] : 0.f;
+    }
+    __syncthreads();
+    for (int v = tid; v < ntl * 16; v += GV_WAVES * 64) {
+        const int j = v >> 4, col = v & 15;
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < GV_WAVES; ++w) s += red[(j * GV_WAVES + w) * 16 + col];
+        a.Y[(wg + j * G) * 16 + col] = (_Float16)s;
+    }
+}
+
+static size_t gemv_lds_bytes(int R, int tpw) {
+    return (size_t)GV_WAVES * (R * GV_SLOT + GV_XW) + (size_t)tpw * GV_WAVES * 16 * sizeof(float);
+}
+
+template <int R, int TPW>
+static hipError_t launch_gemv_t(const GemvArgs &a, int grid, hipStream_t s) {
+    const size_t lds = gemv_lds_bytes(R, TPW);
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(done.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void *)q4_gemv_dma_kernel<R, TPW>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        done.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    hipLaunchKernelGGL((q4_gemv_dma_kernel<R, TPW>), dim3(grid), dim3(GV_WAVES * 64), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int R>
+static hipError_t launch_gemv_r(const GemvArgs &a, int grid, int tpw, hipStream_t s) {
+    switch (tpw) {
+        case 1: return launch_gemv_t<R, 1>(a, grid, s);
+        case 2: return launch_gemv_t<R, 2>(a, grid, s);
+        case 3: return launch_gemv_t<R, 3>(a, grid, s);
+        default: return launch_gemv_t<R, 4>(a, grid, s);
+    }
+}
+
+// True when the M == 1 kernel applies: 16-byte aligned weights and
+// activations, 18*N a multiple of 16 (N % 8 == 0), at least one whole 16-column
+// tile, at most GV_TPW_MAX tiles per workgroup on a 256-workgroup grid
+// (N <= 16384) and at most GV_XB_MAX batches per wave (K <= 16384).
+bool gemv_dma_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t N) {
+    if (const char *env = getenv("MCQ4_GEMV_PATH"))
+        if (env[0] == 'o') return false;        // "off": use the batched decode kernel
+    return N % 8 == 0 && N >= 16 && N / 16 <= 256 * GV_TPW_MAX && ((uintptr_t)W % 16) == 0 &&
+           ((uintptr_t)X % 16) == 0 && K >= QK && K <= GV_WAVES * GV_XB_MAX * GV_B * QK &&
+           N * 18 * 8 < ((int64_t)1 << 31);
+}
+
+// Launches the M == 1 kernel over the whole 16-column tiles; *n_done returns the
+// number of leading columns covered.
+hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int K, int N,
+                           int *n_done, hipStream_t s) {
+    GemvArgs a;
+    a.X = X; a.W = W; a.Y = Y;
+    a.nb = K / QK; a.N = N;
+    a.ntiles = N / 16;
+    a.nbt = (a.nb + GV_B - 1) / GV_B;
+    *n_done = a.ntiles * 16;
+    const int grid = std::min(a.ntiles, 256);
+    const int tpw = (a.ntiles + grid - 1) / grid;
+    int ring = 2;
+    if (const char *env = getenv("MCQ4_GEMV_RING")) ring = std::max(1, std::min(3, atoi(env)));
+    switch (ring) {
+        case 3: return launch_gemv_r<3>(a, grid, tpw, s);
+        case 2: return launch_gemv_r<2>(a, grid, tpw, s);
+        default: return launch_gemv_r<1>(a, grid, tpw, s);
+    }
+}
+
+}  // namespace mcq4

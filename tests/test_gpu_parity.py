@@ -177,6 +177,10 @@ def test_matmul_lm_head(dev):
 # Every kernel variant on ragged and full shapes: the launchers read these
 # environment variables on each call, so a test can pin the variant it checks.
 PATHS = {
+    "gemv_dma": {},
+    "gemv_dma_ring1": {"MCQ4_GEMV_RING": "1"},
+    "gemv_dma_ring3": {"MCQ4_GEMV_RING": "3"},
+    "decode_lds_m1": {"MCQ4_GEMV_PATH": "off"},
     "decode_lds": {},
     "decode_direct": {"MCQ4_DECODE_PATH": "direct"},
     "gemm_sync": {"MCQ4_GEMM_PATH": "sync"},
@@ -184,6 +188,11 @@ PATHS = {
     "gemm_async_bm128": {"MCQ4_GEMM_PATH": "async", "MCQ4_GEMM2_BM": "128"},
 }
 PATH_SHAPES = {
+    "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
+                 (1, 16384, 272), (1, 14336, 4096)],
+    "gemv_dma_ring1": [(1, 352, 264), (1, 2048, 1040)],
+    "gemv_dma_ring3": [(1, 352, 264), (1, 11008, 4096), (1, 4096, 12288)],
+    "decode_lds_m1": [(1, 352, 264), (1, 4096, 1032)],
     "decode_lds": [(1, 352, 264), (3, 1024, 520), (16, 4096, 1032), (40, 2048, 96), (64, 256, 64)],
     "decode_direct": [(1, 352, 257), (7, 1024, 520), (16, 4096, 1000), (64, 512, 72)],
     "gemm_sync": [(65, 352, 70), (200, 1024, 264), (300, 2048, 520)],
@@ -194,7 +203,8 @@ PATH_SHAPES = {
 
 @pytest.mark.parametrize("path,M,K,N", [(p, *s) for p, shapes in PATH_SHAPES.items() for s in shapes])
 def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
-    for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM"):
+    for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM", "MCQ4_GEMV_PATH",
+              "MCQ4_GEMV_RING"):
         monkeypatch.delenv(k, raising=False)
     for k, v in PATHS[path].items():
         monkeypatch.setenv(k, v)
