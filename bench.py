@@ -36,7 +36,7 @@ FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
 # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the same
 # workloads (bench.py --part decode|prefill), each counter scaled by what it reads
 # for a plain 256 MiB device copy (FETCH_SIZE x 2, WRITE_SIZE x 1).  Figures and
-# commands: profiles/gemv_dma_llama7b_m1.md, profiles/gemm2_llama7b_m2048.md.
+# commands: profiles/gemv_dma_llama7b_m1.md, profiles/gemm4_llama7b_m2048.md.
 DECODE_TRAFFIC_BYTES = 22985587       # average over the five projections
 PREFILL_UP_TRAFFIC_BYTES = 360800000  # 302.0 MB read + 58.8 MB written
 
@@ -159,7 +159,7 @@ def decode_bench(mo, torch, dev, args):
     }
 
 
-def prefill_bench(mo, torch, dev, iters=20, warmup=3):
+def prefill_bench(mo, torch, dev, iters=30, warmup=10):
     out = []
     stream = torch.cuda.Stream(dev)
     for name, M, K, N in PREFILL:
@@ -306,7 +306,7 @@ def main():
                 "unit": "TFLOP/s",
                 "frac": round(pre_up["tflops"] / FP16_PEAK_TFLOPS, 4),
                 "traffic": PREFILL_UP_TRAFFIC_BYTES,
-                "kernel": "q4_gemm2_kernel (M=2048 K=4096 N=14336)",
+                "kernel": "q4_gemm4_kernel (M=2048 K=4096 N=14336)",
             },
         },
         "cpu_baseline": cpu,

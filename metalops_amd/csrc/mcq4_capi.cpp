@@ -26,6 +26,11 @@ hipError_t launch_gemm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float1
 bool gemm2_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
 hipError_t launch_gemm2(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, hipStream_t s);
+hipError_t launch_gemm3(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, hipStream_t s);
+bool gemm4_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
+hipError_t launch_gemm4(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, hipStream_t s);
 }  // namespace mcq4
 
 namespace {
@@ -50,18 +55,25 @@ constexpr int64_t kMaxDim = (int64_t)1 << 30;  // keeps 32-bit lane offsets safe
 
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Prefill kernel choice: the async-copy GEMM when its alignment needs hold and
-// the output has at least 128 tiles of 128x256 (about half the CUs); smaller
-// outputs go to the register-staged kernel, whose split-K fills the chip.
-// MCQ4_GEMM_PATH=sync / =async force one kernel.
-bool use_gemm2(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
-               int64_t N) {
-    if (!mcq4::gemm2_supported(X, ldx, W, K, N)) return false;
+// Prefill kernel choice (M > 64).  Default: the barrier-free GEMM (q4_gemm4)
+// when N % 128 == 0 and the pointers are 16-byte aligned; otherwise the
+// async-copy GEMM (q4_gemm2) when its alignment needs hold and the output has
+// at least 128 tiles of 128x256; otherwise the register-staged split-K kernel.
+// MCQ4_GEMM_PATH=sync|async|3|4 forces one kernel (tests, experiments).
+enum class Prefill { Sync, Async2, Async3, Free4 };
+Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
+                       int64_t N) {
+    const bool ok2 = mcq4::gemm2_supported(X, ldx, W, K, N);
+    const bool ok4 = mcq4::gemm4_supported(X, ldx, W, K, N);
     if (const char *env = getenv("MCQ4_GEMM_PATH")) {
-        if (env[0] == 's') return false;
-        if (env[0] == 'a') return true;
+        if (env[0] == 's') return Prefill::Sync;
+        if (env[0] == 'a' && ok2) return Prefill::Async2;
+        if (env[0] == '3' && ok2) return Prefill::Async3;
+        if (env[0] == '4' && ok4) return Prefill::Free4;
     }
-    return ((M + 127) / 128) * ((N + 255) / 256) >= 128;
+    if (ok4) return Prefill::Free4;
+    if (ok2 && ((M + 127) / 128) * ((N + 255) / 256) >= 128) return Prefill::Async2;
+    return Prefill::Sync;
 }
 
 int check_kn(int64_t K, int64_t N) {
@@ -163,12 +175,17 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
     if (M <= 64)
         e = mcq4::launch_skinny((const _Float16 *)X, ldx, W, (_Float16 *)Y, ldy, (int)M, (int)K,
                                 (int)N, workspace, (hipStream_t)stream);
-    else if (use_gemm2((const _Float16 *)X, ldx, W, M, K, N))
-        e = mcq4::launch_gemm2((const _Float16 *)X, ldx, W, (_Float16 *)Y, ldy, (int)M, (int)K,
-                               (int)N, (hipStream_t)stream);
-    else
-        e = mcq4::launch_gemm((const _Float16 *)X, ldx, W, (_Float16 *)Y, ldy, (int)M, (int)K,
-                              (int)N, workspace, (hipStream_t)stream);
+    else {
+        const _Float16 *x = (const _Float16 *)X;
+        _Float16 *y = (_Float16 *)Y;
+        hipStream_t st = (hipStream_t)stream;
+        switch (prefill_kernel(x, ldx, W, M, K, N)) {
+            case Prefill::Free4: e = mcq4::launch_gemm4(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;
+            case Prefill::Async3: e = mcq4::launch_gemm3(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;
+            case Prefill::Async2: e = mcq4::launch_gemm2(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;
+            default: e = mcq4::launch_gemm(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
+        }
+    }
     return hip_status(e, "matmul launch");
 }
 

@@ -128,6 +128,21 @@ __device__ __forceinline__ half8_t dequant8_perm(uint32_t w, uint32_t dbits) {
     return r;
 }
 
+// Eight nibbles (natural order e0..e7, byte i = e_{2i} | e_{2i+1} << 4) and the
+// fp16 bits of d -> eight fp16 weights (q-8)*d in natural order: 1024 + q
+// exactly via the 0x64 exponent byte, minus 1032 exactly, then one fp16
+// multiply (the single rounding of the exact product, as the reference's fp16
+// dequant).
+__device__ __forceinline__ half8_t dequant8_nat(uint32_t w, half2_t d2) {
+#pragma clang fp contract(off)
+    const uint4_t u = bitcast<uint4_t>(unpack8_1024_nat(w));
+    const half2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
+    uint4_t r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = bitcast<uint32_t>((bitcast<half2_t>(u[i]) - off) * d2);
+    return bitcast<half8_t>(r);
+}
+
 // Eight nibbles -> fp16 halves 1024 + q (exact) in the dequant8_perm slot order.
 // Used where the -8 offset and the scale d are applied after the MFMA.
 __device__ __forceinline__ half8_t unpack8_1024(uint32_t w) {

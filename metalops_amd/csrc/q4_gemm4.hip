@@ -1,0 +1,244 @@
+// Prefill-shaped q4_0 matmul (M > 64) on gfx950: barrier-free MFMA GEMM.
+//
+//   * WG = 256 threads = 4 waves in a 2x2 grid; WG tile BM x 256 (BM = 256 or
+//     128); wave tile (BM/2) x 128 of v_mfma_f32_32x32x16_f16 tiles, fp32
+//     accumulation.  K advances one q4_0 block (32) per step.
+//   * Every wave fetches everything it consumes itself, so waves never wait for
+//     each other and no workgroup barrier is needed:
+//       - activations: the wave's MFMA A operands (16 bytes per lane and
+//         operand) are loaded from global memory (L2-resident; the workgroup's
+//         two waves of a row half read the same lines) straight into registers,
+//         G4_P steps ahead, in a register ring of G4_P slots;
+//       - weights: the raw q4_0 bytes of the wave's 128 columns for one step
+//         (2304 contiguous bytes) are copied with three global_load_lds_dwordx4
+//         into a private LDS ring of G4_P + 1 slots, G4_P steps ahead.
+//   * B operand of lane l (column n = l%32 of a 32-column MFMA tile, K elements
+//     8*(l/32)..+8 of a 16-wide K half): the qs dword of those 8 elements and
+//     the column's scale d from the raw slot, unpacked in natural order to fp16
+//     1024+q, minus 1032 (exact) and times d (one rounding: the reference's fp16
+//     dequant value).  Step k+1's B operands are built while the MFMAs of step k
+//     run.
+//   * Per step a wave issues the same number of loads and copies (steps past the
+//     end are clamped to the last), so one explicit vmcnt wait per step covers
+//     the copies; the compiler's own waits cover the register loads.
+//   * Workgroup ids are remapped so each XCD works on a contiguous range of
+//     tiles.
+//
+// MFMA 32x32 output layout: lane l holds D[8*(r/4) + 4*(l/32) + r%4][l%32], r = 0..15.
+#include <algorithm>
+#include <atomic>
+
+#include "q4_common.h"
+
+namespace mcq4 {
+
+constexpr int G4_THREADS = 256;
+constexpr int G4_BN = 256;
+#ifndef MCQ4_G4_P
+#define MCQ4_G4_P 3
+#endif
+constexpr int G4_P = MCQ4_G4_P;                // steps in flight ahead of the MFMAs
+constexpr int G4_R = G4_P + 1;                 // raw ring slots per wave
+constexpr int G4_RAW_W = 18 * 128;             // raw bytes per wave and step (2304)
+constexpr int G4_RAW_SLOT = G4_RAW_W + 64;     // + read overhang
+
+struct Gemm4Args {
+    const _Float16 *X;
+    int64_t ldx;
+    const uint8_t *W;
+    _Float16 *Y;
+    int64_t ldy;
+    int M, nb, N;
+    int tiles_m, tiles_n;
+};
+
+template <int BM>
+__global__ void __launch_bounds__(G4_THREADS, 1)
+q4_gemm4_kernel(Gemm4Args a) {
+    constexpr int WM = BM / 2, WN = G4_BN / 2;
+    constexpr int TM = WM / 32, TN = WN / 32;
+    constexpr int A_LD = 2 * TM;                 // register loads per step
+    constexpr int GROUP = A_LD + 3;              // vector-memory instructions per step
+    static_assert((G4_P - 1) * GROUP < 64, "vmcnt range");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+
+    const int ntiles = a.tiles_m * a.tiles_n;
+    const int bid = blockIdx.x;
+    int tile_id = bid;
+    if (ntiles % 8 == 0) tile_id = (bid % 8) * (ntiles / 8) + bid / 8;
+    const int tm = tile_id % a.tiles_m;
+    const int tn = tile_id / a.tiles_m;
+    const int m0 = tm * BM, n0 = tn * G4_BN;
+    const int nk = a.nb;
+
+    const int lrow = lane & 31, lhi = lane >> 5;
+    // A operand (i, ks) of step k: row m0 + wm*WM + 32 i + lrow, halves 32k + 16ks + 8lhi.
+    const _Float16 *a_src[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        const int m = min(m0 + wm * WM + 32 * i + lrow, a.M - 1);
+        a_src[i] = a.X + (int64_t)m * a.ldx + 8 * lhi;
+    }
+    // Raw copies: chunk q = lane + 64 c (q < 144) of the wave's 2304-byte segment.
+    uint8_t *ring = smem + wave * (G4_R * G4_RAW_SLOT);
+    const int64_t row_bytes = (int64_t)a.N * BLOCK_BYTES;
+    const uint8_t *w_src = a.W + (int64_t)(n0 + wn * WN) * BLOCK_BYTES + 16 * lane;
+    const bool wcols = n0 + wn * WN < a.N;       // whole wave past N: copy column 0 instead
+    const uint8_t *w_base = wcols ? w_src : a.W + 16 * lane;
+
+    half8_t av[G4_P][2][TM];
+    auto load_a = [&](int k, half8_t (&dst)[2][TM]) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                dst[ks][i] = *(const half8_t *)(a_src[i] + (int64_t)k * QK + 16 * ks);
+    };
+    auto copy_raw = [&](int k) {
+        const uint8_t *src = w_base + (int64_t)k * row_bytes;
+        uint8_t *dst = ring + (k % G4_R) * G4_RAW_SLOT;
+#pragma unroll
+        for (int c = 0; c < 3; ++c)
+            if (c < 2 || lane < 16)
+                __builtin_amdgcn_global_load_lds(
+                    (void *)(src + 1024 * c),
+                    (__attribute__((address_space(3))) void *)(dst + 1024 * c), 16, 0, 0);
+    };
+
+    // B operand addresses within a raw slot (columns relative to the wave's 128).
+    const int qoff0 = 18 * lrow + 2 + 4 * lhi;   // + 18*32 j + 8 ks
+    const int q_al = qoff0 & ~3;
+    const uint32_t q_sh = (uint32_t)(qoff0 & 3) * 8;
+    const int d_off = 18 * lrow;
+    auto load_b = [&](int k, half8_t (&bv)[2][TN]) {
+        const lds_u8 *Rs = lds_ptr(lds_addr(ring + (k % G4_R) * G4_RAW_SLOT));
+        uint32_t qd[TN][4], dd[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const lds_u32 *qp = (const lds_u32 *)(Rs + q_al + j * 32 * 18);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) qd[j][t] = qp[t];
+            dd[j] = *(const lds_u16 *)(Rs + d_off + j * 32 * 18);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const half2_t d2 = bitcast<half2_t>(__builtin_amdgcn_perm(dd[j], dd[j], 0x01000100u));
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                bv[ks][j] = dequant8_nat(__builtin_amdgcn_alignbit(qd[j][2 * ks + 1], qd[j][2 * ks], q_sh), d2);
+        }
+    };
+
+    float16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // ---- prologue: steps 0..P-1 in flight (A then raw per step), step 0's B built.
+#pragma unroll
+    for (int p = 0; p < G4_P; ++p) {
+        const int kp = min(p, nk - 1);
+        load_a(kp, av[p]);
+        copy_raw(kp);
+    }
+    wait_vmcnt<(G4_P - 1) * GROUP>();             // step 0 (and everything older) landed
+    half8_t bcur[2][TN];
+    load_b(0, bcur);
+
+    // One step: MFMAs of step k (A ring slot S), B of step k+1 built meanwhile,
+    // then step k+P's loads into the freed slot S.
+    auto step = [&](int k, half8_t (&a_cur)[2][TM]) {
+        wait_vmcnt<(G4_P - 2) * GROUP>();         // step k+1's raw copies landed
+        half8_t bnxt[2][TN];
+        load_b(min(k + 1, nk - 1), bnxt);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[ks][i], bcur[ks][j],
+                                                                        acc[i][j], 0, 0, 0);
+        const int kn = min(k + G4_P, nk - 1);
+        load_a(kn, a_cur);
+        copy_raw(kn);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bcur[ks][j] = bnxt[ks][j];
+    };
+
+    int k = 0;
+    for (; k + G4_P <= nk; k += G4_P) {
+#pragma unroll
+        for (int u = 0; u < G4_P; ++u) step(k + u, av[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < G4_P; ++u)
+        if (k + u < nk) step(k + u, av[u]);
+    wait_vmcnt<0>();
+
+    // ---- epilogue ----------------------------------------------------------------
+    const int rsub = 4 * lhi;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int n = n0 + wn * WN + j * 32 + lrow;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
+                if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (_Float16)acc[i][j][r];
+            }
+        }
+}
+
+template <int BM>
+static hipError_t launch_g4(const Gemm4Args &a, hipStream_t s) {
+    constexpr size_t lds = (size_t)4 * G4_R * G4_RAW_SLOT;
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(done.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void *)q4_gemm4_kernel<BM>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        done.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    hipLaunchKernelGGL((q4_gemm4_kernel<BM>), dim3(a.tiles_m * a.tiles_n), dim3(G4_THREADS), lds,
+                       s, a);
+    return hipGetLastError();
+}
+
+// Needs N % 128 == 0 (every wave's 128 columns are whole, 16-byte aligned raw
+// segments), a 16-byte aligned weight base, and 16-byte aligned activation rows.
+bool gemm4_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N) {
+    return N % 128 == 0 && ((uintptr_t)W % 16) == 0 && ((uintptr_t)X % 16) == 0 && ldx % 8 == 0 &&
+           K >= QK;
+}
+
+hipError_t launch_gemm4(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, hipStream_t s) {
+    Gemm4Args a;
+    a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
+    a.M = M; a.nb = K / QK; a.N = N;
+    a.tiles_n = (N + G4_BN - 1) / G4_BN;
+    int bm = 256;
+    if (((int64_t)(M + 255) / 256) * a.tiles_n < 192) bm = 128;
+    if (const char *env = getenv("MCQ4_GEMM2_BM")) bm = atoi(env) == 128 ? 128 : 256;
+    a.tiles_m = (M + bm - 1) / bm;
+    if (bm == 256) return launch_g4<256>(a, s);
+    return launch_g4<128>(a, s);
+}
+
+}  // namespace mcq4

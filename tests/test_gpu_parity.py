@@ -186,6 +186,10 @@ PATHS = {
     "gemm_sync": {"MCQ4_GEMM_PATH": "sync"},
     "gemm_async_bm256": {"MCQ4_GEMM_PATH": "async", "MCQ4_GEMM2_BM": "256"},
     "gemm_async_bm128": {"MCQ4_GEMM_PATH": "async", "MCQ4_GEMM2_BM": "128"},
+    "gemm3_bm256": {"MCQ4_GEMM_PATH": "3", "MCQ4_GEMM2_BM": "256"},
+    "gemm3_bm128": {"MCQ4_GEMM_PATH": "3", "MCQ4_GEMM2_BM": "128"},
+    "gemm4_bm256": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM2_BM": "256"},
+    "gemm4_bm128": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM2_BM": "128"},
 }
 PATH_SHAPES = {
     "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
@@ -198,6 +202,11 @@ PATH_SHAPES = {
     "gemm_sync": [(65, 352, 70), (200, 1024, 264), (300, 2048, 520)],
     "gemm_async_bm256": [(65, 352, 72), (257, 1024, 264), (300, 2048, 520), (512, 4096, 776)],
     "gemm_async_bm128": [(65, 352, 72), (129, 1024, 264), (300, 2048, 520), (384, 4096, 776)],
+    "gemm3_bm256": [(65, 352, 72), (257, 1024, 264), (300, 2048, 520), (512, 4096, 776), (2048, 4096, 1024)],
+    "gemm3_bm128": [(65, 352, 72), (129, 1024, 264), (300, 2048, 520), (384, 4096, 776)],
+    "gemm4_bm256": [(65, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
+                    (100, 32, 256), (70, 64, 384)],
+    "gemm4_bm128": [(65, 352, 128), (129, 1024, 384), (300, 2048, 512), (384, 4096, 896), (100, 96, 256)],
 }
 
 
