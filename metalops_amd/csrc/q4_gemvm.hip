@@ -1,0 +1,258 @@
+// Small-batch (2 <= M <= 16) q4_0 GEMV/GEMM on gfx950: the M = 1 kernel's
+// structure (q4_gemv.hip) with a 16-row MFMA A operand.
+//
+//   * Column tile = 16 columns; item = one tile's batch of 8 K blocks (2304 bytes
+//     of strip rows), copied with three global_load_lds_dwordx4 into a 2-slot
+//     per-wave LDS ring; item k+1 is issued before the wave waits for item k.
+//   * Workgroup = WAVES waves owning TPW tiles (XCD-renumbered); wave w owns
+//     batches w, w+WAVES, ... of every tile, walked batch-major.
+//   * Activations: lane (r = l%16, g = l/16) holds row min(r, M-1) (rows >= M
+//     only feed output rows that are never stored), elements 8g..8g+7 of each of
+//     the batch's 8 K blocks, loaded from global memory into registers right
+//     before the batch's first weight copy is issued (so the in-order vmcnt never
+//     makes a weight wait stall behind them), then rearranged to
+//     x' = [x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16].
+//   * Per K block row: B = [1024+q0, 1024+q4, 1024+16q1, ...] from four
+//     v_and_or_b32, and mfma(x', B, -S) with -S = mfma(x', -C) of that row
+//     (C = [1032, 1032, 1152, 1152, ...]) gives sum x*(q-8) for the lane's four
+//     output rows 4g..4g+3 of column r; acc += d * that in fp32.
+//   * Epilogue: per-wave partials through LDS, summed over waves in order
+//     (deterministic), stored as fp16 for rows < M.
+#include <algorithm>
+#include <atomic>
+
+#include "q4_common.h"
+
+namespace mcq4 {
+
+constexpr int GM_B = 8;                      // K blocks per item
+constexpr int GM_ROW = 288;                  // strip bytes per K block (16 columns)
+constexpr int GM_WCH = GM_B * 18;            // 144 strip chunks per item
+constexpr int GM_SLOT = GM_WCH * 16 + 64;    // + read overhang
+constexpr int GM_TPW_MAX = 4;
+constexpr int GM_NT = 2;                     // cache policy of the weight copies: non-temporal
+
+struct GemvMArgs {
+    const _Float16 *X;
+    int64_t ldx;
+    const uint8_t *W;
+    _Float16 *Y;
+    int64_t ldy;
+    int M, nb, N, ntiles, nbt;
+};
+
+template <int WAVES, int TPW>
+__global__ void __launch_bounds__(WAVES * 64)
+q4_gemvm_kernel(GemvMArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const uint32_t grow = (uint32_t)a.N * BLOCK_BYTES;
+
+    // LDS: [WAVES x 2 slots][partials: TPW x WAVES x 16 rows x 16 columns]
+    uint8_t *ring = smem + wave * (2 * GM_SLOT);
+    float *red = (float *)(smem + WAVES * 2 * GM_SLOT);
+
+    const int G = (int)gridDim.x, G8 = G & ~7;
+    int wg = (int)blockIdx.x;
+    if (wg < G8) wg = (wg & 7) * (G8 >> 3) + (wg >> 3);
+    const int ntl = min(TPW, (a.ntiles - wg + G - 1) / G);
+    const int nbm = a.nbt > wave ? (a.nbt - wave + WAVES - 1) / WAVES : 0;
+    const int nmine = nbm * ntl;
+
+    int crow[3];
+    uint32_t coff[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int q = lane + 64 * i;
+        crow[i] = q < GM_WCH ? q / 18 : 0;
+        coff[i] = q < GM_WCH ? (uint32_t)(q / 18) * grow + 16u * (uint32_t)(q % 18) : 0u;
+    }
+    const uint8_t *xrow = (const uint8_t *)a.X + (int64_t)min(c, a.M - 1) * a.ldx * 2 + 16 * g;
+    uint4_t xr[GM_B];
+    auto load_x = [&](int m) {
+        const int row0 = (wave + WAVES * m) * GM_B;
+#pragma unroll
+        for (int u = 0; u < GM_B; ++u)
+            xr[u] = *(const uint4_t *)(xrow + (int64_t)min(row0 + u, a.nb - 1) * (QK * 2));
+    };
+    auto copy_item = [&](int m, int j, int slot) {
+        const int row0 = (wave + WAVES * m) * GM_B;
+        const int rows = min(GM_B, a.nb - row0);
+        const uint8_t *wb = a.W + (int64_t)(wg + j * G) * GM_ROW + (int64_t)row0 * grow;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const uint32_t off = crow[i] < rows ? coff[i] : coff[i] - (uint32_t)crow[i] * grow;
+            if (i < 2 || lane < GM_WCH - 128)
+                __builtin_amdgcn_global_load_lds(
+                    (void *)(wb + off),
+                    (__attribute__((address_space(3))) void *)(ring + slot * GM_SLOT + 1024 * i),
+                    16, 0, GM_NT);
+        }
+    };
+    // Issue cursor: a batch's activation loads go right before its first copy.
+    int im = 0, ij = 0, islot = 0;
+    auto issue_next = [&]() {
+        if (ij == 0) load_x(im);
+        copy_item(im, ij, islot);
+        islot ^= 1;
+        if (++ij == ntl) { ij = 0; ++im; }
+    };
+    if (nmine > 0) issue_next();
+
+    const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
+    const uint32_t qal = (uint32_t)(qoff & ~3), qsh = (uint32_t)(qoff & 3) * 8;
+    const uint32_t doff = (uint32_t)(c * BLOCK_BYTES);
+    const uint32_t c64 = opaque_vgpr(0x64006400u);
+    const uint32_t mlo = opaque_sgpr(0x000F000Fu), mhi = opaque_sgpr(0x00F000F0u);
+    const uint32_t nlo = 0xE408E408u, nhi = 0xE480E480u;     // -1032, -1152 pairs
+    const half8_t negc = bitcast<half8_t>(uint4_t{nlo, nhi, nlo, nhi});
+    const float4_t z = {0.f, 0.f, 0.f, 0.f};
+    const half2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+
+    float4_t acc[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) acc[j] = z;
+
+    int k = 0, slot = 0;
+    for (int m = 0; m < nbm; ++m) {
+        const int rows = min(GM_B, a.nb - (wave + WAVES * m) * GM_B);
+        half8_t xq[GM_B];
+#pragma unroll
+        for (int u = 0; u < GM_B; ++u) {
+            const uint4_t x = xr[u];
+            const uint32_t h15 = __builtin_amdgcn_perm(x[2], x[0], 0x07060302u);   // x1, x5
+            const uint32_t h37 = __builtin_amdgcn_perm(x[3], x[1], 0x07060302u);   // x3, x7
+            const uint4_t v = {__builtin_amdgcn_perm(x[2], x[0], 0x05040100u),     // x0, x4
+                               bitcast<uint32_t>(bitcast<half2_t>(h15) * s16),
+                               __builtin_amdgcn_perm(x[3], x[1], 0x05040100u),     // x2, x6
+                               bitcast<uint32_t>(bitcast<half2_t>(h37) * s16)};
+            xq[u] = bitcast<half8_t>(v);
+        }
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) {
+            if (j < ntl) {
+                // Younger than item k after this issue: the next item's 3 copies,
+                // plus its batch's 8 activation loads when it starts a batch.
+                const bool more = k + 1 < nmine;
+                const bool xnext = more && ij == 0;
+                if (more) issue_next();
+                if (!more) wait_vmcnt<0>();
+                else if (xnext) wait_vmcnt<GM_B + 3>();
+                else wait_vmcnt<3>();
+                const uint32_t base = lds_addr(ring + slot * GM_SLOT);
+                const uint32_t qa = base + qal, da = base + doff;
+                auto row = [&](int u) {
+                    const lds_u32 *qp = (const lds_u32 *)(lds_ptr(qa) + u * GM_ROW);
+                    const uint32_t q0 = qp[0], q1 = qp[1];
+                    const uint32_t w = __builtin_amdgcn_alignbit(q1, q0, qsh);
+                    const uint32_t w8 = __builtin_amdgcn_alignbit(q1, q0, qsh + 8);
+                    const float d = (float)bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(da) + u * GM_ROW));
+                    const uint4_t bq = {and_or(w, mlo, c64), and_or(w, mhi, c64),
+                                        and_or(w8, mlo, c64), and_or(w8, mhi, c64)};
+                    // -S of this row, recomputed per item: keeps 32 VGPRs free so a
+                    // 16-wave workgroup fits in 128 VGPRs (the MFMA pipe has room).
+                    const float4_t ns = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], negc, z, 0, 0, 0);
+                    const float4_t blk =
+                        __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], bitcast<half8_t>(bq), ns, 0, 0, 0);
+                    acc[j] += d * blk;
+                };
+                if (rows == GM_B) {
+#pragma unroll
+                    for (int u = 0; u < GM_B; ++u) row(u);
+                } else {
+#pragma unroll
+                    for (int u = 0; u < GM_B; ++u)
+                        if (u < rows) row(u);
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                slot ^= 1;
+                ++k;
+            }
+        }
+    }
+
+    // Partials: lane (c, g) holds rows 4g..4g+3 of column c.
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+        if (j < ntl) {
+            float *rp = red + ((j * WAVES + wave) * 16 + 4 * g) * 16 + c;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) rp[16 * i] = nbm > 0 ? acc[j][i] : 0.f;
+        }
+    __syncthreads();
+    for (int v = tid; v < ntl * 256; v += WAVES * 64) {
+        const int j = v >> 8, rr = (v >> 4) & 15, col = v & 15;
+        if (rr >= a.M) continue;
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) s += red[((j * WAVES + w) * 16 + rr) * 16 + col];
+        a.Y[(int64_t)rr * a.ldy + (wg + j * G) * 16 + col] = (_Float16)s;
+    }
+}
+
+static size_t gemvm_lds_bytes(int waves, int tpw) {
+    return (size_t)waves * 2 * GM_SLOT + (size_t)tpw * waves * 256 * sizeof(float);
+}
+
+template <int WAVES, int TPW>
+static hipError_t launch_gemvm_t(const GemvMArgs &a, int grid, hipStream_t s) {
+    const size_t lds = gemvm_lds_bytes(WAVES, TPW);
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(done.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void *)q4_gemvm_kernel<WAVES, TPW>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        done.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    hipLaunchKernelGGL((q4_gemvm_kernel<WAVES, TPW>), dim3(grid), dim3(WAVES * 64), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int WAVES>
+static hipError_t launch_gemvm_w(const GemvMArgs &a, int grid, int tpw, hipStream_t s) {
+    switch (tpw) {
+        case 1: return launch_gemvm_t<WAVES, 1>(a, grid, s);
+        case 2: return launch_gemvm_t<WAVES, 2>(a, grid, s);
+        case 3: return launch_gemvm_t<WAVES, 3>(a, grid, s);
+        default: return launch_gemvm_t<WAVES, 4>(a, grid, s);
+    }
+}
+
+// 2 <= M <= 16, 16-byte aligned weights and activation rows, N % 8 == 0, at
+// least one 16-column tile and at most 4 tiles per workgroup on a
+// 512-workgroup grid (N <= 32768).
+bool gemvm_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
+                     int64_t N) {
+    if (const char *env = getenv("MCQ4_GEMV_PATH"))
+        if (env[0] == 'o') return false;
+    return M >= 2 && M <= 16 && N % 8 == 0 && N >= 16 && N / 16 <= 512 * GM_TPW_MAX &&
+           ((uintptr_t)W % 16) == 0 && ((uintptr_t)X % 16) == 0 && ldx % 8 == 0 && K >= QK &&
+           N * 18 * 8 < ((int64_t)1 << 31);
+}
+
+hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, int *n_done, hipStream_t s) {
+    GemvMArgs a;
+    a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
+    a.M = M; a.nb = K / QK; a.N = N;
+    a.ntiles = N / 16;
+    a.nbt = (a.nb + GM_B - 1) / GM_B;
+    *n_done = a.ntiles * 16;
+    // 16-wave workgroups, one per CU (8-wave ones, two per CU, as an option).
+    int waves = 16;
+    if (const char *env = getenv("MCQ4_GEMVM_WAVES")) waves = atoi(env) == 8 ? 8 : 16;
+    const int cap = waves == 8 ? 512 : 256;
+    const int tpw = std::min(GM_TPW_MAX, (a.ntiles + cap - 1) / cap);
+    const int grid = (a.ntiles + tpw - 1) / tpw;
+    if (waves == 16) return launch_gemvm_w<16>(a, grid, tpw, s);
+    return launch_gemvm_w<8>(a, grid, tpw, s);
+}
+
+}  // namespace mcq4

@@ -280,6 +280,11 @@ bool gemv_dma_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t 
 hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int K, int N,
                            int *n_done, hipStream_t s);
 
+bool gemvm_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
+                     int64_t N);
+hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, int *n_done, hipStream_t s);
+
 static bool use_decode_lds(const uint8_t *W, int64_t N, int64_t ldx) {
     if (const char *env = getenv("MCQ4_DECODE_PATH"))  // "direct" forces this file's kernel
         if (env[0] == 'd') return false;
@@ -290,9 +295,13 @@ hipError_t launch_skinny(const _Float16 *X, int64_t ldx, const uint8_t *W, _Floa
                          int64_t ldy, int M, int K, int N, void *ws, hipStream_t s) {
     int n_begin = 0;
     if (use_decode_lds(W, N, ldx) && skinny_config(M, K, N).S == 1) {
-        hipError_t e = (M == 1 && gemv_dma_supported(X, W, K, N))
-                           ? launch_gemv_dma(X, W, Y, K, N, &n_begin, s)
-                           : launch_decode_lds(X, ldx, W, Y, ldy, M, K, N, &n_begin, s);
+        hipError_t e;
+        if (M == 1 && gemv_dma_supported(X, W, K, N))
+            e = launch_gemv_dma(X, W, Y, K, N, &n_begin, s);
+        else if (gemvm_supported(X, ldx, W, M, K, N))
+            e = launch_gemvm(X, ldx, W, Y, ldy, M, K, N, &n_begin, s);
+        else
+            e = launch_decode_lds(X, ldx, W, Y, ldy, M, K, N, &n_begin, s);
         if (e != hipSuccess || n_begin == N) return e;
     }
     const SkinnyCfg c = skinny_config(M, K, N);

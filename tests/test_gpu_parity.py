@@ -181,7 +181,10 @@ PATHS = {
     "gemv_dma_ring1": {"MCQ4_GEMV_RING": "1"},
     "gemv_dma_ring3": {"MCQ4_GEMV_RING": "3"},
     "decode_lds_m1": {"MCQ4_GEMV_PATH": "off"},
+    "gemvm": {},
+    "gemvm_w8": {"MCQ4_GEMVM_WAVES": "8"},
     "decode_lds": {},
+    "decode_lds_small_m": {"MCQ4_GEMV_PATH": "off"},
     "decode_direct": {"MCQ4_DECODE_PATH": "direct"},
     "gemm_sync": {"MCQ4_GEMM_PATH": "sync"},
     "gemm_async_bm256": {"MCQ4_GEMM_PATH": "async", "MCQ4_GEMM2_BM": "256"},
@@ -197,7 +200,11 @@ PATH_SHAPES = {
     "gemv_dma_ring1": [(1, 352, 264), (1, 2048, 1040)],
     "gemv_dma_ring3": [(1, 352, 264), (1, 11008, 4096), (1, 4096, 12288)],
     "decode_lds_m1": [(1, 352, 264), (1, 4096, 1032)],
-    "decode_lds": [(1, 352, 264), (3, 1024, 520), (16, 4096, 1032), (40, 2048, 96), (64, 256, 64)],
+    "gemvm": [(2, 32, 16), (3, 352, 264), (4, 1024, 4104), (5, 11008, 512), (8, 4096, 14336),
+              (11, 2048, 1040), (16, 14336, 4096), (16, 352, 8200)],
+    "gemvm_w8": [(2, 352, 264), (7, 4096, 1040), (16, 11008, 512)],
+    "decode_lds": [(1, 352, 264), (40, 2048, 96), (64, 256, 64), (17, 1024, 520), (33, 4096, 1032)],
+    "decode_lds_small_m": [(3, 1024, 520), (16, 4096, 1032)],
     "decode_direct": [(1, 352, 257), (7, 1024, 520), (16, 4096, 1000), (64, 512, 72)],
     "gemm_sync": [(65, 352, 70), (200, 1024, 264), (300, 2048, 520)],
     "gemm_async_bm256": [(65, 352, 72), (257, 1024, 264), (300, 2048, 520), (512, 4096, 776)],
@@ -213,7 +220,7 @@ PATH_SHAPES = {
 @pytest.mark.parametrize("path,M,K,N", [(p, *s) for p, shapes in PATH_SHAPES.items() for s in shapes])
 def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM", "MCQ4_GEMV_PATH",
-              "MCQ4_GEMV_RING"):
+              "MCQ4_GEMV_RING", "MCQ4_GEMVM_WAVES"):
         monkeypatch.delenv(k, raising=False)
     for k, v in PATHS[path].items():
         monkeypatch.setenv(k, v)
