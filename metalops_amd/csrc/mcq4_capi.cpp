@@ -7,6 +7,8 @@
 // (core_mps.mm:5923-5938) become status codes, the Metal encode on the current
 // MPS stream (core_mps.mm:5947-5969) becomes a launch on the given HIP stream.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -29,8 +31,9 @@ hipError_t launch_gemm2(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
 hipError_t launch_gemm3(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, hipStream_t s);
 bool gemm4_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
+size_t gemm4_workspace_bytes(int64_t M, int64_t K, int64_t N);
 hipError_t launch_gemm4(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
-                        int64_t ldy, int M, int K, int N, hipStream_t s);
+                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
 }  // namespace mcq4
 
 namespace {
@@ -148,7 +151,8 @@ int mcq4_dequantize_q4_0(const uint8_t *blocks, int64_t K, int64_t N, void *out,
 size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M <= 0 || K <= 0 || N <= 0 || K % 32) return 0;
     if (M <= 64) return mcq4::skinny_workspace_bytes(M, K, N);
-    return mcq4::gemm_workspace_bytes(M, K, N);  // an upper bound for either prefill kernel
+    // The larger of the two split-K kernels' needs: an upper bound for any prefill kernel.
+    return std::max(mcq4::gemm_workspace_bytes(M, K, N), mcq4::gemm4_workspace_bytes(M, K, N));
 }
 
 int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, int64_t ldy,
@@ -180,7 +184,7 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
         _Float16 *y = (_Float16 *)Y;
         hipStream_t st = (hipStream_t)stream;
         switch (prefill_kernel(x, ldx, W, M, K, N)) {
-            case Prefill::Free4: e = mcq4::launch_gemm4(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;
+            case Prefill::Free4: e = mcq4::launch_gemm4(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
             case Prefill::Async3: e = mcq4::launch_gemm3(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;
             case Prefill::Async2: e = mcq4::launch_gemm2(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;
             default: e = mcq4::launch_gemm(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;

@@ -23,6 +23,10 @@
 //     the copies; the compiler's own waits cover the register loads.
 //   * Workgroup ids are remapped so each XCD works on a contiguous range of
 //     tiles.
+//   * Outputs with few tiles split K over grid.z: each split writes an fp32
+//     partial tile to the caller's workspace, and a second small kernel on the
+//     same stream sums the partials in split order and writes fp16 (the kernel
+//     boundary orders the two; no fences or atomics).
 //
 // MFMA 32x32 output layout: lane l holds D[8*(r/4) + 4*(l/32) + r%4][l%32], r = 0..15.
 #include <algorithm>
@@ -50,6 +54,8 @@ struct Gemm4Args {
     int64_t ldy;
     int M, nb, N;
     int tiles_m, tiles_n;
+    int S;               // K splits (grid.z)
+    float *partials;     // [tiles][S][BM*256] when S > 1
 };
 
 template <int BM>
@@ -74,7 +80,10 @@ q4_gemm4_kernel(Gemm4Args a) {
     const int tm = tile_id % a.tiles_m;
     const int tn = tile_id / a.tiles_m;
     const int m0 = tm * BM, n0 = tn * G4_BN;
-    const int nk = a.nb;
+    // K range of this split: steps [k_lo, k_lo + nk).
+    const int z = (int)blockIdx.z;
+    const int k_lo = (int)((int64_t)a.nb * z / a.S);
+    const int nk = (int)((int64_t)a.nb * (z + 1) / a.S) - k_lo;
 
     const int lrow = lane & 31, lhi = lane >> 5;
     // A operand (i, ks) of step k: row m0 + wm*WM + 32 i + lrow, halves 32k + 16ks + 8lhi.
@@ -82,14 +91,15 @@ q4_gemm4_kernel(Gemm4Args a) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
         const int m = min(m0 + wm * WM + 32 * i + lrow, a.M - 1);
-        a_src[i] = a.X + (int64_t)m * a.ldx + 8 * lhi;
+        a_src[i] = a.X + (int64_t)m * a.ldx + (int64_t)k_lo * QK + 8 * lhi;
     }
     // Raw copies: chunk q = lane + 64 c (q < 144) of the wave's 2304-byte segment.
     uint8_t *ring = smem + wave * (G4_R * G4_RAW_SLOT);
     const int64_t row_bytes = (int64_t)a.N * BLOCK_BYTES;
-    const uint8_t *w_src = a.W + (int64_t)(n0 + wn * WN) * BLOCK_BYTES + 16 * lane;
+    const uint8_t *w_k = a.W + (int64_t)k_lo * row_bytes;
+    const uint8_t *w_src = w_k + (int64_t)(n0 + wn * WN) * BLOCK_BYTES + 16 * lane;
     const bool wcols = n0 + wn * WN < a.N;       // whole wave past N: copy column 0 instead
-    const uint8_t *w_base = wcols ? w_src : a.W + 16 * lane;
+    const uint8_t *w_base = wcols ? w_src : w_k + 16 * lane;
 
     half8_t av[G4_P][2][TM];
     auto load_a = [&](int k, half8_t (&dst)[2][TM]) {
@@ -188,17 +198,56 @@ q4_gemm4_kernel(Gemm4Args a) {
 
     // ---- epilogue ----------------------------------------------------------------
     const int rsub = 4 * lhi;
+    if (a.S == 1) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int n = n0 + wn * WN + j * 32 + lrow;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
+                    if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (_Float16)acc[i][j][r];
+                }
+            }
+        return;
+    }
+    // Split-K: this split's fp32 partial tile (dense BM x 256, row-major); the
+    // reduction kernel launched right after sums the splits in order.
+    float *part = a.partials + ((int64_t)tile_id * a.S + z) * (BM * G4_BN);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int n = n0 + wn * WN + j * 32 + lrow;
+            const int nl = wn * WN + j * 32 + lrow;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
-                if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (_Float16)acc[i][j][r];
+                const int ml = wm * WM + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
+                part[ml * G4_BN + nl] = acc[i][j][r];
             }
         }
+}
+
+// Sums the S fp32 partial tiles of every output tile in split order
+// (deterministic) and stores fp16; four consecutive columns per thread.
+template <int BM>
+__global__ void __launch_bounds__(256)
+q4_gemm4_reduce_kernel(Gemm4Args a) {
+    constexpr int TILE = BM * G4_BN;
+    const int64_t v4 = (int64_t)blockIdx.x * 256 + threadIdx.x;     // float4 index
+    const int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n;
+    if (v4 >= ntiles * (TILE / 4)) return;
+    const int64_t tile = v4 / (TILE / 4);
+    const int e = (int)(v4 % (TILE / 4)) * 4;
+    const int tm = (int)(tile % a.tiles_m), tn = (int)(tile / a.tiles_m);
+    const float4_t *p = (const float4_t *)(a.partials + tile * a.S * TILE + e);
+    float4_t sum = p[0];
+    for (int sp = 1; sp < a.S; ++sp) sum += p[(int64_t)sp * (TILE / 4)];
+    const int m = tm * BM + e / G4_BN, n = tn * G4_BN + e % G4_BN;
+    if (m >= a.M) return;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        if (n + c < a.N) a.Y[(int64_t)m * a.ldy + n + c] = (_Float16)sum[c];
 }
 
 template <int BM>
@@ -215,8 +264,13 @@ static hipError_t launch_g4(const Gemm4Args &a, hipStream_t s) {
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL((q4_gemm4_kernel<BM>), dim3(a.tiles_m * a.tiles_n), dim3(G4_THREADS), lds,
-                       s, a);
+    hipLaunchKernelGGL((q4_gemm4_kernel<BM>), dim3(a.tiles_m * a.tiles_n, 1, a.S), dim3(G4_THREADS),
+                       lds, s, a);
+    if (a.S > 1) {
+        const int64_t n4 = (int64_t)a.tiles_m * a.tiles_n * (BM * G4_BN / 4);
+        hipLaunchKernelGGL((q4_gemm4_reduce_kernel<BM>), dim3((unsigned)((n4 + 255) / 256)), dim3(256),
+                           0, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -227,17 +281,50 @@ bool gemm4_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K
            K >= QK;
 }
 
+struct G4Cfg {
+    int bm, S;
+};
+
+// Row-tile height and K splits: BM = 128 when 256-row tiles would leave fewer
+// than 192 tiles; K is split (powers of two, at least 16 steps per split) until
+// about 192 workgroups have work.
+static G4Cfg gemm4_config(int64_t M, int64_t K, int64_t N) {
+    const int64_t tn = (N + G4_BN - 1) / G4_BN;
+    G4Cfg c{256, 1};
+    if (((M + 255) / 256) * tn < 192) c.bm = 128;
+    if (const char *env = getenv("MCQ4_GEMM2_BM")) c.bm = atoi(env) == 128 ? 128 : 256;
+    const int64_t t = ((M + c.bm - 1) / c.bm) * tn;
+    const int64_t nb = K / QK;
+    while (t * c.S < 192 && nb / (c.S * 2) >= 16 && c.S < 16) c.S *= 2;
+    if (const char *env = getenv("MCQ4_GEMM4_SPLIT")) c.S = std::max(1, std::min(16, atoi(env)));
+    if (c.S > nb) c.S = 1;
+    return c;
+}
+
+size_t gemm4_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    const G4Cfg c = gemm4_config(M, K, N);
+    if (c.S == 1) return 0;
+    const int64_t t = ((M + c.bm - 1) / c.bm) * ((N + G4_BN - 1) / G4_BN);
+    // Partials follow the workspace's counter area, which stays untouched (zero)
+    // for the kernels that use it.
+    return COUNTER_BYTES + (size_t)t * c.S * c.bm * G4_BN * sizeof(float);
+}
+
 hipError_t launch_gemm4(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
-                        int64_t ldy, int M, int K, int N, hipStream_t s) {
+                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s) {
+    const G4Cfg c = gemm4_config(M, K, N);
     Gemm4Args a;
     a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
     a.M = M; a.nb = K / QK; a.N = N;
     a.tiles_n = (N + G4_BN - 1) / G4_BN;
-    int bm = 256;
-    if (((int64_t)(M + 255) / 256) * a.tiles_n < 192) bm = 128;
-    if (const char *env = getenv("MCQ4_GEMM2_BM")) bm = atoi(env) == 128 ? 128 : 256;
-    a.tiles_m = (M + bm - 1) / bm;
-    if (bm == 256) return launch_g4<256>(a, s);
+    a.tiles_m = (M + c.bm - 1) / c.bm;
+    a.S = c.S;
+    a.partials = nullptr;
+    if (c.S > 1) {
+        if (!ws) return hipErrorInvalidValue;
+        a.partials = (float *)((char *)ws + COUNTER_BYTES);
+    }
+    if (c.bm == 256) return launch_g4<256>(a, s);
     return launch_g4<128>(a, s);
 }
 

@@ -268,12 +268,11 @@ static hipError_t launch_gemv_r(const GemvArgs &a, int grid, int tpw, hipStream_
 
 // True when the M == 1 kernel applies: 16-byte aligned weights and
 // activations, 18*N a multiple of 16 (N % 8 == 0), at least one whole 16-column
-// tile, at most GV_TPW_MAX tiles per workgroup on a 256-workgroup grid
-// (N <= 16384) and at most GV_XB_MAX batches per wave (K <= 16384).
+// tile and at most GV_XB_MAX batches per wave (K <= 16384).
 bool gemv_dma_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t N) {
     if (const char *env = getenv("MCQ4_GEMV_PATH"))
         if (env[0] == 'o') return false;        // "off": use the batched decode kernel
-    return N % 8 == 0 && N >= 16 && N / 16 <= 256 * GV_TPW_MAX && ((uintptr_t)W % 16) == 0 &&
+    return N % 8 == 0 && N >= 16 && ((uintptr_t)W % 16) == 0 &&
            ((uintptr_t)X % 16) == 0 && K >= QK && K <= GV_WAVES * GV_XB_MAX * GV_B * QK &&
            N * 18 * 8 < ((int64_t)1 << 31);
 }
@@ -288,7 +287,10 @@ hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int
     a.ntiles = N / 16;
     a.nbt = (a.nb + GV_B - 1) / GV_B;
     *n_done = a.ntiles * 16;
-    const int grid = std::min(a.ntiles, 256);
+    // One 16-wave workgroup per CU and up to GV_TPW_MAX tiles each; larger N
+    // (lm_head) runs more workgroups of GV_TPW_MAX tiles, backfilled as CUs free up.
+    int grid = std::min(a.ntiles, 256);
+    if (a.ntiles > 256 * GV_TPW_MAX) grid = (a.ntiles + GV_TPW_MAX - 1) / GV_TPW_MAX;
     const int tpw = (a.ntiles + grid - 1) / grid;
     int ring = 2;
     if (const char *env = getenv("MCQ4_GEMV_RING")) ring = std::max(1, std::min(3, atoi(env)));
