@@ -81,11 +81,18 @@ def make_weights(mo, torch, K, N, seed, dev, outliers=False):
     return b
 
 
-def time_region(torch, stream, fn, steps, warmup):
-    """Run fn(i) warmup times, then time `steps` calls between HIP events on `stream`."""
+def time_region(torch, stream, fn, steps, warmup, min_warm_s=0.2):
+    """Run fn(i) at least `warmup` times and for at least `min_warm_s` seconds (the
+    GPU clocks ramp up after host-side setup), then time `steps` calls between HIP
+    events on `stream`."""
+    t_w = time.perf_counter()
+    i = 0
     with torch.cuda.stream(stream):
-        for i in range(warmup):
+        while i < warmup or time.perf_counter() - t_w < min_warm_s:
             fn(i)
+            i += 1
+            if i % 16 == 0:
+                torch.cuda.synchronize()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)

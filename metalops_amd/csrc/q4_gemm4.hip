@@ -36,7 +36,6 @@
 
 namespace mcq4 {
 
-constexpr int G4_THREADS = 256;
 constexpr int G4_BN = 256;
 #ifndef MCQ4_G4_P
 #define MCQ4_G4_P 3
@@ -58,10 +57,14 @@ struct Gemm4Args {
     float *partials;     // [tiles][S][BM*256] when S > 1
 };
 
-template <int BM>
-__global__ void __launch_bounds__(G4_THREADS, 1)
+template <int BM, int WGM>
+__global__ void __launch_bounds__(WGM * 128, 1)
 q4_gemm4_kernel(Gemm4Args a) {
-    constexpr int WM = BM / 2, WN = G4_BN / 2;
+    // WGM waves along M x 2 along N.  WGM = 2: one wave per SIMD, B operands
+    // double-buffered in registers.  WGM = 4: two waves per SIMD (<= 256
+    // registers each), B built just in time per 32-column tile.
+    constexpr bool JIT_B = WGM == 4;
+    constexpr int WM = BM / WGM, WN = G4_BN / 2;
     constexpr int TM = WM / 32, TN = WN / 32;
     constexpr int A_LD = 2 * TM;                 // register loads per step
     constexpr int GROUP = A_LD + 3;              // vector-memory instructions per step
@@ -71,7 +74,7 @@ q4_gemm4_kernel(Gemm4Args a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave >> 1, wn = wave & 1;     // wm < WGM
 
     const int ntiles = a.tiles_m * a.tiles_n;
     const int bid = blockIdx.x;
@@ -152,38 +155,66 @@ q4_gemm4_kernel(Gemm4Args a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    // ---- prologue: steps 0..P-1 in flight (A then raw per step), step 0's B built.
+    // ---- prologue: steps 0..P-1 in flight (A then raw per step) ----------------
 #pragma unroll
     for (int p = 0; p < G4_P; ++p) {
         const int kp = min(p, nk - 1);
         load_a(kp, av[p]);
         copy_raw(kp);
     }
-    wait_vmcnt<(G4_P - 1) * GROUP>();             // step 0 (and everything older) landed
     half8_t bcur[2][TN];
-    load_b(0, bcur);
+    if constexpr (!JIT_B) {
+        wait_vmcnt<(G4_P - 1) * GROUP>();         // step 0 (and everything older) landed
+        load_b(0, bcur);
+    }
 
-    // One step: MFMAs of step k (A ring slot S), B of step k+1 built meanwhile,
-    // then step k+P's loads into the freed slot S.
+    // One step: MFMAs of step k (A ring slot S), then step k+P's loads into the
+    // freed slot S.  Double-buffered B: step k+1's B is built during step k's
+    // MFMAs.  Just-in-time B: each 32-column tile's B is built right before its
+    // MFMAs (the other wave on the SIMD covers the latency).
     auto step = [&](int k, half8_t (&a_cur)[2][TM]) {
-        wait_vmcnt<(G4_P - 2) * GROUP>();         // step k+1's raw copies landed
-        half8_t bnxt[2][TN];
-        load_b(min(k + 1, nk - 1), bnxt);
+        if constexpr (JIT_B) {
+            wait_vmcnt<(G4_P - 1) * GROUP>();     // step k's raw copies landed
+            const lds_u8 *Rs = lds_ptr(lds_addr(ring + (k % G4_R) * G4_RAW_SLOT));
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+            for (int j = 0; j < TN; ++j) {
+                const lds_u32 *qp = (const lds_u32 *)(Rs + q_al + j * 32 * 18);
+                uint32_t qd[4];
 #pragma unroll
-            for (int i = 0; i < TM; ++i)
+                for (int t = 0; t < 4; ++t) qd[t] = qp[t];
+                const uint32_t dd = *(const lds_u16 *)(Rs + d_off + j * 32 * 18);
+                const half2_t d2 = bitcast<half2_t>(__builtin_amdgcn_perm(dd, dd, 0x01000100u));
+                half8_t bv[2];
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[ks][i], bcur[ks][j],
-                                                                        acc[i][j], 0, 0, 0);
+                for (int ks = 0; ks < 2; ++ks)
+                    bv[ks] = dequant8_nat(__builtin_amdgcn_alignbit(qd[2 * ks + 1], qd[2 * ks], q_sh), d2);
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[ks][i], bv[ks],
+                                                                            acc[i][j], 0, 0, 0);
+            }
+        } else {
+            wait_vmcnt<(G4_P - 2) * GROUP>();     // step k+1's raw copies landed
+            half8_t bnxt[2][TN];
+            load_b(min(k + 1, nk - 1), bnxt);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_cur[ks][i], bcur[ks][j],
+                                                                            acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) bcur[ks][j] = bnxt[ks][j];
+        }
         const int kn = min(k + G4_P, nk - 1);
         load_a(kn, a_cur);
         copy_raw(kn);
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int j = 0; j < TN; ++j) bcur[ks][j] = bnxt[ks][j];
     };
 
     int k = 0;
@@ -250,22 +281,22 @@ q4_gemm4_reduce_kernel(Gemm4Args a) {
         if (n + c < a.N) a.Y[(int64_t)m * a.ldy + n + c] = (_Float16)sum[c];
 }
 
-template <int BM>
+template <int BM, int WGM>
 static hipError_t launch_g4(const Gemm4Args &a, hipStream_t s) {
-    constexpr size_t lds = (size_t)4 * G4_R * G4_RAW_SLOT;
+    constexpr size_t lds = (size_t)(2 * WGM) * G4_R * G4_RAW_SLOT;
     static std::atomic<uint64_t> done{0};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)q4_gemm4_kernel<BM>,
+        e = hipFuncSetAttribute((const void *)q4_gemm4_kernel<BM, WGM>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL((q4_gemm4_kernel<BM>), dim3(a.tiles_m * a.tiles_n, 1, a.S), dim3(G4_THREADS),
-                       lds, s, a);
+    hipLaunchKernelGGL((q4_gemm4_kernel<BM, WGM>), dim3(a.tiles_m * a.tiles_n, 1, a.S),
+                       dim3(WGM * 128), lds, s, a);
     if (a.S > 1) {
         const int64_t n4 = (int64_t)a.tiles_m * a.tiles_n * (BM * G4_BN / 4);
         hipLaunchKernelGGL((q4_gemm4_reduce_kernel<BM>), dim3((unsigned)((n4 + 255) / 256)), dim3(256),
@@ -324,8 +355,10 @@ hipError_t launch_gemm4(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
         if (!ws) return hipErrorInvalidValue;
         a.partials = (float *)((char *)ws + COUNTER_BYTES);
     }
-    if (c.bm == 256) return launch_g4<256>(a, s);
-    return launch_g4<128>(a, s);
+    int wgm = 2;
+    if (const char *env = getenv("MCQ4_GEMM4_WGM")) wgm = atoi(env) == 4 ? 4 : 2;
+    if (c.bm == 256) return wgm == 4 ? launch_g4<256, 4>(a, s) : launch_g4<256, 2>(a, s);
+    return wgm == 4 ? launch_g4<128, 4>(a, s) : launch_g4<128, 2>(a, s);
 }
 
 }  // namespace mcq4

@@ -194,6 +194,8 @@ PATHS = {
     "gemm4_bm256": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM2_BM": "256"},
     "gemm4_bm128": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM2_BM": "128"},
     "gemm4_split3": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM4_SPLIT": "3"},
+    "gemm4_wgm4_bm256": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM4_WGM": "4", "MCQ4_GEMM2_BM": "256"},
+    "gemm4_wgm4_bm128": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM4_WGM": "4", "MCQ4_GEMM2_BM": "128"},
     "gemm4_split5_bm256": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM4_SPLIT": "5", "MCQ4_GEMM2_BM": "256"},
 }
 PATH_SHAPES = {
@@ -218,6 +220,8 @@ PATH_SHAPES = {
     "gemm4_bm128": [(65, 352, 128), (129, 1024, 384), (300, 2048, 512), (384, 4096, 896), (100, 96, 256),
                     (128, 4096, 4096), (512, 11008, 512)],
     "gemm4_split3": [(200, 352, 384), (129, 1024, 256), (300, 4096, 640)],
+    "gemm4_wgm4_bm256": [(65, 352, 128), (257, 1024, 384), (512, 4096, 768), (2048, 4096, 1024), (128, 4096, 512)],
+    "gemm4_wgm4_bm128": [(65, 352, 128), (300, 2048, 512), (384, 4096, 896), (512, 11008, 512)],
     "gemm4_split5_bm256": [(257, 352, 256), (100, 2048, 512)],
 }
 
@@ -225,7 +229,7 @@ PATH_SHAPES = {
 @pytest.mark.parametrize("path,M,K,N", [(p, *s) for p, shapes in PATH_SHAPES.items() for s in shapes])
 def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM", "MCQ4_GEMV_PATH",
-              "MCQ4_GEMV_RING", "MCQ4_GEMVM_WAVES", "MCQ4_GEMM4_SPLIT"):
+              "MCQ4_GEMV_RING", "MCQ4_GEMVM_WAVES", "MCQ4_GEMM4_SPLIT", "MCQ4_GEMM4_WGM"):
         monkeypatch.delenv(k, raising=False)
     for k, v in PATHS[path].items():
         monkeypatch.setenv(k, v)
