@@ -89,7 +89,7 @@ def time_region(torch, stream, fn, steps, warmup, min_warm_s=0.2):
     i = 0
     with torch.cuda.stream(stream):
         while i < warmup or time.perf_counter() - t_w < min_warm_s:
-            fn(i)
+            fn(i % max(1, steps))
             i += 1
             if i % 16 == 0:
                 torch.cuda.synchronize()
