@@ -36,7 +36,7 @@ typedef enum mcq4_status {
     MCQ4_ERR_HIP = 5           /* a HIP runtime call (launch) failed */
 } mcq4_status;
 
-enum { MCQ4_DTYPE_F32 = 0, MCQ4_DTYPE_F16 = 1 };
+enum { MCQ4_DTYPE_F32 = 0, MCQ4_DTYPE_F16 = 1, MCQ4_DTYPE_BF16 = 2 };
 
 /* Library version: major*10000 + minor*100 + patch. */
 int mcq4_version(void);
@@ -89,6 +89,74 @@ size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N);
 int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y,
                          int64_t ldy, int64_t M, int64_t K, int64_t N,
                          void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Per-group INT4 (metalcore quantization.py:26-239, Int4Linear :457-613).
+ *
+ * Format: packed[K/2][N] uint8, row k in byte row k/2 (even k low nibble, odd
+ * k high nibble); scales[G][N] and zeros[G][N] with G = ceil(K/group_size), in
+ * one float dtype (sz_dtype: MCQ4_DTYPE_F32 / F16 / BF16);
+ * W[k][n] = (q - zeros[k/group_size][n]) * scales[k/group_size][n].
+ * Rows are dense: packed row stride N bytes, scales/zeros row stride N.
+ * ------------------------------------------------------------------------- */
+
+/*
+ * quantize_int4 (quantization.py:26-92): per group and column
+ *   scale = (max - min)/15 clamped to >= 1e-8, zero = -min/scale,
+ *   q = round_half_even(w/scale + zero) clamped to [0, 15],
+ * every step rounded to w_dtype as the reference's torch ops on a weight of
+ * that dtype are.  W: [K][ldw] in w_dtype (ldw >= N); scales/zeros are written
+ * in w_dtype.  K must be even; group_size >= 1.
+ */
+int mcq4_quantize_int4(const void *W, int w_dtype, int64_t ldw, int64_t K, int64_t N,
+                       int64_t group_size, uint8_t *packed, void *scales, void *zeros,
+                       void *stream);
+
+/*
+ * dequantize_int4 (quantization.py:95-153): out[K][ldo] =
+ * ((float)q - zero) * scale in fp32 (zero and scale upcast exactly, two fp32
+ * roundings), then one rounding to out_dtype (F32 / F16 / BF16).
+ */
+int mcq4_dequantize_int4(const uint8_t *packed, const void *scales, const void *zeros,
+                         int sz_dtype, int64_t K, int64_t N, int64_t group_size, void *out,
+                         int64_t ldo, int out_dtype, void *stream);
+
+/* Workspace bytes the int4 matmul entry points need for this shape (0 = none);
+ * same conventions as mcq4_matmul_workspace_bytes (zero-filled counter area
+ * first, reusable, one workspace per stream). */
+size_t mcq4_matmul_int4_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
+                                        int x_dtype);
+
+/*
+ * matmul_int4 (quantization.py:156-239; Metal binding matmul_int4_metal,
+ * native/core_mps.mm:5612-5776): Y[M][ldy] = X[M][ldx] @ dequant(W) with
+ * fp32 accumulation; X and Y in x_dtype (F16, BF16 or F32).  fp16 activations
+ * with group_size % 32 == 0, K % 32 == 0 and N % 8 == 0 run the MFMA kernels
+ * (decode GEMV for M <= 16, prefill GEMM above); every other case runs a
+ * general fp32 kernel.  X needs x_dtype alignment (16 bytes and ldx % 8 == 0
+ * for the MFMA kernels; the general kernel is used otherwise), Y x_dtype
+ * alignment; ldx >= K, ldy >= N.
+ */
+int mcq4_matmul_int4(const void *X, int x_dtype, int64_t ldx, const uint8_t *packed,
+                     const void *scales, const void *zeros, int sz_dtype, void *Y, int64_t ldy,
+                     int64_t M, int64_t K, int64_t N, int64_t group_size, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
+/*
+ * matmul_int4_silu / matmul_int4_gelu (native/core_mps.mm:5780-5914, fused
+ * kernels native/quant_kernels.metal:884-1145): the same product with the
+ * activation applied to the fp32 result before the store, as the fused kernels
+ * do: silu(y) = y / (1 + exp(-y)) (:996-998);
+ * gelu(y) = y/2 * (1 + tanh(sqrt(2/pi) * (y + 0.044715 y^3))) (:1126-1132).
+ */
+int mcq4_matmul_int4_silu(const void *X, int x_dtype, int64_t ldx, const uint8_t *packed,
+                          const void *scales, const void *zeros, int sz_dtype, void *Y,
+                          int64_t ldy, int64_t M, int64_t K, int64_t N, int64_t group_size,
+                          void *workspace, size_t workspace_bytes, void *stream);
+int mcq4_matmul_int4_gelu(const void *X, int x_dtype, int64_t ldx, const uint8_t *packed,
+                          const void *scales, const void *zeros, int sz_dtype, void *Y,
+                          int64_t ldy, int64_t M, int64_t K, int64_t N, int64_t group_size,
+                          void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

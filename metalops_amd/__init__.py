@@ -1,9 +1,12 @@
-"""metalops_amd -- MI355X (gfx950) native GGML block_q4_0 INT4 matmul path.
+"""metalops_amd -- MI355X (gfx950) native INT4 matmul paths.
 
-Drop-in for metalcore's q4_0 API (reference ``metalcore/quantization.py:288-454``,
-re-exported by ``metalcore/__init__.py:39,182-184``): the same function names,
-argument order, tensor layout ``[K/32, N, 18]`` uint8 and error behaviour, backed
-by hand-written HIP kernels through the C ABI in ``include/mcq4.h``.
+Drop-in for metalcore's quantized-matmul API (reference
+``metalcore/quantization.py``, re-exported by ``metalcore/__init__.py:38-39``):
+the GGML block_q4_0 path (``quantization.py:288-454``, tensor layout
+``[K/32, N, 18]`` uint8) and the per-group INT4 path (``quantization.py:26-239``
+and ``Int4Linear`` :457-613, layout ``[K/2, N]`` uint8 + scales/zeros), with the
+same function names, argument order and error behaviour, backed by
+hand-written HIP kernels through the C ABI in ``include/mcq4.h``.
 """
 from .quantization import (
     BLOCK_Q4_0_SIZE,
@@ -13,8 +16,16 @@ from .quantization import (
     quantize_ggml_q4_0,
     quantize_ggml_q4_0_llama,
 )
+from .int4 import (
+    Int4Linear,
+    dequantize_int4,
+    matmul_int4,
+    matmul_int4_gelu,
+    matmul_int4_silu,
+    quantize_int4,
+)
 
-__version__ = "1.0.0"
+__version__ = "1.1.0"
 
 __all__ = [
     "QK4_0",
@@ -23,4 +34,10 @@ __all__ = [
     "quantize_ggml_q4_0_llama",
     "dequantize_ggml_q4_0",
     "matmul_ggml_q4_0",
+    "quantize_int4",
+    "dequantize_int4",
+    "matmul_int4",
+    "matmul_int4_silu",
+    "matmul_int4_gelu",
+    "Int4Linear",
 ]

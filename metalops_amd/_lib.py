@@ -19,6 +19,7 @@ MCQ4_ERR_WORKSPACE = 4
 MCQ4_ERR_HIP = 5
 MCQ4_DTYPE_F32 = 0
 MCQ4_DTYPE_F16 = 1
+MCQ4_DTYPE_BF16 = 2
 
 # Every symbol declared in include/mcq4.h with (restype, argtypes).
 _i64, _p, _int, _sz = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
@@ -31,6 +32,15 @@ SIGNATURES = {
     "mcq4_dequantize_q4_0": (_int, [_p, _i64, _i64, _p, _i64, _int, _p]),
     "mcq4_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "mcq4_matmul_q4_0_f16": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
+    "mcq4_quantize_int4": (_int, [_p, _int, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "mcq4_dequantize_int4": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _p, _i64, _int, _p]),
+    "mcq4_matmul_int4_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _int]),
+    "mcq4_matmul_int4": (_int, [_p, _int, _i64, _p, _p, _p, _int, _p, _i64, _i64, _i64, _i64,
+                                _i64, _p, _sz, _p]),
+    "mcq4_matmul_int4_silu": (_int, [_p, _int, _i64, _p, _p, _p, _int, _p, _i64, _i64, _i64,
+                                     _i64, _i64, _p, _sz, _p]),
+    "mcq4_matmul_int4_gelu": (_int, [_p, _int, _i64, _p, _p, _p, _int, _p, _i64, _i64, _i64,
+                                     _i64, _i64, _p, _sz, _p]),
 }
 
 

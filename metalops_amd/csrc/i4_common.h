@@ -1,0 +1,68 @@
+// Shared definitions for the gfx950 per-group INT4 kernels.
+//
+// Format (metalcore quantization.py:26-92): packed[K/2][N] uint8 with row k in
+// byte row k/2 (even k in the low nibble, odd k in the high nibble);
+// scales[G][N], zeros[G][N] (G = ceil(K/group)) in one float dtype;
+// W[k][n] = (q - zeros[k/group][n]) * scales[k/group][n].
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "q4_common.h"
+
+namespace mcq4 {
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// dtype codes of the C ABI (MCQ4_DTYPE_*)
+enum : int { DT_F32 = 0, DT_F16 = 1, DT_BF16 = 2 };
+// fused activations of the matmul store
+enum : int { ACT_NONE = 0, ACT_SILU = 1, ACT_GELU = 2 };
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+    return __uint_as_float((uint32_t)b << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Element i of a float array of dtype dt, upcast exactly to fp32.
+__device__ __forceinline__ float load_dt(const void *p, int64_t i, int dt) {
+    if (dt == DT_F32) return ((const float *)p)[i];
+    if (dt == DT_F16) return (float)((const _Float16 *)p)[i];
+    return bf16_bits_to_f32(((const uint16_t *)p)[i]);
+}
+
+// fp32 value rounded (nearest even) to dtype dt and returned as fp32.
+__device__ __forceinline__ float round_dt(float x, int dt) {
+    if (dt == DT_F32) return x;
+    if (dt == DT_F16) return (float)(_Float16)x;
+    return bf16_bits_to_f32(f32_to_bf16_bits(x));
+}
+
+__device__ __forceinline__ void store_dt(void *p, int64_t i, float v, int dt) {
+    if (dt == DT_F32) ((float *)p)[i] = v;
+    else if (dt == DT_F16) ((_Float16 *)p)[i] = (_Float16)v;
+    else ((uint16_t *)p)[i] = f32_to_bf16_bits(v);
+}
+
+// Fused activations of native/quant_kernels.metal: SiLU y / (1 + exp(-y))
+// (:996-998) and the tanh form of GELU (:1126-1132).
+template <int ACT>
+__device__ __forceinline__ float activate(float y) {
+    if constexpr (ACT == ACT_SILU) {
+        return y / (1.0f + expf(-y));
+    } else if constexpr (ACT == ACT_GELU) {
+        const float k0 = 0.7978845608028654f;   // sqrt(2/pi)
+        return 0.5f * y * (1.0f + tanhf(k0 * (y + 0.044715f * y * y * y)));
+    } else {
+        return y;
+    }
+}
+
+}  // namespace mcq4

@@ -1,0 +1,467 @@
+// Decode-shaped (M <= 16) per-group INT4 matmul on gfx950: MFMA GEMV.
+//
+// Y[M][N] = X[M][K] @ W with W[k][n] = (q - z) * s per (group, column),
+// packed[K/2][N] (byte row k/2, even k low nibble), fp16 activations, fp32
+// accumulation.  The kernel streams the 0.5 byte/weight nibble array once from
+// HBM, so its roofline is HBM bandwidth.
+//
+// Work decomposition
+//   * Tile = 16*NC columns (128 by default); step = 32 K rows (16 byte rows of
+//     the tile).  Workgroup (tile t, split sp) = IW waves; wave w owns the
+//     steps [(sp*IW + w)*spw, +spw).  Waves of a workgroup are summed through
+//     LDS in wave order; when K is split, splits are summed through the
+//     workspace by the last-arriving workgroup of the tile in split order
+//     (deterministic).
+//   * Lane (c = l%16, g = l/16): columns NC*c..NC*c+NC-1 of the tile, byte rows
+//     4g..4g+3 of the step (K elements 8g..8g+7), activation row min(c, M-1).
+//     Per step it loads four NC-byte weight rows and 16 bytes of activations
+//     into a register ring D steps ahead (loads past the range are clamped
+//     to the last step so every step issues the same five loads).
+//   * B operand of virtual MFMA column c (actual column NC*c + j for the j-th
+//     of the NC 16x16x32 MFMAs): per byte row r, one v_perm_b32 moves the byte
+//     of column NC*c+j and the same byte shifted right by 4 into bytes 0 and 2,
+//     one v_and_or_b32 keeps the two nibbles and adds the 0x64 exponent bytes:
+//     the fp16 pair {1024 + q(2r), 1024 + q(2r+1)}.  The activations are the
+//     natural MFMA A operand (row m = l%16, K elements 8g..8g+7).
+//   * Per group: P_j = sum x*(1024 + q) (MFMA chain), S = sum x (MFMA against
+//     ones); at the group's last step (or the range end)
+//       acc_j += s_j * (P_j - (1024 + z_j) * S)
+//     in fp32 -- i.e. sum x*(q - z)*s.  The group's scales and zeros (one row
+//     of the tile per group) are copied to LDS by global_load_lds before the
+//     first weight load, so they have landed once the first step's weights
+//     have; the flush reads them with ds_read after an explicit vmcnt wait that
+//     leaves only the ring's newer loads pending.
+//   * Store: act(sum) rounded to fp16.
+//
+// MFMA 16x16x32 f16 layout: A lane l = row l%16, K 8(l/16)..+8; B lane l =
+// column l%16, K 8(l/16)..+8; D lane l = rows 4(l/16)+i, column l%16.
+#include <algorithm>
+#include <stdlib.h>
+
+#include "i4_common.h"
+
+namespace mcq4 {
+
+// Two tile shapes (template NC = weight columns per lane):
+//   * NC = 8: 128-column tiles (128-byte row pieces), 4 waves per workgroup,
+//     K split over workgroups.  Default.
+//   * NC = 4: 64-column tiles, 16 waves per workgroup, the whole K range of a
+//     tile in one workgroup when the scale/zero slots allow.  Selectable.
+constexpr int I4V_LPS = 5;                // vector-memory loads per step
+constexpr int I4V_GMAX = 8;               // groups per wave held in LDS
+constexpr int I4V_SMAX = 16;              // K splits at most
+
+template <int NC>
+struct I4vShape {
+    static constexpr int IW = NC == 8 ? 4 : 16;                 // waves per workgroup
+    static constexpr int TC = 16 * NC;                          // tile columns
+    static constexpr int SLOT = TC * 4 * 2;                     // fp32 scales + zeros of a tile row
+    static constexpr int SZ_BYTES = IW * I4V_GMAX * SLOT;
+    static constexpr int RED_BYTES = IW * 16 * TC * 4;
+    static constexpr int LDS = SZ_BYTES > RED_BYTES ? SZ_BYTES : RED_BYTES;
+};
+
+struct I4GemvArgs {
+    const _Float16 *X;
+    int64_t ldx;
+    const uint8_t *P;
+    const void *scales, *zeros;
+    _Float16 *Y;
+    int64_t ldy;
+    int M, N, nsteps, spg;    // spg = steps per group (group_size / 32)
+    int spw, S;               // steps per wave, splits (grid.y)
+    float *part;              // [tiles][S][M][TC] when S > 1
+    uint32_t *counters;       // [tiles]
+};
+
+// Scales and zeros of the lane's NC columns (fp32 slot layout: TC scales then
+// TC zeros; 16-bit layouts: TC scales then TC zeros at half the size).
+template <int SZ, int NC>
+__device__ __forceinline__ void i4v_load_sz(const lds_u8 *slot, int c, float (&s)[NC],
+                                            float (&z)[NC]) {
+    constexpr int TC = 16 * NC;
+    if constexpr (SZ == DT_F32) {
+        typedef __attribute__((address_space(3))) float4_t lds_f4;
+        const lds_f4 *sp = (const lds_f4 *)(slot + 4 * NC * c);
+        const lds_f4 *zp = (const lds_f4 *)(slot + 4 * TC + 4 * NC * c);
+#pragma unroll
+        for (int h = 0; h < NC / 4; ++h) {
+            const float4_t sv = sp[h], zv = zp[h];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { s[4 * h + i] = sv[i]; z[4 * h + i] = zv[i]; }
+        }
+    } else {
+        uint32_t sv[NC / 2], zv[NC / 2];
+        if constexpr (NC == 8) {
+            const uint4_t a = *(const __attribute__((address_space(3))) uint4_t *)(slot + 2 * NC * c);
+            const uint4_t b = *(const __attribute__((address_space(3))) uint4_t *)(slot + 2 * TC + 2 * NC * c);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) { sv[i] = a[i]; zv[i] = b[i]; }
+        } else {
+            const u32x2 a = *(const __attribute__((address_space(3))) u32x2 *)(slot + 2 * NC * c);
+            const u32x2 b = *(const __attribute__((address_space(3))) u32x2 *)(slot + 2 * TC + 2 * NC * c);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) { sv[i] = a[i]; zv[i] = b[i]; }
+        }
+#pragma unroll
+        for (int i = 0; i < NC / 2; ++i) {
+            if constexpr (SZ == DT_F16) {
+                const half2_t sh = bitcast<half2_t>(sv[i]), zh = bitcast<half2_t>(zv[i]);
+                s[2 * i] = (float)sh[0]; s[2 * i + 1] = (float)sh[1];
+                z[2 * i] = (float)zh[0]; z[2 * i + 1] = (float)zh[1];
+            } else {
+                s[2 * i] = __uint_as_float(sv[i] << 16); s[2 * i + 1] = __uint_as_float(sv[i] & 0xFFFF0000u);
+                z[2 * i] = __uint_as_float(zv[i] << 16); z[2 * i + 1] = __uint_as_float(zv[i] & 0xFFFF0000u);
+            }
+        }
+    }
+}
+
+template <int NC> struct WRow;
+template <> struct WRow<8> { typedef u32x2 T; };
+template <> struct WRow<4> { typedef uint32_t T; };
+
+template <int SZ, int ACT, int D, int NC>
+__global__ void __launch_bounds__(I4vShape<NC>::IW * 64)
+i4_gemv_kernel(I4GemvArgs a) {
+    constexpr int IW = I4vShape<NC>::IW, TC = I4vShape<NC>::TC, SLOT = I4vShape<NC>::SLOT;
+    typedef typename WRow<NC>::T wrow_t;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[I4vShape<NC>::LDS];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    // Consecutive tiles (which share 128-byte lines when TC = 64) go to one XCD.
+    const int G = (int)gridDim.x, G8 = G & ~7;
+    int t = (int)blockIdx.x;
+    if (t < G8) t = (t & 7) * (G8 >> 3) + (t >> 3);
+    const int sp = (int)blockIdx.y;
+    const int N = a.N;
+    const int col0 = t * TC;
+
+    const int s_begin = (sp * IW + wave) * a.spw;
+    const int ns = max(0, min(a.spw, a.nsteps - s_begin));
+
+    float4_t acc[NC];
+#pragma unroll
+    for (int j = 0; j < NC; ++j) acc[j] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    if (ns > 0) {
+        // ---- scales / zeros of the wave's groups -> LDS (one copy per group) ----
+        const int g_first = s_begin / a.spg;
+        const int ngr = (s_begin + ns - 1) / a.spg - g_first + 1;     // <= I4V_GMAX by launch
+        uint8_t *szw = smem + wave * (I4V_GMAX * SLOT);
+        {
+            constexpr int esz = SZ == DT_F32 ? 4 : 2;
+            constexpr int per_lane = 16 / esz;                         // elements per lane copy
+            constexpr int lanes_per_row = TC / per_lane;
+            const bool is_z = lane >= lanes_per_row;
+            const int li = is_z ? lane - lanes_per_row : lane;
+            int col = col0 + li * per_lane;
+            if (col >= N) col = 0;                                     // valid, never read back
+            const uint8_t *src = (const uint8_t *)(is_z ? a.zeros : a.scales) + (int64_t)col * esz;
+            for (int gl = 0; gl < ngr; ++gl) {
+                if (lane < 2 * lanes_per_row)
+                    __builtin_amdgcn_global_load_lds(
+                        (void *)(src + (int64_t)(g_first + gl) * N * esz),
+                        (__attribute__((address_space(3))) void *)(szw + gl * SLOT), 16, 0, 0);
+            }
+        }
+
+        // ---- register ring of weight rows and activations ----
+        const int ncol = col0 + NC * c < N ? col0 + NC * c : 0;
+        const uint8_t *wbase = a.P + (int64_t)(s_begin * 16 + 4 * g) * N + ncol;
+        const int m = min(c, a.M - 1);
+        const _Float16 *xbase = a.X + (int64_t)m * a.ldx + (int64_t)s_begin * 32 + 8 * g;
+        wrow_t wr[D][4];
+        uint4_t xr[D];
+        auto load_step = [&](int j, wrow_t (&w)[4], uint4_t &x) {
+            const uint8_t *p = wbase + (int64_t)j * 16 * N;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                w[r] = __builtin_nontemporal_load((const wrow_t *)(p + (int64_t)r * N));
+            x = *(const uint4_t *)(xbase + (int64_t)j * 32);
+        };
+#pragma unroll
+        for (int d = 0; d < D; ++d) load_step(min(d, ns - 1), wr[d], xr[d]);
+        // The scale/zero copies are older than the ring's loads: retire them
+        // here, once, so no ds_read below waits on an LDS copy in flight.
+        wait_vmcnt<D * I4V_LPS>();
+
+        const uint32_t c64 = opaque_vgpr(0x64006400u);
+        const uint32_t mlo = opaque_sgpr(0x000F000Fu);
+        const half8_t ones = bitcast<half8_t>(uint4_t{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
+        const float4_t zf = {0.f, 0.f, 0.f, 0.f};
+        float4_t P[NC], Ssum = zf;
+#pragma unroll
+        for (int j = 0; j < NC; ++j) P[j] = zf;
+
+        auto step = [&](const wrow_t (&w)[4], const uint4_t &xv) {
+            const half8_t x = bitcast<half8_t>(xv);
+            uint32_t lo[4][NC / 4], hi[4][NC / 4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int h = 0; h < NC / 4; ++h) {
+                    if constexpr (NC == 8) lo[r][h] = w[r][h];
+                    else lo[r][h] = w[r];
+                    hi[r][h] = lo[r][h] >> 4;
+                }
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const int h = j >> 2, b = j & 3;
+                const uint32_t sel = (uint32_t)b | (uint32_t)b << 8 | (uint32_t)(4 + b) << 16 |
+                                     (uint32_t)(4 + b) << 24;
+                uint4_t bq;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    bq[r] = and_or(__builtin_amdgcn_perm(hi[r][h], lo[r][h], sel), mlo, c64);
+                P[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x, bitcast<half8_t>(bq), P[j], 0, 0, 0);
+            }
+            Ssum = __builtin_amdgcn_mfma_f32_16x16x32_f16(x, ones, Ssum, 0, 0, 0);
+        };
+        auto flush = [&](int gl) {
+            float sv[NC], zv[NC];
+            i4v_load_sz<SZ, NC>(lds_ptr(lds_addr(szw + gl * SLOT)), c, sv, zv);
+#pragma unroll
+            for (int j = 0; j < NC; ++j) {
+                const float zz = -(1024.0f + zv[j]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float tq = __builtin_fmaf(zz, Ssum[i], P[j][i]);
+                    acc[j][i] = __builtin_fmaf(sv[j], tq, acc[j][i]);
+                }
+                P[j] = zf;
+            }
+            Ssum = zf;
+        };
+
+        // Whole blocks of D steps with unconditional (clamped) loads, so the
+        // compiler's waits count exactly; then the < D remaining steps,
+        // whose data is already in the ring.
+        int j0 = 0;
+        for (; j0 + D <= ns; j0 += D) {
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                const int j = j0 + u;
+                step(wr[u], xr[u]);
+                load_step(min(j + D, ns - 1), wr[u], xr[u]);
+                const int sg = s_begin + j;
+                if ((sg + 1) % a.spg == 0 || j == ns - 1) flush(sg / a.spg - g_first);
+            }
+        }
+        wait_vmcnt<0>();
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int j = j0 + u;
+            if (j < ns) {
+                step(wr[u], xr[u]);
+                const int sg = s_begin + j;
+                if ((sg + 1) % a.spg == 0 || j == ns - 1) flush(sg / a.spg - g_first);
+            }
+        }
+        wait_vmcnt<0>();
+    }
+
+    // ---- wave partials -> LDS, ordered sum over waves ----
+    __syncthreads();                              // all waves done with their s/z slots
+    float *red = (float *)smem;                   // [IW][16][TC]
+    const int M = a.M;
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * g + i;
+            if (row < M) red[(wave * 16 + row) * TC + NC * c + j] = acc[j][i];
+        }
+    __syncthreads();
+    if (a.S == 1) {
+        for (int v = tid; v < M * TC; v += IW * 64) {
+            const int row = v / TC, cl = v % TC;
+            if (col0 + cl >= N) continue;
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < IW; ++w) sum += red[(w * 16 + row) * TC + cl];
+            a.Y[(int64_t)row * a.ldy + col0 + cl] = (_Float16)activate<ACT>(sum);
+        }
+        return;
+    }
+    // Split K: this workgroup's partial goes out with write-through stores
+    // (agent-scope relaxed atomic stores: global_store sc1), and once they are
+    // acknowledged (vmcnt(0)) one lane takes a ticket on the tile's counter.
+    // The workgroup that draws the last ticket reads every split's partial with
+    // L2-bypassing loads (agent-scope atomic loads: sc1) in split order.  This
+    // keeps the cross-XCD exchange to the partials themselves instead of the
+    // full-L2 write-back and invalidate that an agent-scope fence costs.
+    float *part = a.part + ((int64_t)t * a.S + sp) * M * TC;
+    if (!a.counters) {
+        // Reduction kernel mode: plain stores; the next kernel on the stream sums.
+        for (int v = tid; v < M * TC; v += IW * 64) {
+            const int row = v / TC, cl = v % TC;
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < IW; ++w) sum += red[(w * 16 + row) * TC + cl];
+            part[v] = sum;
+        }
+        return;
+    }
+    for (int v = tid; v < M * TC; v += IW * 64) {
+        const int row = v / TC, cl = v % TC;
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < IW; ++w) sum += red[(w * 16 + row) * TC + cl];
+        __hip_atomic_store(part + v, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();                              // red is dead from here: its first word holds the flag
+    uint32_t *last_flag = (uint32_t *)smem;
+    if (tid == 0) {
+        const uint32_t prev =
+            __hip_atomic_fetch_add(&a.counters[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last_flag = prev == (uint32_t)(a.S - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!*last_flag) return;
+    const float *base = a.part + (int64_t)t * a.S * M * TC;
+    for (int v = tid; v < M * TC; v += IW * 64) {
+        const int row = v / TC, cl = v % TC;
+        // Eight independent loads in flight at a time (clamped indices, summed
+        // in split order), not one memory round trip per split.
+        float sum = 0.f;
+        for (int q0 = 0; q0 < a.S; q0 += 8) {
+            float pv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                pv[i] = __hip_atomic_load(base + (int64_t)min(q0 + i, a.S - 1) * M * TC + v,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (q0 + i < a.S) sum += pv[i];
+        }
+        if (col0 + cl < N) a.Y[(int64_t)row * a.ldy + col0 + cl] = (_Float16)activate<ACT>(sum);
+    }
+    if (tid == 0) __hip_atomic_store(&a.counters[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Reduction-kernel mode: sums the S partials of every output in split order
+// and stores act(sum) as fp16 (the kernel boundary orders it after the GEMV).
+template <int ACT>
+__global__ void __launch_bounds__(256) i4_gemv_reduce_kernel(I4GemvArgs a, int tc) {
+    const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t per_tile = (int64_t)a.M * tc;
+    const int64_t ntiles = (a.N + tc - 1) / tc;
+    if (v >= ntiles * per_tile) return;
+    const int64_t t = v / per_tile;
+    const int e = (int)(v % per_tile);
+    const int row = e / tc, cl = e % tc;
+    if (t * tc + cl >= a.N) return;
+    const float *p = a.part + t * a.S * per_tile + e;
+    float sum = 0.f;
+    for (int q = 0; q < a.S; ++q) sum += p[(int64_t)q * per_tile];
+    a.Y[(int64_t)row * a.ldy + t * tc + cl] = (_Float16)activate<ACT>(sum);
+}
+
+struct I4GemvCfg {
+    int nc, spw, S;
+};
+
+// Tile shape and K split.  Default: 128-column tiles of 4 waves, K split so
+// that about 1024 waves run (2..32 steps each, at most I4V_SMAX splits).  A
+// wave's steps must fit its I4V_GMAX scale/zero slots: a range of spw steps
+// touches at most ceil(spw/spg) + 1 groups, or exactly spw/spg when spw is a
+// multiple of spg (every range then starts on a group boundary).
+// Experiments: MCQ4_I4_MODE=narrow selects 64-column tiles of 16 waves with
+// the whole K in one workgroup where the slots allow (64-byte row pieces read
+// at about half the bandwidth of 128-byte pieces on MI355X, so it is slower);
+// MCQ4_I4_SPW / MCQ4_I4_SPLIT force the steps per wave / split count;
+// MCQ4_I4_RED=kernel sums splits in a second kernel instead of the ticket.
+static I4GemvCfg i4_gemv_config(int64_t K, int64_t N, int64_t gs) {
+    const int64_t nsteps = K / 32, spg = gs / 32;
+    const int64_t loose = (I4V_GMAX - 1) * spg;          // any alignment
+    auto fit = [&](int64_t w) {
+        if (w <= loose) return w;
+        return std::min<int64_t>((w + spg - 1) / spg * spg, I4V_GMAX * spg);
+    };
+    const char *mode = getenv("MCQ4_I4_MODE");
+    const bool wide = !(mode && mode[0] == 'n');
+    const int nc = wide ? 8 : 4;
+    const int64_t iw = wide ? 4 : 16;
+    const int64_t ntiles = (N + 16 * nc - 1) / (16 * nc);
+    int64_t S;
+    if (wide) {
+        int64_t spw = (ntiles * nsteps + 1023) / 1024;
+        if (const char *env = getenv("MCQ4_I4_SPW")) spw = atoi(env);
+        spw = std::max<int64_t>(spw, (nsteps + iw * I4V_SMAX - 1) / (iw * I4V_SMAX));
+        spw = fit(std::min<int64_t>(std::max<int64_t>(spw, 2), 32));
+        S = (nsteps + iw * spw - 1) / (iw * spw);
+    } else {
+        S = 1;
+        while ((nsteps + iw * S - 1) / (iw * S) > fit((nsteps + iw * S - 1) / (iw * S)) && S < I4V_SMAX)
+            S *= 2;
+    }
+    if (const char *env = getenv("MCQ4_I4_SPLIT")) S = std::max(1, std::min(I4V_SMAX, atoi(env)));
+    int64_t spw = fit((nsteps + iw * S - 1) / (iw * S));
+    S = (nsteps + iw * spw - 1) / (iw * spw);
+    return {nc, (int)spw, (int)S};
+}
+
+bool i4_gemv_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
+                       const void *P, const void *scales, const void *zeros) {
+    return M >= 1 && M <= 16 && K % 32 == 0 && gs % 32 == 0 && N % 8 == 0 &&
+           (N + 63) / 64 <= COUNTER_SLOTS && ldx % 8 == 0 && ((uintptr_t)X % 16) == 0 &&
+           ((uintptr_t)P % 8) == 0 && ((uintptr_t)scales % 16) == 0 &&
+           ((uintptr_t)zeros % 16) == 0 && K / 32 < (1 << 24);
+}
+
+size_t i4_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs) {
+    const I4GemvCfg c = i4_gemv_config(K, N, gs);
+    if (c.S == 1) return 0;
+    const int64_t tc = 16 * c.nc;
+    return COUNTER_BYTES + (size_t)((N + tc - 1) / tc) * c.S * M * tc * sizeof(float);
+}
+
+template <int SZ, int D, int NC>
+static hipError_t launch_gemv_sz(const I4GemvArgs &a, int ntiles, int act, hipStream_t s) {
+    const dim3 grid(ntiles, a.S), block(I4vShape<NC>::IW * 64);
+    if (act == ACT_SILU) hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_SILU, D, NC>), grid, block, 0, s, a);
+    else if (act == ACT_GELU) hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_GELU, D, NC>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_NONE, D, NC>), grid, block, 0, s, a);
+    if (a.S > 1 && !a.counters) {
+        constexpr int tc = I4vShape<NC>::TC;
+        const int64_t n = (int64_t)ntiles * a.M * tc;
+        const dim3 rg((unsigned)((n + 255) / 256));
+        if (act == ACT_SILU) hipLaunchKernelGGL((i4_gemv_reduce_kernel<ACT_SILU>), rg, dim3(256), 0, s, a, tc);
+        else if (act == ACT_GELU) hipLaunchKernelGGL((i4_gemv_reduce_kernel<ACT_GELU>), rg, dim3(256), 0, s, a, tc);
+        else hipLaunchKernelGGL((i4_gemv_reduce_kernel<ACT_NONE>), rg, dim3(256), 0, s, a, tc);
+    }
+    return hipGetLastError();
+}
+
+template <int NC>
+static hipError_t launch_gemv_nc(const I4GemvArgs &a, int ntiles, int sz_dt, int act, hipStream_t s) {
+    if (sz_dt == DT_F32) return launch_gemv_sz<DT_F32, 4, NC>(a, ntiles, act, s);
+    if (sz_dt == DT_F16) return launch_gemv_sz<DT_F16, 4, NC>(a, ntiles, act, s);
+    return launch_gemv_sz<DT_BF16, 4, NC>(a, ntiles, act, s);
+}
+
+hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
+                          const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K,
+                          int N, int gs, int act, void *ws, hipStream_t s) {
+    const I4GemvCfg c = i4_gemv_config(K, N, gs);
+    I4GemvArgs a;
+    a.X = X; a.ldx = ldx; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y; a.ldy = ldy;
+    a.M = M; a.N = N; a.nsteps = K / 32; a.spg = gs / 32;
+    a.spw = c.spw; a.S = c.S;
+    a.part = nullptr; a.counters = nullptr;
+    if (c.S > 1) {
+        if (!ws) return hipErrorInvalidValue;
+        a.part = (float *)((char *)ws + COUNTER_BYTES);
+        const char *red = getenv("MCQ4_I4_RED");                   // experiments
+        if (!(red && red[0] == 'k')) a.counters = (uint32_t *)ws;
+    }
+    const int ntiles = (N + 16 * c.nc - 1) / (16 * c.nc);
+    if (c.nc == 8) return launch_gemv_nc<8>(a, ntiles, sz_dt, act, s);
+    return launch_gemv_nc<4>(a, ntiles, sz_dt, act, s);
+}
+
+}  // namespace mcq4

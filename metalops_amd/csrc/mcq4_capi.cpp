@@ -91,9 +91,16 @@ int check_kn(int64_t K, int64_t N) {
 
 }  // namespace
 
+namespace mcq4 {
+int set_error(int code, const char *msg) {
+    snprintf(g_err, sizeof(g_err), "%s", msg);
+    return code;
+}
+}  // namespace mcq4
+
 extern "C" {
 
-int mcq4_version(void) { return 1 * 10000 + 0 * 100 + 0; }
+int mcq4_version(void) { return 1 * 10000 + 1 * 100 + 0; }
 
 const char *mcq4_status_string(int status) {
     switch (status) {

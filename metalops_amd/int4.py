@@ -1,0 +1,330 @@
+"""Per-group INT4 quantize / dequantize / matmul and ``Int4Linear`` on MI355X.
+
+Mirrors metalcore's per-group INT4 API
+(``packages/metalcore/src/metalcore/quantization.py``):
+
+* ``quantize_int4(weight, group_size=128)``                       -- :26-92
+* ``dequantize_int4(W_packed, scales, zeros, group_size, dtype)`` -- :95-153
+* ``matmul_int4(X, W_packed, scales, zeros, group_size=128)``     -- :156-239
+* ``matmul_int4_silu`` / ``matmul_int4_gelu`` (the native bindings of
+  ``native/core_mps.mm:5780-5914``, registered at :6936-6937)
+* ``Int4Linear``                                                  -- :457-613
+
+Same names, argument order, defaults, layouts (``W_packed [K/2, N]`` uint8,
+``scales``/``zeros`` ``[ceil(K/group_size), N]`` in the weight's dtype) and
+result dtypes.  The computation runs in the HIP kernels of ``libmcq4.so``;
+tensors must live on a ROCm device and there is no CPU fallback.  Work is
+enqueued on the current stream without synchronising.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .quantization import _workspace   # split-K workspace shared with the q4_0 path
+
+__all__ = [
+    "quantize_int4",
+    "dequantize_int4",
+    "matmul_int4",
+    "matmul_int4_silu",
+    "matmul_int4_gelu",
+    "Int4Linear",
+]
+
+_DT = {torch.float32: _lib.MCQ4_DTYPE_F32, torch.float16: _lib.MCQ4_DTYPE_F16,
+       torch.bfloat16: _lib.MCQ4_DTYPE_BF16}
+
+
+def _require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "metalops_amd int4 ops run only on a ROCm GPU (torch device 'cuda'); "
+                f"got a tensor on '{t.device}'. There is no CPU fallback.")
+    dev = tensors[0].device
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"all tensors must be on one device, got {dev} and {t.device}")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _dense(t: torch.Tensor, align: int) -> torch.Tensor:
+    t = t.contiguous()
+    if t.data_ptr() % align:
+        t = t.clone()
+    return t
+
+
+def quantize_int4(
+    weight: torch.Tensor,
+    group_size: int = 128,
+) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Quantize ``weight[K, N]`` to INT4 with a scale and zero point per group of rows.
+
+    Returns ``(weight_packed [K/2, N] uint8, scales [G, N], zeros [G, N])`` with
+    ``G = ceil(K / group_size)`` and scales/zeros in ``weight.dtype``.  Per group
+    and column: ``scale = (max - min) / 15`` (at least 1e-8), ``zero = -min / scale``,
+    ``q = round_half_even(w / scale + zero)`` clamped to [0, 15]; row ``k`` is
+    the low nibble of byte row ``k // 2`` for even ``k``, the high nibble for
+    odd ``k`` (quantization.py:62-90).  Each step is rounded to the weight's
+    dtype as the reference's torch ops are.  float32, float16 and bfloat16
+    weights are supported.
+    """
+    K, N = weight.shape
+    if K % 2:
+        # The reference indexes byte row K // 2 of a [K // 2, N] tensor here.
+        raise IndexError(f"K ({K}) must be even: two rows share each packed byte")
+    _require_device(weight)
+    if weight.dtype not in _DT:
+        raise RuntimeError(f"quantize_int4: unsupported weight dtype {weight.dtype}")
+    w = weight
+    es = w.element_size()
+    if w.stride(1) != 1 or w.stride(0) < N or w.data_ptr() % es:
+        w = w.contiguous()
+    G = (K + group_size - 1) // group_size
+    packed = torch.empty((K // 2, N), dtype=torch.uint8, device=w.device)
+    scales = torch.empty((G, N), dtype=w.dtype, device=w.device)
+    zeros = torch.empty((G, N), dtype=w.dtype, device=w.device)
+    if K == 0 or N == 0:
+        return packed, scales, zeros
+    with torch.cuda.device(w.device):
+        _lib.check(_lib.lib.mcq4_quantize_int4(w.data_ptr(), _DT[w.dtype], w.stride(0), K, N,
+                                               group_size, packed.data_ptr(), scales.data_ptr(),
+                                               zeros.data_ptr(), _stream(w.device)),
+                   "mcq4_quantize_int4")
+    return packed, scales, zeros
+
+
+def _sz_pair(scales: torch.Tensor, zeros: torch.Tensor):
+    """Scales and zeros in one kernel dtype (exact upcast to fp32 when they differ)."""
+    if scales.dtype != zeros.dtype or scales.dtype not in _DT:
+        scales, zeros = scales.float(), zeros.float()
+    return _dense(scales, 16), _dense(zeros, 16)
+
+
+def _check_shapes(W_packed, scales, zeros, group_size):
+    Kh, N = W_packed.shape
+    K = Kh * 2
+    G = (K + group_size - 1) // group_size
+    if W_packed.dtype != torch.uint8:
+        raise RuntimeError("W_packed must be uint8 [K/2, N]")
+    if tuple(scales.shape) != (G, N) or tuple(zeros.shape) != (G, N):
+        raise RuntimeError(
+            f"scales/zeros must be [{G}, {N}] for K={K}, group_size={group_size}; got "
+            f"{tuple(scales.shape)} and {tuple(zeros.shape)}")
+    return K, N
+
+
+def dequantize_int4(
+    W_packed: torch.Tensor,
+    scales: torch.Tensor,
+    zeros: torch.Tensor,
+    group_size: int = 128,
+    dtype: Optional[torch.dtype] = None,
+) -> torch.Tensor:
+    """``W[k, n] = ((q - zero) * scale)`` computed in fp32, returned in ``dtype`` (default fp16).
+
+    Zero and scale are upcast exactly, the subtraction and the product are two
+    fp32 roundings, and the result is rounded once to ``dtype`` -- bit for bit
+    what quantization.py:144-151 computes.
+    """
+    if dtype is None:
+        dtype = torch.float16
+    _require_device(W_packed, scales, zeros)
+    K, N = _check_shapes(W_packed, scales, zeros, group_size)
+    s, z = _sz_pair(scales, zeros)
+    p = _dense(W_packed, 1)
+    kernel_dtype = dtype if dtype in _DT else torch.float32
+    out = torch.empty((K, N), dtype=kernel_dtype, device=p.device)
+    if K and N:
+        with torch.cuda.device(p.device):
+            _lib.check(_lib.lib.mcq4_dequantize_int4(p.data_ptr(), s.data_ptr(), z.data_ptr(),
+                                                     _DT[s.dtype], K, N, group_size,
+                                                     out.data_ptr(), N, _DT[kernel_dtype],
+                                                     _stream(p.device)),
+                       "mcq4_dequantize_int4")
+    return out if out.dtype == dtype else out.to(dtype)
+
+
+_FN = {0: "mcq4_matmul_int4", 1: "mcq4_matmul_int4_silu", 2: "mcq4_matmul_int4_gelu"}
+
+
+def _matmul(X, W_packed, scales, zeros, group_size, act):
+    _require_device(X, W_packed, scales, zeros)
+    K, N = _check_shapes(W_packed, scales, zeros, group_size)
+    batched = X.dim() == 3                                   # quantization.py:185-192
+    if X.dim() not in (2, 3):
+        raise RuntimeError(f"X must be [M, K] or [B, M, K], got shape {tuple(X.shape)}")
+    if X.shape[-1] != K:
+        raise RuntimeError(f"X K dim ({X.shape[-1]}) must match weight K ({K})")
+    lead = X.shape[:-1]
+    x = X.reshape(-1, K)
+    out_dtype = X.dtype
+    if x.dtype not in _DT:
+        x = x.float()
+    if x.stride(1) != 1 or x.stride(0) < K or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = _dense(x, 16)
+    M = x.shape[0]
+    s, z = _sz_pair(scales, zeros)
+    p = _dense(W_packed, 16)
+    Y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    if M and N:
+        if K == 0:
+            Y.zero_()
+        else:
+            xdt = _DT[x.dtype]
+            need = int(_lib.lib.mcq4_matmul_int4_workspace_bytes(M, K, N, group_size, xdt))
+            stream = _stream(x.device)
+            ws_ptr, ws_bytes = None, 0
+            if need:
+                ws = _workspace.get(x.device, stream, need)
+                ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+            fn = getattr(_lib.lib, _FN[act])
+            with torch.cuda.device(x.device):
+                _lib.check(fn(x.data_ptr(), xdt, x.stride(0), p.data_ptr(), s.data_ptr(),
+                              z.data_ptr(), _DT[s.dtype], Y.data_ptr(), N, M, K, N, group_size,
+                              ws_ptr, ws_bytes, stream),
+                           _FN[act])
+    Y = Y if Y.dtype == out_dtype else Y.to(out_dtype)
+    return Y.reshape(*lead, N) if batched else Y
+
+
+def matmul_int4(
+    X: torch.Tensor,
+    W_packed: torch.Tensor,
+    scales: torch.Tensor,
+    zeros: torch.Tensor,
+    group_size: int = 128,
+) -> torch.Tensor:
+    """``Y = X @ dequant(W_packed, scales, zeros)`` for ``X`` ``[M, K]`` or ``[B, M, K]``.
+
+    fp32 accumulation; the result has ``X``'s dtype.  fp16 activations run the
+    MFMA kernels (decode GEMV for M <= 16 rows, prefill GEMM above); fp32 and
+    bf16 activations run the general fp32 kernel with the weight rounded to
+    ``X``'s dtype first, as the reference builds ``W`` in ``X.dtype``
+    (quantization.py:220-239).
+    """
+    return _matmul(X, W_packed, scales, zeros, group_size, 0)
+
+
+def _fused(X, W_packed, scales, zeros, group_size, act):
+    if X.dtype != torch.float16:
+        raise RuntimeError("Fused kernel requires half precision")   # core_mps.mm:5795
+    if X.dim() != 2:
+        raise RuntimeError(f"X must be [M, K], got shape {tuple(X.shape)}")
+    return _matmul(X, W_packed, scales, zeros, group_size, act)
+
+
+def matmul_int4_silu(X, W_packed, scales, zeros, group_size: int = 128) -> torch.Tensor:
+    """``silu(X @ dequant(W))`` with the activation fused into the matmul store (fp16 X)."""
+    return _fused(X, W_packed, scales, zeros, group_size, 1)
+
+
+def matmul_int4_gelu(X, W_packed, scales, zeros, group_size: int = 128) -> torch.Tensor:
+    """``gelu(X @ dequant(W))`` (tanh form, as the fused reference kernel) fused into the store."""
+    return _fused(X, W_packed, scales, zeros, group_size, 2)
+
+
+class Int4Linear(nn.Module):
+    """INT4 quantized linear layer (quantization.py:457-613).
+
+    ``weight_packed [in/2, out]`` uint8, ``scales``/``zeros [G, out]`` and ``bias``
+    are buffers.  ``dequant_on_load=True`` keeps a dequantized fp16 weight and
+    runs a plain fp16 matmul; ``keep_quantized()`` drops it and runs the INT4
+    kernels on every forward.
+    """
+
+    def __init__(
+        self,
+        in_features: int,
+        out_features: int,
+        group_size: int = 128,
+        bias: bool = True,
+        device: Optional[torch.device] = None,
+        dtype: Optional[torch.dtype] = None,
+        dequant_on_load: bool = True,
+    ):
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.group_size = group_size
+        self._dequant_on_load = dequant_on_load
+        self.register_buffer(
+            "weight_packed",
+            torch.zeros((in_features // 2, out_features), dtype=torch.uint8, device=device))
+        num_groups = (in_features + group_size - 1) // group_size
+        self.register_buffer(
+            "scales",
+            torch.ones((num_groups, out_features), dtype=dtype or torch.float32, device=device))
+        self.register_buffer(
+            "zeros",
+            torch.zeros((num_groups, out_features), dtype=dtype or torch.float32, device=device))
+        self._weight_dequant: Optional[torch.Tensor] = None
+        if bias:
+            self.register_buffer(
+                "bias", torch.zeros(out_features, dtype=dtype or torch.float32, device=device))
+        else:
+            self.register_parameter("bias", None)
+
+    def dequantize(self, dtype: Optional[torch.dtype] = None) -> None:
+        """Materialise the dequantized weight (default fp16) for plain matmuls."""
+        if dtype is None:
+            dtype = torch.float16
+        self._weight_dequant = dequantize_int4(
+            self.weight_packed, self.scales, self.zeros, self.group_size, dtype)
+        self._dequant_on_load = True
+
+    def keep_quantized(self) -> None:
+        """Drop the dequantized weight; forward then runs the INT4 kernels."""
+        self._weight_dequant = None
+        self._dequant_on_load = False
+
+    @classmethod
+    def from_float(
+        cls,
+        module: nn.Linear,
+        group_size: int = 128,
+        dequant_on_load: bool = True,
+    ) -> "Int4Linear":
+        """Quantize an ``nn.Linear`` (its weight ``[out, in]`` transposed to ``[in, out]``)."""
+        q_linear = cls(
+            in_features=module.in_features,
+            out_features=module.out_features,
+            group_size=group_size,
+            bias=module.bias is not None,
+            device=module.weight.device,
+            dtype=module.weight.dtype,
+            dequant_on_load=dequant_on_load,
+        )
+        weight = module.weight.data.T.contiguous()
+        W_packed, scales, zeros = quantize_int4(weight, group_size)
+        q_linear.weight_packed.copy_(W_packed)
+        q_linear.scales.copy_(scales)
+        q_linear.zeros.copy_(zeros)
+        if module.bias is not None:
+            q_linear.bias.copy_(module.bias.data)
+        if dequant_on_load:
+            q_linear.dequantize()
+        return q_linear
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self._weight_dequant is not None:
+            x_half = x.half() if x.dtype != torch.float16 else x
+            y = (x_half @ self._weight_dequant).to(x.dtype)
+        else:
+            y = matmul_int4(x, self.weight_packed, self.scales, self.zeros, self.group_size)
+        if self.bias is not None:
+            y = y + self.bias
+        return y
+
+    def extra_repr(self) -> str:
+        mode = "fast_fp16" if self._weight_dequant is not None else "int4_kernel"
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"group_size={self.group_size}, bias={self.bias is not None}, mode={mode}")

@@ -88,3 +88,58 @@ def test_quantize_dequant_validation_codes():
 def test_error_raises_runtime_error_subclass():
     with pytest.raises(RuntimeError, match="invalid argument"):
         _lib.check(_lib.lib.mcq4_quantize_q4_0(None, 8, 32, 8, None, None), "mcq4_quantize_q4_0")
+
+
+def test_int4_validation_codes():
+    """Per-group INT4 entry points reject bad arguments before any launch."""
+    L = _lib.lib
+    F32, F16, BF16 = _lib.MCQ4_DTYPE_F32, _lib.MCQ4_DTYPE_F16, _lib.MCQ4_DTYPE_BF16
+    X, P, S, Z, Y = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+    mm = L.mcq4_matmul_int4
+    assert mm(None, F16, 64, P, S, Z, F32, Y, 8, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert mm(X, 7, 64, P, S, Z, F32, Y, 8, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert mm(X, F16, 64, P, S, Z, 9, Y, 8, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert mm(X, F16, 64, P, S, Z, F32, Y, 8, 1, 63, 8, 32, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert "even" in _err()
+    assert mm(X, F16, 64, P, S, Z, F32, Y, 8, 1, 64, 8, 0, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert "group_size" in _err()
+    assert mm(X, F16, 64, P, S, Z, F32, Y, 8, 0, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert mm(X, F16, 32, P, S, Z, F32, Y, 8, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert mm(X, F16, 64, P, S, Z, F32, Y, 4, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert mm(X + 1, F16, 64, P, S, Z, F32, Y, 8, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_ALIGNMENT
+    assert mm(X, F32, 64, P, S, Z, F32, Y + 2, 8, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_ALIGNMENT
+    assert mm(X, F16, 64, P, S + 2, Z, F32, Y, 8, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_ALIGNMENT
+    # The decode kernel with a split K (long K, small groups) needs the workspace it reports.
+    need = L.mcq4_matmul_int4_workspace_bytes(1, 16384, 4096, 32, F16)
+    assert need > 0
+    assert mm(X, F16, 16384, P, S, Z, F16, Y, 4096, 1, 16384, 4096, 32, None, 0, None) == _lib.MCQ4_ERR_WORKSPACE
+    assert L.mcq4_matmul_int4_silu(None, F16, 64, P, S, Z, F32, Y, 8, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert L.mcq4_matmul_int4_gelu(X, F16, 64, P, S, Z, F32, Y, 8, 1, 63, 8, 32, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    # quantize / dequantize
+    q = L.mcq4_quantize_int4
+    assert q(None, F32, 8, 64, 8, 32, P, S, Z, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert q(X, 5, 8, 64, 8, 32, P, S, Z, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert q(X, F32, 8, 63, 8, 32, P, S, Z, None) == _lib.MCQ4_ERR_SHAPE
+    assert q(X, F32, 4, 64, 8, 32, P, S, Z, None) == _lib.MCQ4_ERR_SHAPE
+    assert q(X + 2, F32, 8, 64, 8, 32, P, S, Z, None) == _lib.MCQ4_ERR_ALIGNMENT
+    assert q(X, BF16, 8, 64, 8, 32, P, S + 1, Z, None) == _lib.MCQ4_ERR_ALIGNMENT
+    d = L.mcq4_dequantize_int4
+    assert d(None, S, Z, F32, 64, 8, 32, Y, 8, F16, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert d(P, S, Z, F32, 64, 8, 32, Y, 8, 3, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert d(P, S, Z, F32, 64, 8, 32, Y, 4, F16, None) == _lib.MCQ4_ERR_SHAPE
+    assert d(P, S, Z, F32, 64, 8, -1, Y, 8, F16, None) == _lib.MCQ4_ERR_SHAPE
+    assert d(P, S, Z, F32, 64, 8, 32, Y + 2, 8, F32, None) == _lib.MCQ4_ERR_ALIGNMENT
+
+
+def test_int4_workspace_sizes():
+    L = _lib.lib
+    F16, F32 = _lib.MCQ4_DTYPE_F16, _lib.MCQ4_DTYPE_F32
+    # fp32 activations and odd group sizes run the general kernel: no workspace
+    assert L.mcq4_matmul_int4_workspace_bytes(1, 4096, 4096, 128, F32) == 0
+    assert L.mcq4_matmul_int4_workspace_bytes(1, 4096, 4096, 100, F16) == 0
+    # wide-N decode keeps K in one workgroup: no workspace
+    assert L.mcq4_matmul_int4_workspace_bytes(1, 4096, 128256, 128, F16) == 0
+    # split-K layouts start with the 256 KiB counter area
+    for M, K, N in ((1, 4096, 4096), (16, 14336, 4096), (128, 4096, 4096)):
+        ws = L.mcq4_matmul_int4_workspace_bytes(M, K, N, 128, F16)
+        assert ws == 0 or ws > 256 * 1024

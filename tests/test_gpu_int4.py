@@ -1,0 +1,264 @@
+"""GPU parity tests of the per-group INT4 path against the CPU oracle (oracle/int4_ref.py).
+
+* quantize / dequantize: bit-exact (packed bytes, scales, zeros, outputs) for
+  fp32 / fp16 / bf16, group sizes 128, 64, 32, 33 and 3, partial last groups;
+* matmul (every kernel: decode GEMV M <= 16, prefill GEMM, general kernel; fp16,
+  bf16 and fp32 activations; fp32 / fp16 / bf16 scales): per output row
+  max|Y - Y_ref| <= 1e-2 * max|Y_ref[m, :]| against X.float() @ dequant_f32(W)
+  (the tolerance of the fp16 matmul path; the dequant itself is pinned exactly);
+* fused SiLU / GELU stores, 3-D activations, repeated split-K calls, Int4Linear.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import int4_ref as R
+
+pytestmark = pytest.mark.gpu
+
+TDT = {R.F32: torch.float32, R.F16: torch.float16, R.BF16: torch.bfloat16}
+
+
+@pytest.fixture(scope="module")
+def mo(dev):
+    import metalops_amd
+    return metalops_amd
+
+
+def _weights(K, N, seed, dtype=R.F32):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(K, N, generator=g) * 0.02
+    idx = torch.randperm(K * N, generator=g)[: max(1, K * N // 100)]
+    w.view(-1)[idx] = torch.randn(idx.numel(), generator=g) * 0.2
+    return R.round_to(w.numpy(), dtype)
+
+
+def _quant(mo, dev, K, N, gs, dtype=R.F32, seed=0):
+    w = _weights(K, N, seed, dtype)
+    wt = torch.from_numpy(w).to(TDT[dtype]).to(dev)
+    packed, s, z = mo.quantize_int4(wt, gs)
+    return w, packed, s, z
+
+
+def _bits_equal(a: np.ndarray, b: np.ndarray) -> bool:
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    return np.array_equal(a, b) or np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ---- quantize / dequantize ----------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [R.F32, R.F16, R.BF16])
+@pytest.mark.parametrize("K,N,gs", [(256, 96, 128), (96, 40, 64), (24, 10, 3), (66, 9, 33),
+                                    (4096, 512, 128)])
+def test_quantize_bit_exact(mo, dev, dtype, K, N, gs):
+    print(f"quantize {dtype} K={K} N={N} gs={gs}", flush=True)
+    w, packed, s, z = _quant(mo, dev, K, N, gs, dtype, seed=K + N)
+    rp, rs, rz = R.quantize(w, gs, dtype)
+    assert s.dtype == TDT[dtype] and z.dtype == TDT[dtype]
+    np.testing.assert_array_equal(packed.cpu().numpy(), rp)
+    assert _bits_equal(s.float().cpu().numpy(), rs)
+    assert _bits_equal(z.float().cpu().numpy(), rz)
+
+
+def test_quantize_strided_input(mo, dev):
+    w = _weights(128, 80, 5)
+    big = torch.zeros(128, 96, device=dev)
+    big[:, :80] = torch.from_numpy(w).to(dev)
+    packed, s, z = mo.quantize_int4(big[:, :80], 64)
+    rp, rs, rz = R.quantize(w, 64)
+    np.testing.assert_array_equal(packed.cpu().numpy(), rp)
+    assert _bits_equal(s.cpu().numpy(), rs) and _bits_equal(z.cpu().numpy(), rz)
+
+
+@pytest.mark.parametrize("sz", [R.F32, R.F16, R.BF16])
+@pytest.mark.parametrize("out", [torch.float32, torch.float16, torch.bfloat16])
+def test_dequant_bit_exact(mo, dev, sz, out):
+    K, N, gs = 192, 72, 64
+    w, packed, s, z = _quant(mo, dev, K, N, gs, sz, seed=3)
+    got = mo.dequantize_int4(packed, s, z, gs, out)
+    assert got.dtype == out and tuple(got.shape) == (K, N)
+    name = {torch.float32: R.F32, torch.float16: R.F16, torch.bfloat16: R.BF16}[out]
+    want = R.dequantize(packed.cpu().numpy(), s.float().cpu().numpy(), z.float().cpu().numpy(),
+                        gs, name)
+    assert _bits_equal(got.float().cpu().numpy(), want)
+    # default dtype is fp16 (quantization.py:137-138)
+    assert mo.dequantize_int4(packed, s, z, gs).dtype == torch.float16
+
+
+def test_dequant_handmade_codes(mo, dev):
+    """Every code 0..15 in both nibbles against chosen scales/zeros."""
+    K, N, gs = 32, 16, 16
+    q = np.array([[(k + 3 * n) % 16 for n in range(N)] for k in range(K)], np.uint8)
+    packed = (q[0::2] | (q[1::2] << 4)).astype(np.uint8)
+    rng = np.random.default_rng(0)
+    s = rng.normal(0, 1, (2, N)).astype(np.float32)
+    z = rng.uniform(-2, 17, (2, N)).astype(np.float32)
+    got = mo.dequantize_int4(torch.from_numpy(packed).to(dev), torch.from_numpy(s).to(dev),
+                             torch.from_numpy(z).to(dev), gs, torch.float32)
+    assert _bits_equal(got.cpu().numpy(), R.dequantize(packed, s, z, gs, R.F32))
+
+
+# ---- matmul -------------------------------------------------------------------
+
+def _check_rows(Y, Yref, tol=1e-2):
+    Y = np.asarray(Y, np.float64)
+    Yref = np.asarray(Yref, np.float64)
+    assert np.all(np.isfinite(Y))
+    scale = np.maximum(np.abs(Yref).max(axis=-1, keepdims=True), 1e-6)
+    err = np.abs(Y - Yref) / scale
+    assert err.max() <= tol, f"max row-relative error {err.max():.3e}"
+
+
+def _ref(X, packed, s, z, gs):
+    return R.matmul_f32(X.float().cpu().numpy(), packed.cpu().numpy(), s.float().cpu().numpy(),
+                        z.float().cpu().numpy(), gs)
+
+
+@pytest.fixture
+def i4_path():
+    old = os.environ.get("MCQ4_I4_PATH")
+
+    def set_path(v):
+        if v is None:
+            os.environ.pop("MCQ4_I4_PATH", None)
+        else:
+            os.environ["MCQ4_I4_PATH"] = v
+    yield set_path
+    set_path(old)
+
+
+MM_CASES = [
+    # (M, K, N, gs): decode GEMV shapes (M <= 16)
+    (1, 4096, 4096, 128), (1, 256, 136, 128), (2, 512, 256, 64), (5, 1024, 392, 32),
+    (16, 2048, 1024, 128), (8, 96, 24, 64), (3, 4096, 11008, 128), (1, 14336, 512, 128),
+    (1, 512, 2176, 256), (2, 512, 2004, 128),
+    # prefill GEMM shapes (M > 16, N % 128 == 0)
+    (17, 512, 256, 128), (64, 1024, 512, 64), (128, 4096, 1024, 128), (300, 2048, 768, 32),
+    (512, 1024, 2048, 128), (33, 96, 128, 64),
+    # general kernel (N % 128 != 0 with M > 16; N % 8 != 0)
+    (40, 256, 200, 128), (3, 128, 21, 64),
+]
+
+
+@pytest.mark.parametrize("M,K,N,gs", MM_CASES)
+@pytest.mark.parametrize("sz", [R.F32, R.F16])
+def test_matmul_fp16(mo, dev, M, K, N, gs, sz):
+    print(f"matmul_int4 fp16 M={M} K={K} N={N} gs={gs} sz={sz}", flush=True)
+    w, packed, s, z = _quant(mo, dev, K, N, gs, sz, seed=M + K + N)
+    X = (torch.randn(M, K, generator=torch.Generator().manual_seed(M)) ).half().to(dev)
+    Y = mo.matmul_int4(X, packed, s, z, gs)
+    assert Y.dtype == torch.float16 and tuple(Y.shape) == (M, N)
+    _check_rows(Y.float().cpu().numpy(), _ref(X, packed, s, z, gs))
+
+
+@pytest.mark.parametrize("M,K,N,gs", [(1, 1024, 512, 128), (16, 512, 256, 64), (130, 512, 384, 128)])
+def test_matmul_bf16_scales(mo, dev, M, K, N, gs):
+    w, packed, s, z = _quant(mo, dev, K, N, gs, R.BF16, seed=11)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(1)).half().to(dev)
+    Y = mo.matmul_int4(X, packed, s, z, gs)
+    _check_rows(Y.float().cpu().numpy(), _ref(X, packed, s, z, gs))
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("M,K,N,gs", [(1, 4096, 512, 128), (8, 512, 100, 64), (128, 1024, 256, 128)])
+def test_matmul_other_activation_dtypes(mo, dev, xdt, M, K, N, gs):
+    """fp32 / bf16 activations run the general kernel; result in X.dtype."""
+    w, packed, s, z = _quant(mo, dev, K, N, gs, R.F32, seed=2)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(4)).to(xdt).to(dev)
+    Y = mo.matmul_int4(X, packed, s, z, gs)
+    assert Y.dtype == xdt
+    Yref = _ref(X, packed, s, z, gs)
+    _check_rows(Y.float().cpu().numpy(), Yref, tol=1e-2)
+    if xdt == torch.float32:
+        # fp32 activations with fp32 weights: much tighter than the fp16 bar
+        _check_rows(Y.cpu().numpy(), Yref, tol=1e-4)
+
+
+@pytest.mark.parametrize("M,K,N,gs", [(1, 1024, 512, 128), (12, 512, 256, 64), (200, 1024, 512, 128)])
+def test_matmul_kernels_agree_with_general(mo, dev, i4_path, M, K, N, gs):
+    """The MFMA kernels and the general kernel agree within the same tolerance."""
+    w, packed, s, z = _quant(mo, dev, K, N, gs, R.F32, seed=9)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(5)).half().to(dev)
+    Y_fast = mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy()
+    i4_path("generic")
+    Y_gen = mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy()
+    _check_rows(Y_fast, Y_gen)
+
+
+def test_matmul_batched_and_strided(mo, dev):
+    K, N, gs = 512, 256, 128
+    w, packed, s, z = _quant(mo, dev, K, N, gs)
+    X3 = torch.randn(3, 5, K, generator=torch.Generator().manual_seed(6)).half().to(dev)
+    Y3 = mo.matmul_int4(X3, packed, s, z, gs)
+    assert tuple(Y3.shape) == (3, 5, N)
+    _check_rows(Y3.reshape(15, N).float().cpu().numpy(), _ref(X3.reshape(15, K), packed, s, z, gs))
+    Xbig = torch.randn(40, K + 8, generator=torch.Generator().manual_seed(7)).half().to(dev)
+    Xv = Xbig[:, 3:3 + K]                       # misaligned view: copied to a dense buffer
+    _check_rows(mo.matmul_int4(Xv, packed, s, z, gs).float().cpu().numpy(),
+                _ref(Xv, packed, s, z, gs))
+
+
+def test_split_k_repeat_and_interleave(mo, dev):
+    """Split-K counters are left at zero: repeated and interleaved shapes stay correct."""
+    cases = [(1, 4096, 4096, 128), (16, 14336, 512, 128), (128, 4096, 512, 128)]
+    data = []
+    for i, (M, K, N, gs) in enumerate(cases):
+        w, packed, s, z = _quant(mo, dev, K, N, gs, seed=20 + i)
+        X = torch.randn(M, K, generator=torch.Generator().manual_seed(i)).half().to(dev)
+        data.append((X, packed, s, z, gs, _ref(X, packed, s, z, gs)))
+    for rep in range(3):
+        for X, packed, s, z, gs, Yref in data:
+            _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
+
+
+def _silu(y):
+    return y / (1.0 + np.exp(-y))
+
+
+def _gelu_tanh(y):
+    return 0.5 * y * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (y + 0.044715 * y ** 3)))
+
+
+@pytest.mark.parametrize("M,K,N,gs", [(1, 1024, 512, 128), (16, 512, 256, 64), (256, 1024, 512, 128),
+                                      (40, 256, 200, 128)])
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+def test_fused_activation(mo, dev, M, K, N, gs, act):
+    w, packed, s, z = _quant(mo, dev, K, N, gs, seed=31)
+    X = (torch.randn(M, K, generator=torch.Generator().manual_seed(8)) * 4).half().to(dev)
+    fn = mo.matmul_int4_silu if act == "silu" else mo.matmul_int4_gelu
+    Y = fn(X, packed, s, z, gs)
+    base = _ref(X, packed, s, z, gs).astype(np.float64)
+    want = _silu(base) if act == "silu" else _gelu_tanh(base)
+    Y = Y.float().cpu().numpy().astype(np.float64)
+    scale = np.maximum(np.abs(base).max(axis=-1, keepdims=True), 1e-6)
+    assert (np.abs(Y - want) / scale).max() <= 1e-2
+
+
+def test_fused_requires_half(mo, dev):
+    w, packed, s, z = _quant(mo, dev, 64, 16, 32)
+    with pytest.raises(RuntimeError, match="half precision"):
+        mo.matmul_int4_silu(torch.zeros(2, 64, device=dev), packed, s, z, 32)
+
+
+@pytest.mark.parametrize("dequant_on_load", [True, False])
+def test_int4_linear(mo, dev, dequant_on_load):
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(512, 256).to(dev)
+    q = mo.Int4Linear.from_float(lin, group_size=128, dequant_on_load=dequant_on_load)
+    assert q.scales.dtype == torch.float32 and tuple(q.weight_packed.shape) == (256, 256)
+    x = torch.randn(4, 7, 512, device=dev)
+    y = q(x)
+    assert y.dtype == torch.float32 and tuple(y.shape) == (4, 7, 256)
+    ref = _ref(x.reshape(28, 512).half() if dequant_on_load else x.reshape(28, 512),
+               q.weight_packed, q.scales, q.zeros, 128) + lin.bias.detach().cpu().numpy()
+    _check_rows(y.reshape(28, 256).detach().cpu().numpy(), ref)
+    q.keep_quantized()
+    assert "int4_kernel" in q.extra_repr()
+    y2 = q(x.half())
+    assert y2.dtype == torch.float32      # fp16 product + fp32 bias buffer promotes (reference :604-605)
+    _check_rows(y2.reshape(28, 256).float().detach().cpu().numpy(), ref)
+    q.dequantize()
+    assert "fast_fp16" in q.extra_repr()
