@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X q4_0 path -- one JSON line on stdout.
+"""Benchmark of the MI355X q4_0 and per-group INT4 paths -- one JSON line on stdout.
 
 Metric: q4_0 GEMV GB/s (% HBM peak) at M=1; q4_0 GEMM TFLOP/s
 (% MFMA) at M=2048.
@@ -15,6 +15,9 @@ Metric: q4_0 GEMV GB/s (% HBM peak) at M=1; q4_0 GEMM TFLOP/s
 * ``cpu_baseline``: the reference's CPU path (dequantize to fp16 on every call,
   then ``X @ W``; quantization.py:452-454) restated in oracle/, timed on this
   host's cores on a bounded sample.
+* ``int4``: the per-group INT4 path (quantization.py:26-239) on the same decode
+  layer and prefill shapes, group size 128 with fp16 scales and zeros (an fp16
+  model's weights), with its own roofline and CPU baseline.
 
 Inputs are synthetic: seeded N(0, 0.02) fp32 weights quantized on the GPU with
 the llama.cpp q4_0 rule, N(0, 1) fp16 activations.
@@ -48,10 +51,20 @@ DECODE_LAYER = [  # (name, K, N) -- Llama-2-7B projections, configs[1]
     ("down", 11008, 4096),
 ]
 PREFILL = [("up", 2048, 4096, 14336), ("down", 2048, 14336, 4096)]
+I4_GROUP = 128
+# HBM bytes per launch of the INT4 kernels (rocprofv3 FETCH_SIZE / WRITE_SIZE,
+# scaled as above); None until measured.
+I4_DECODE_TRAFFIC_BYTES = None
+I4_PREFILL_UP_TRAFFIC_BYTES = None
 
 
 def wbytes(K, N):
     return 18 * (K // 32) * N
+
+
+def i4_wbytes(K, N, gs=I4_GROUP):
+    """Packed nibbles plus fp16 scales and zeros of one INT4 weight."""
+    return K // 2 * N + 2 * 2 * ((K + gs - 1) // gs) * N
 
 
 def parse():
@@ -63,7 +76,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
-    p.add_argument("--part", choices=["all", "decode", "prefill", "copy"], default="all",
+    p.add_argument("--part", choices=["all", "decode", "prefill", "copy", "int4-decode",
+                                      "int4-prefill"], default="all",
                    help="run one part only (for profiler passes); 'copy' runs a plain 256 MiB "
                         "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters")
     return p.parse_args()
@@ -183,6 +197,92 @@ def prefill_bench(mo, torch, dev, iters=30, warmup=10):
     return out
 
 
+def make_i4_weights(mo, torch, K, N, seed, dev, outliers=False):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    W = torch.randn(K, N, generator=g, device=dev) * 0.02
+    if outliers:
+        idx = torch.randperm(K * N, generator=g, device=dev)[: K * N // 100]
+        W.view(-1)[idx] = torch.randn(idx.numel(), generator=g, device=dev) * 0.2
+    out = mo.quantize_int4(W.half(), I4_GROUP)
+    del W
+    return out
+
+
+def i4_decode_bench(mo, torch, dev, args):
+    R = max(1, args.copies)
+    layers = [[make_i4_weights(mo, torch, K, N, 5000 + 1000 * r + i, dev)
+               for i, (_, K, N) in enumerate(DECODE_LAYER)] for r in range(R)]
+    g = torch.Generator(device=dev).manual_seed(1)
+    xs = {K: torch.randn(1, K, generator=g, device=dev).half() for K in (4096, 11008)}
+    stream = torch.cuda.Stream(dev)
+
+    def one_step(r):
+        return [mo.matmul_int4(xs[K], *w, I4_GROUP) for (_, K, _), w in zip(DECODE_LAYER, layers[r % R])]
+
+    with torch.cuda.stream(stream):
+        one_step(0)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for r in range(R):
+            one_step(r)
+    reps = max(1, args.steps // R)
+    secs, _ = time_region(torch, stream, lambda i: graph.replay(), reps, max(1, args.warmup // R))
+    steps = reps * R
+    bytes_step = sum(i4_wbytes(K, N) for _, K, N in DECODE_LAYER)
+    return {"seconds": secs, "steps": steps, "bytes_step": bytes_step,
+            "launches_step": len(DECODE_LAYER), "copies": R}
+
+
+def i4_prefill_bench(mo, torch, dev, iters=30, warmup=10):
+    out = []
+    stream = torch.cuda.Stream(dev)
+    for name, M, K, N in PREFILL:
+        w = make_i4_weights(mo, torch, K, N, 77, dev, outliers=True)
+        g = torch.Generator(device=dev).manual_seed(2)
+        x = torch.randn(M, K, generator=g, device=dev).half()
+        with torch.cuda.stream(stream):
+            mo.matmul_int4(x, *w, I4_GROUP)
+        secs, _ = time_region(torch, stream, lambda i: mo.matmul_int4(x, *w, I4_GROUP), iters, warmup)
+        t = secs / iters
+        fl = 2.0 * M * N * K
+        out.append({"name": name, "M": M, "K": K, "N": N, "ms": t * 1e3, "tflops": fl / t / 1e12})
+        del w, x
+    return out
+
+
+def i4_cpu_baseline(seconds_budget):
+    """Reference CPU path of matmul_int4 (W in X.dtype from fp32 (q - z) * s, then X @ W)."""
+    import numpy as np
+    import torch
+
+    from oracle import int4_ref as ref
+
+    K, N = 4096, 4096
+    rng = np.random.default_rng(0)
+    W = (rng.standard_normal((K, N)) * 0.02).astype(np.float16).astype(np.float32)
+    packed, s, z = ref.quantize(W, I4_GROUP, ref.F16)
+    X = torch.from_numpy(rng.standard_normal((1, K)).astype(np.float16))
+    ref.fallback_torch_cpu(X, packed, s, z, I4_GROUP)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        ref.fallback_torch_cpu(X, packed, s, z, I4_GROUP)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds_budget or n >= 10000:
+            break
+    per = el / n
+    return {
+        "value": i4_wbytes(K, N) / per / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"O-proj K=N=4096 M=1 fp16, group 128 fp16 scales/zeros: dequantize + X@W per "
+                  f"call (quantization.py:220-239), numpy + torch CPU, {n} calls in {el:.1f}s "
+                  f"({per * 1e3:.2f} ms/call)",
+    }
+
+
 def cpu_baseline(seconds_budget):
     """Reference CPU path (dequant to fp16 each call, then X @ W) on the O-proj shape."""
     import numpy as np
@@ -232,6 +332,16 @@ def run_part(mo, torch, dev, args):
                           "us_per_launch": round(t / dec["launches_step"] * 1e6, 3),
                           "weight_bytes_per_launch": dec["bytes_step"] / dec["launches_step"]}),
               flush=True)
+    elif args.part == "int4-decode":
+        dec = i4_decode_bench(mo, torch, dev, args)
+        t = dec["seconds"] / dec["steps"]
+        print(json.dumps({"part": "int4-decode", "GB/s": round(dec["bytes_step"] / t / 1e9, 1),
+                          "us_per_launch": round(t / dec["launches_step"] * 1e6, 3),
+                          "weight_bytes_per_launch": dec["bytes_step"] / dec["launches_step"]}),
+              flush=True)
+    elif args.part == "int4-prefill":
+        print(json.dumps({"part": "int4-prefill", "configs": i4_prefill_bench(mo, torch, dev)}),
+              flush=True)
     else:
         print(json.dumps({"part": "prefill", "configs": prefill_bench(mo, torch, dev)}), flush=True)
 
@@ -264,9 +374,15 @@ def main():
     pre = prefill_bench(mo, torch, dev)
     pre_up = pre[0]
 
-    cpu = None
+    i4_dec = i4_decode_bench(mo, torch, dev, args)
+    i4_t = i4_dec["seconds"] / i4_dec["steps"]
+    i4_gbs = i4_dec["bytes_step"] / i4_t / 1e9
+    i4_pre = i4_prefill_bench(mo, torch, dev)
+
+    cpu = i4_cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_seconds)
+        i4_cpu = i4_cpu_baseline(args.cpu_seconds / 2)
 
     line = {
         "metric": "q4_0 GEMV GB/s (% HBM peak) at M=1; q4_0 GEMM TFLOP/s (% MFMA) at M=2048",
@@ -317,6 +433,38 @@ def main():
             },
         },
         "cpu_baseline": cpu,
+        "int4": {
+            "workload": "same decode layer and prefill shapes, per-group INT4 (group 128, fp16 "
+                        "scales/zeros; quantization.py:26-239)",
+            "decode_gbs": round(i4_gbs, 1),
+            "decode_ms_per_step": round(i4_t * 1e3, 5),
+            "bytes_per_step": i4_dec["bytes_step"],
+            "roofline": {
+                "bound": "hbm",
+                "achieved": round(i4_gbs, 1),
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": round(i4_gbs / HBM_PEAK_GBS, 4),
+                "traffic": I4_DECODE_TRAFFIC_BYTES,
+                "algorithmic_bytes_per_launch": i4_dec["bytes_step"] // i4_dec["launches_step"],
+                "kernel": "i4_gemv_kernel (decode GEMV, M=1)",
+                "avg_launch_us": round(i4_t / i4_dec["launches_step"] * 1e6, 3),
+            },
+            "prefill": {
+                "configs": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in p.items()}
+                            for p in i4_pre],
+                "roofline": {
+                    "bound": "mfma",
+                    "achieved": round(i4_pre[0]["tflops"], 1),
+                    "peak": FP16_PEAK_TFLOPS,
+                    "unit": "TFLOP/s",
+                    "frac": round(i4_pre[0]["tflops"] / FP16_PEAK_TFLOPS, 4),
+                    "traffic": I4_PREFILL_UP_TRAFFIC_BYTES,
+                    "kernel": "i4_gemm_kernel (M=2048 K=4096 N=14336)",
+                },
+            },
+            "cpu_baseline": i4_cpu,
+        },
     }
     print(json.dumps(line), flush=True)
 

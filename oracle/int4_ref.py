@@ -155,3 +155,14 @@ def matmul_f64(X, packed, scales, zeros, group_size: int = DEFAULT_GROUP):
                 acc += X[m, k] * w
             Y[m, n] = acc
     return Y
+
+
+def fallback_torch_cpu(X, packed, scales, zeros, group_size: int = DEFAULT_GROUP):
+    """The reference's CPU path for matmul_int4 (quantization.py:220-239): build
+    W in X.dtype from ((q - zero) * scale) in fp32, then ``X @ W`` with torch on
+    the CPU.  The row loop of the reference is vectorised here (same values);
+    used as the CPU baseline of the benchmark."""
+    import torch
+    W = dequantize(packed, scales, zeros, group_size, F32)
+    Wt = torch.from_numpy(W).to(X.dtype)
+    return X @ Wt
