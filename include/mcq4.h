@@ -158,6 +158,52 @@ int mcq4_matmul_int4_gelu(const void *X, int x_dtype, int64_t ldx, const uint8_t
                           int64_t ldy, int64_t M, int64_t K, int64_t N, int64_t group_size,
                           void *workspace, size_t workspace_bytes, void *stream);
 
+/*
+ * GPU-side quantize_to_int4 (binding native/core_mps.mm:4655-4700, kernel
+ * native/quant_kernels.metal:634-686): the quantize_int4 computation in fp32
+ * with round-half-away-from-zero (Metal round()).  W fp32 [K][ldw];
+ * packed [K/2][N]; scales, zeros fp32 [ceil(K/group_size)][N]; group_size even.
+ */
+int mcq4_quantize_to_int4(const float *W, int64_t ldw, int64_t K, int64_t N, int64_t group_size,
+                          uint8_t *packed, float *scales, float *zeros, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Per-group INT8 (quantization.py:242-286; Metal binding matmul_int8_metal,
+ * native/core_mps.mm:4516-4565): W int8 [K][N] (row stride N),
+ * W[k][n] = (q - zeros[k/group_size][n]) * scales[k/group_size][n].
+ * ------------------------------------------------------------------------- */
+size_t mcq4_matmul_int8_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
+                                        int x_dtype);
+
+/* Y[M][ldy] = X[M][ldx] @ dequant(W), fp32 accumulation, X and Y in x_dtype.
+ * fp16 activations with group_size % 16 == 0, K % 16 == 0 and N % 8 == 0 run
+ * the MFMA GEMV (M <= 16); K and group_size % 32 == 0 with N % 128 == 0 the
+ * MFMA GEMM; everything else the general fp32 kernel. */
+int mcq4_matmul_int8(const void *X, int x_dtype, int64_t ldx, const int8_t *W, const void *scales,
+                     const void *zeros, int sz_dtype, void *Y, int64_t ldy, int64_t M, int64_t K,
+                     int64_t N, int64_t group_size, void *workspace, size_t workspace_bytes,
+                     void *stream);
+
+/* Workspace bytes of mcq4_fused_rmsnorm_linear_int4: the matmul's own
+ * workspace (zero-filled counter area first, same conventions), then the
+ * normalized fp16 activations after it. */
+size_t mcq4_fused_rmsnorm_linear_int4_workspace_bytes(int64_t M, int64_t K, int64_t N,
+                                                      int64_t group_size);
+
+/*
+ * fused_rmsnorm_linear_int4 (native/core_mps.mm:3017-3103): Y = matmul_int4(
+ * rmsnorm(X, w_norm, eps), packed, scales, zeros) with X [M][ldx] fp16, w_norm
+ * [K] fp16, Y [M][ldy] fp16.  RMSNorm as native/training_kernels.metal:425-488:
+ * rstd = 1/sqrt(sum(x^2)/K + eps) in fp32, X_norm = fp16(x * rstd * w_norm),
+ * written to the workspace behind the matmul's share (workspace 256-byte
+ * aligned), then the INT4 matmul on the same stream.
+ */
+int mcq4_fused_rmsnorm_linear_int4(const void *X, int64_t ldx, const void *w_norm, float eps,
+                                   const uint8_t *packed, const void *scales, const void *zeros,
+                                   int sz_dtype, void *Y, int64_t ldy, int64_t M, int64_t K,
+                                   int64_t N, int64_t group_size, void *workspace,
+                                   size_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

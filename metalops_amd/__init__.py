@@ -19,10 +19,13 @@ from .quantization import (
 from .int4 import (
     Int4Linear,
     dequantize_int4,
+    fused_rmsnorm_linear_int4,
     matmul_int4,
     matmul_int4_gelu,
     matmul_int4_silu,
+    matmul_int8,
     quantize_int4,
+    quantize_to_int4,
 )
 
 __version__ = "1.1.0"
@@ -39,5 +42,8 @@ __all__ = [
     "matmul_int4",
     "matmul_int4_silu",
     "matmul_int4_gelu",
+    "fused_rmsnorm_linear_int4",
+    "quantize_to_int4",
+    "matmul_int8",
     "Int4Linear",
 ]

@@ -41,6 +41,13 @@ SIGNATURES = {
                                      _i64, _i64, _p, _sz, _p]),
     "mcq4_matmul_int4_gelu": (_int, [_p, _int, _i64, _p, _p, _p, _int, _p, _i64, _i64, _i64,
                                      _i64, _i64, _p, _sz, _p]),
+    "mcq4_quantize_to_int4": (_int, [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
+    "mcq4_matmul_int8_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _int]),
+    "mcq4_matmul_int8": (_int, [_p, _int, _i64, _p, _p, _p, _int, _p, _i64, _i64, _i64, _i64,
+                                _i64, _p, _sz, _p]),
+    "mcq4_fused_rmsnorm_linear_int4_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "mcq4_fused_rmsnorm_linear_int4": (_int, [_p, _i64, _p, ctypes.c_float, _p, _p, _p, _int, _p,
+                                              _i64, _i64, _i64, _i64, _i64, _p, _sz, _p]),
 }
 
 

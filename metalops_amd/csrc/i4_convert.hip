@@ -12,6 +12,10 @@
 // an even row's q waits in a register for the odd row, and the byte is stored
 // once.  Loads and stores are coalesced across the threads (columns).
 //
+// The GPU-side quantizer quantize_to_int4 (native/quant_kernels.metal:634-686,
+// binding core_mps.mm:4655-4700) is the same computation in fp32 with Metal's
+// round() (half away from zero); `away` selects it.
+//
 // dequantize (quantization.py:139-151): one thread per packed byte:
 // w = R_out(((float)q - zero) * scale) for its two rows.
 #include <math.h>
@@ -25,6 +29,7 @@ struct I4QuantArgs {
     int w_dt;
     int64_t ldw, K, N, gs, G;
     int64_t gpt;               // groups per thread (1, or G for odd group sizes)
+    int away;                  // 1: round half away from zero (Metal round()), 0: half to even
     uint8_t *packed;
     void *scales, *zeros;
 };
@@ -55,8 +60,10 @@ __global__ void __launch_bounds__(256) i4_quantize_kernel(I4QuantArgs a) {
             for (int64_t k = k0; k < k1; ++k) {
                 const float w = load_dt(a.W, k * a.ldw + n, dt);
                 const float t = round_dt(round_dt(w / scale, dt) + zero, dt);
-                // rintf: half to even; fmaxf/fminf map NaN to the bound 0.
-                const uint32_t q = (uint32_t)fminf(fmaxf(rintf(t), 0.0f), 15.0f);
+                // rintf: half to even; roundf: half away from zero; fmaxf/fminf
+                // map NaN to the bound 0.
+                const float r = a.away ? roundf(t) : rintf(t);
+                const uint32_t q = (uint32_t)fminf(fmaxf(r, 0.0f), 15.0f);
                 if ((k & 1) == 0) {
                     pending = q;
                 } else {
@@ -96,8 +103,9 @@ __global__ void __launch_bounds__(256) i4_dequant_kernel(I4DequantArgs a) {
 
 hipError_t launch_i4_quantize(const void *W, int w_dt, int64_t ldw, int64_t K, int64_t N,
                               int64_t gs, uint8_t *packed, void *scales, void *zeros,
-                              hipStream_t s) {
+                              hipStream_t s, int away) {
     I4QuantArgs a;
+    a.away = away;
     a.W = W; a.w_dt = w_dt; a.ldw = ldw; a.K = K; a.N = N; a.gs = gs;
     a.G = (K + gs - 1) / gs;
     a.gpt = gs % 2 == 0 ? 1 : a.G;

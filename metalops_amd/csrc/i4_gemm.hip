@@ -1,4 +1,7 @@
-// Prefill-shaped (M > 16) per-group INT4 matmul on gfx950: barrier-free MFMA GEMM.
+// Prefill-shaped (M > 16) per-group INT4 / INT8 matmul on gfx950: barrier-free
+// MFMA GEMM.  The description is for INT4; INT8 (int8 [K][N], quantization.py
+// :242-286) differs only in the raw step (32 byte rows, four copies) and the
+// unpack (byte pairs of rows 2r, 2r+1 -> fp16 1152 + q).
 //
 //   * WG = 256 threads = 4 waves in a 2x2 grid; WG tile BM x 256 (BM = 256 or
 //     128); wave tile (BM/2) x 128 of v_mfma_f32_32x32x16_f16 tiles, fp32
@@ -27,6 +30,7 @@
 //
 // MFMA 32x32 output layout: lane l holds D[8*(r/4) + 4*(l/32) + r%4][l%32], r = 0..15.
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "i4_common.h"
@@ -36,8 +40,17 @@ namespace mcq4 {
 constexpr int I4G_BN = 256;
 constexpr int I4G_P = 3;                       // steps in flight ahead of the MFMAs
 constexpr int I4G_R = I4G_P + 1;               // raw ring slots per wave
-constexpr int I4G_RAW = 16 * 128;              // raw bytes per wave and step
-constexpr int I4G_SLOT = I4G_RAW + 1024;       // + scales/zeros of 128 columns (fp32)
+
+// Per weight format (WB = bits per weight): 32 K per step either way; INT4 packs
+// two rows per byte (16 byte rows per step), INT8 one (32 rows).
+template <int WB>
+struct I4gFmt {
+    static constexpr int ROWS = WB == 4 ? 16 : 32;          // byte rows per step
+    static constexpr int RAW = ROWS * 128;                   // raw bytes per wave and step
+    static constexpr int SLOT = RAW + 1024;                  // + scales/zeros of 128 columns (fp32)
+    static constexpr int COPIES = RAW / 1024;                // global_load_lds_dwordx4 per step
+    static constexpr size_t LDS = (size_t)4 * I4G_R * SLOT;  // 4 waves
+};
 
 struct I4GemmArgs {
     const _Float16 *X;
@@ -52,14 +65,17 @@ struct I4GemmArgs {
     float *partials;     // [tiles][S][BM*256] when S > 1
 };
 
-template <int BM, int SZ, int ACT>
+template <int BM, int SZ, int ACT, int WB>
 __global__ void __launch_bounds__(256, 1)
 i4_gemm_kernel(I4GemmArgs a) {
+    constexpr int I4G_RAW = I4gFmt<WB>::RAW, I4G_SLOT = I4gFmt<WB>::SLOT;
+    constexpr int ROWS = I4gFmt<WB>::ROWS, COPIES = I4gFmt<WB>::COPIES;
+    constexpr int RPL = ROWS / 4;                // byte rows per lane and K half (4 or 8)
     constexpr int WM = BM / 2, WN = I4G_BN / 2;
     constexpr int TM = WM / 32, TN = WN / 32;   // TN = 4
     static_assert(TN == 4, "four 32-column tiles per wave");
     constexpr int A_LD = 2 * TM;
-    constexpr int GROUP = A_LD + 3;             // vector-memory instructions per step
+    constexpr int GROUP = A_LD + COPIES + 1;    // vector-memory instructions per step
     static_assert((I4G_P - 1) * GROUP < 64, "vmcnt range");
     constexpr int ESZ = SZ == DT_F32 ? 4 : 2;
     constexpr int SZ_LANES = 128 * ESZ / 16;    // lanes per scale (or zero) row copy
@@ -94,7 +110,7 @@ i4_gemm_kernel(I4GemmArgs a) {
     uint8_t *ring = smem + wave * (I4G_R * I4G_SLOT);
     const int wcol = n0 + wn * WN;
     const bool wcols = wcol < N;                 // whole wave past N: copy column 0 instead
-    const uint8_t *w_base = a.P + (int64_t)k_lo * 16 * N + (int64_t)(lane >> 3) * N +
+    const uint8_t *w_base = a.P + (int64_t)k_lo * ROWS * N + (int64_t)(lane >> 3) * N +
                             (wcols ? wcol : 0) + 16 * (lane & 7);
     // Scale/zero copy: lanes 0..SZ_LANES-1 copy the scale row, the next
     // SZ_LANES lanes the zero row (16 bytes each) of the wave's 128 columns.
@@ -112,10 +128,10 @@ i4_gemm_kernel(I4GemmArgs a) {
                 dst[ks][i] = *(const half8_t *)(a_src[i] + (int64_t)k * 32 + 16 * ks);
     };
     auto copy_raw = [&](int k) {
-        const uint8_t *src = w_base + (int64_t)k * 16 * N;
+        const uint8_t *src = w_base + (int64_t)k * ROWS * N;
         uint8_t *dst = ring + (k % I4G_R) * I4G_SLOT;
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
+        for (int c = 0; c < COPIES; ++c)
             __builtin_amdgcn_global_load_lds(
                 (void *)(src + (int64_t)8 * c * N),
                 (__attribute__((address_space(3))) void *)(dst + 1024 * c), 16, 0, 0);
@@ -128,11 +144,13 @@ i4_gemm_kernel(I4GemmArgs a) {
 
     const uint32_t c64 = opaque_vgpr(0x64006400u);
     const uint32_t mlo = opaque_sgpr(0x000F000Fu);
-    const half2_t m1024 = {(_Float16)-1024.0f, (_Float16)-1024.0f};
+    // fp16 value of code 0 in the unpacked pair: 1024 (INT4) or 1152 (INT8, q + 128).
+    const half2_t m1024 = WB == 4 ? half2_t{(_Float16)-1024.0f, (_Float16)-1024.0f}
+                                  : half2_t{(_Float16)-1152.0f, (_Float16)-1152.0f};
     // B source of a step: the lane's eight raw dwords and the fp16 scale and
     // offset pairs of its four columns.
     struct BSrc {
-        uint32_t raw[2][4];
+        uint32_t raw[2][RPL];
         half2_t s2[4], c2[4];
     };
     auto fetch_b = [&](int k, BSrc &b) {
@@ -140,8 +158,8 @@ i4_gemm_kernel(I4GemmArgs a) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                b.raw[ks][r] = *(const lds_u32 *)(Rs + (8 * ks + 4 * lhi + r) * 128 + 4 * lrow);
+            for (int r = 0; r < RPL; ++r)
+                b.raw[ks][r] = *(const lds_u32 *)(Rs + (2 * RPL * ks + RPL * lhi + r) * 128 + 4 * lrow);
         float s[4], zz[4];
         typedef __attribute__((address_space(3))) float4_t lds_f4;
         typedef __attribute__((address_space(3))) u32x2 lds_u2;
@@ -180,8 +198,17 @@ i4_gemm_kernel(I4GemmArgs a) {
             uint4_t d;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const uint32_t w = b.raw[ks][r];
-                const half2_t q = bitcast<half2_t>(and_or(__builtin_amdgcn_perm(w >> 4, w, sel), mlo, c64)) + m1024;
+                uint32_t pair;
+                if constexpr (WB == 4) {
+                    const uint32_t w = b.raw[ks][r];
+                    pair = and_or(__builtin_amdgcn_perm(w >> 4, w, sel), mlo, c64);
+                } else {
+                    // bytes of K rows 2r, 2r+1 to positions 0 and 2; the xor flips
+                    // the sign bit (q + 128) and sets the 0x64 exponent bytes.
+                    const uint32_t sel8 = (uint32_t)j | 0x0Cu << 8 | (uint32_t)(4 + j) << 16 | 0x0Cu << 24;
+                    pair = __builtin_amdgcn_perm(b.raw[ks][2 * r + 1], b.raw[ks][2 * r], sel8) ^ 0x64806480u;
+                }
+                const half2_t q = bitcast<half2_t>(pair) + m1024;
                 d[r] = bitcast<uint32_t>(__builtin_elementwise_fma(q, b.s2[j], b.c2[j]));
             }
             bv[ks] = bitcast<half8_t>(d);
@@ -333,10 +360,24 @@ i4_gemm_reduce_kernel(I4GemmArgs a) {
     *(half4_t *)((_Float16 *)a.Y + (int64_t)m * a.ldy + n) = v;
 }
 
-template <int BM, int SZ, int ACT>
+template <int BM, int SZ, int ACT, int WB>
 static hipError_t launch_i4g(const I4GemmArgs &a, hipStream_t s) {
-    constexpr size_t lds = (size_t)4 * I4G_R * I4G_SLOT;
-    hipLaunchKernelGGL((i4_gemm_kernel<BM, SZ, ACT>), dim3(a.tiles_m * a.tiles_n, 1, a.S),
+    constexpr size_t lds = I4gFmt<WB>::LDS;
+    if (lds > 64 * 1024) {
+        // Raise the kernel's dynamic-LDS limit once per device.
+        static std::atomic<uint64_t> done{0};
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        const uint64_t bit = 1ull << (dev & 63);
+        if (!(done.load(std::memory_order_acquire) & bit)) {
+            e = hipFuncSetAttribute((const void *)i4_gemm_kernel<BM, SZ, ACT, WB>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+            done.fetch_or(bit, std::memory_order_acq_rel);
+        }
+    }
+    hipLaunchKernelGGL((i4_gemm_kernel<BM, SZ, ACT, WB>), dim3(a.tiles_m * a.tiles_n, 1, a.S),
                        dim3(256), lds, s, a);
     if (a.S > 1) {
         const int64_t n4 = (int64_t)a.tiles_m * a.tiles_n * (BM * I4G_BN / 4);
@@ -346,11 +387,18 @@ static hipError_t launch_i4g(const I4GemmArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int BM, int SZ>
+template <int BM, int SZ, int WB>
 static hipError_t launch_i4g_act(const I4GemmArgs &a, int act, hipStream_t s) {
-    if (act == ACT_SILU) return launch_i4g<BM, SZ, ACT_SILU>(a, s);
-    if (act == ACT_GELU) return launch_i4g<BM, SZ, ACT_GELU>(a, s);
-    return launch_i4g<BM, SZ, ACT_NONE>(a, s);
+    if (act == ACT_SILU) return launch_i4g<BM, SZ, ACT_SILU, WB>(a, s);
+    if (act == ACT_GELU) return launch_i4g<BM, SZ, ACT_GELU, WB>(a, s);
+    return launch_i4g<BM, SZ, ACT_NONE, WB>(a, s);
+}
+
+template <int BM, int WB>
+static hipError_t launch_i4g_sz(const I4GemmArgs &a, int sz_dt, int act, hipStream_t s) {
+    if (sz_dt == DT_F32) return launch_i4g_act<BM, DT_F32, WB>(a, act, s);
+    if (sz_dt == DT_F16) return launch_i4g_act<BM, DT_F16, WB>(a, act, s);
+    return launch_i4g_act<BM, DT_BF16, WB>(a, act, s);
 }
 
 // Needs N % 128 == 0 (whole 128-column wave strips),
@@ -389,7 +437,7 @@ size_t i4_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
 
 hipError_t launch_i4_gemm(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K,
-                          int N, int gs, int act, void *ws, hipStream_t s) {
+                          int N, int gs, int act, void *ws, hipStream_t s, int wb) {
     const I4GCfg c = i4_gemm_config(M, K, N);
     I4GemmArgs a;
     a.X = X; a.ldx = ldx; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y; a.ldy = ldy;
@@ -402,14 +450,12 @@ hipError_t launch_i4_gemm(const _Float16 *X, int64_t ldx, const uint8_t *P, cons
         if (!ws) return hipErrorInvalidValue;
         a.partials = (float *)((char *)ws + COUNTER_BYTES);
     }
-    if (c.bm == 256) {
-        if (sz_dt == DT_F32) return launch_i4g_act<256, DT_F32>(a, act, s);
-        if (sz_dt == DT_F16) return launch_i4g_act<256, DT_F16>(a, act, s);
-        return launch_i4g_act<256, DT_BF16>(a, act, s);
+    if (wb == 8) {
+        if (c.bm == 256) return launch_i4g_sz<256, 8>(a, sz_dt, act, s);
+        return launch_i4g_sz<128, 8>(a, sz_dt, act, s);
     }
-    if (sz_dt == DT_F32) return launch_i4g_act<128, DT_F32>(a, act, s);
-    if (sz_dt == DT_F16) return launch_i4g_act<128, DT_F16>(a, act, s);
-    return launch_i4g_act<128, DT_BF16>(a, act, s);
+    if (c.bm == 256) return launch_i4g_sz<256, 4>(a, sz_dt, act, s);
+    return launch_i4g_sz<128, 4>(a, sz_dt, act, s);
 }
 
 }  // namespace mcq4

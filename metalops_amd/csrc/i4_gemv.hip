@@ -37,6 +37,7 @@
 // column l%16, K 8(l/16)..+8; D lane l = rows 4(l/16)+i, column l%16.
 #include <algorithm>
 #include <stdlib.h>
+#include <type_traits>
 
 #include "i4_common.h"
 
@@ -121,10 +122,16 @@ template <int NC> struct WRow;
 template <> struct WRow<8> { typedef u32x2 T; };
 template <> struct WRow<4> { typedef uint32_t T; };
 
-template <int SZ, int ACT, int D, int NC>
+// WB = weight bits: 4 (packed[K/2][N], 32 K per step, 16x16x32 MFMA) or 8
+// (int8 [K][N], 16 K per step, 16x16x16 MFMA).  A step is 16 byte rows of the
+// tile in both formats.
+template <int SZ, int ACT, int D, int NC, int WB>
 __global__ void __launch_bounds__(I4vShape<NC>::IW * 64)
 i4_gemv_kernel(I4GemvArgs a) {
     constexpr int IW = I4vShape<NC>::IW, TC = I4vShape<NC>::TC, SLOT = I4vShape<NC>::SLOT;
+    constexpr int KS = WB == 4 ? 32 : 16;                // K per step
+    constexpr float OFF = WB == 4 ? 1024.0f : 1152.0f;  // fp16 value of code 0 in the B operand
+    typedef typename std::conditional<WB == 4, uint4_t, u32x2>::type xv_t;
     typedef typename WRow<NC>::T wrow_t;
     __shared__ __attribute__((aligned(16))) uint8_t smem[I4vShape<NC>::LDS];
     const int tid = threadIdx.x;
@@ -172,15 +179,15 @@ i4_gemv_kernel(I4GemvArgs a) {
         const int ncol = col0 + NC * c < N ? col0 + NC * c : 0;
         const uint8_t *wbase = a.P + (int64_t)(s_begin * 16 + 4 * g) * N + ncol;
         const int m = min(c, a.M - 1);
-        const _Float16 *xbase = a.X + (int64_t)m * a.ldx + (int64_t)s_begin * 32 + 8 * g;
+        const _Float16 *xbase = a.X + (int64_t)m * a.ldx + (int64_t)s_begin * KS + (KS / 4) * g;
         wrow_t wr[D][4];
-        uint4_t xr[D];
-        auto load_step = [&](int j, wrow_t (&w)[4], uint4_t &x) {
+        xv_t xr[D];
+        auto load_step = [&](int j, wrow_t (&w)[4], xv_t &x) {
             const uint8_t *p = wbase + (int64_t)j * 16 * N;
 #pragma unroll
             for (int r = 0; r < 4; ++r)
                 w[r] = __builtin_nontemporal_load((const wrow_t *)(p + (int64_t)r * N));
-            x = *(const uint4_t *)(xbase + (int64_t)j * 32);
+            x = *(const xv_t *)(xbase + (int64_t)j * KS);
         };
 #pragma unroll
         for (int d = 0; d < D; ++d) load_step(min(d, ns - 1), wr[d], xr[d]);
@@ -191,12 +198,35 @@ i4_gemv_kernel(I4GemvArgs a) {
         const uint32_t c64 = opaque_vgpr(0x64006400u);
         const uint32_t mlo = opaque_sgpr(0x000F000Fu);
         const half8_t ones = bitcast<half8_t>(uint4_t{0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u});
+        const half4_t ones4 = bitcast<half4_t>(u32x2{0x3C003C00u, 0x3C003C00u});
         const float4_t zf = {0.f, 0.f, 0.f, 0.f};
         float4_t P[NC], Ssum = zf;
 #pragma unroll
         for (int j = 0; j < NC; ++j) P[j] = zf;
 
-        auto step = [&](const wrow_t (&w)[4], const uint4_t &xv) {
+        auto step = [&](const wrow_t (&w)[4], const xv_t &xv) {
+            if constexpr (WB == 8) {
+                // int8: B pair of K rows 2p, 2p+1 (p = 0, 1) for column NC*c + j:
+                // bytes to positions 0 and 2, then the xor flips the sign bit
+                // (q + 128) and sets the 0x64 exponent bytes: fp16 1152 + q.
+                const half4_t x = bitcast<half4_t>(xv);
+#pragma unroll
+                for (int j = 0; j < NC; ++j) {
+                    const int h = j >> 2, b = j & 3;
+                    const uint32_t sel = (uint32_t)b | 0x0Cu << 8 | (uint32_t)(4 + b) << 16 | 0x0Cu << 24;
+                    u32x2 bq;
+#pragma unroll
+                    for (int p = 0; p < 2; ++p) {
+                        uint32_t r0, r1;
+                        if constexpr (NC == 8) { r0 = w[2 * p][h]; r1 = w[2 * p + 1][h]; }
+                        else { r0 = w[2 * p]; r1 = w[2 * p + 1]; }
+                        bq[p] = __builtin_amdgcn_perm(r1, r0, sel) ^ 0x64806480u;
+                    }
+                    P[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(x, bitcast<half4_t>(bq), P[j], 0, 0, 0);
+                }
+                Ssum = __builtin_amdgcn_mfma_f32_16x16x16f16(x, ones4, Ssum, 0, 0, 0);
+                return;
+            } else {
             const half8_t x = bitcast<half8_t>(xv);
             uint32_t lo[4][NC / 4], hi[4][NC / 4];
 #pragma unroll
@@ -219,13 +249,14 @@ i4_gemv_kernel(I4GemvArgs a) {
                 P[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x, bitcast<half8_t>(bq), P[j], 0, 0, 0);
             }
             Ssum = __builtin_amdgcn_mfma_f32_16x16x32_f16(x, ones, Ssum, 0, 0, 0);
+            }
         };
         auto flush = [&](int gl) {
             float sv[NC], zv[NC];
             i4v_load_sz<SZ, NC>(lds_ptr(lds_addr(szw + gl * SLOT)), c, sv, zv);
 #pragma unroll
             for (int j = 0; j < NC; ++j) {
-                const float zz = -(1024.0f + zv[j]);
+                const float zz = -(OFF + zv[j]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float tq = __builtin_fmaf(zz, Ssum[i], P[j][i]);
@@ -375,8 +406,8 @@ struct I4GemvCfg {
 // at about half the bandwidth of 128-byte pieces on MI355X, so it is slower);
 // MCQ4_I4_SPW / MCQ4_I4_SPLIT force the steps per wave / split count;
 // MCQ4_I4_RED=kernel sums splits in a second kernel instead of the ticket.
-static I4GemvCfg i4_gemv_config(int64_t K, int64_t N, int64_t gs) {
-    const int64_t nsteps = K / 32, spg = gs / 32;
+static I4GemvCfg i4_gemv_config(int64_t K, int64_t N, int64_t gs, int ks) {
+    const int64_t nsteps = K / ks, spg = gs / ks;
     const int64_t loose = (I4V_GMAX - 1) * spg;          // any alignment
     auto fit = [&](int64_t w) {
         if (w <= loose) return w;
@@ -405,27 +436,29 @@ static I4GemvCfg i4_gemv_config(int64_t K, int64_t N, int64_t gs) {
     return {nc, (int)spw, (int)S};
 }
 
+// wb = weight bits (4: packed[K/2][N]; 8: int8 [K][N]).
 bool i4_gemv_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
-                       const void *P, const void *scales, const void *zeros) {
-    return M >= 1 && M <= 16 && K % 32 == 0 && gs % 32 == 0 && N % 8 == 0 &&
+                       const void *P, const void *scales, const void *zeros, int wb) {
+    const int ks = wb == 4 ? 32 : 16;
+    return M >= 1 && M <= 16 && K % ks == 0 && gs % ks == 0 && N % 8 == 0 &&
            (N + 63) / 64 <= COUNTER_SLOTS && ldx % 8 == 0 && ((uintptr_t)X % 16) == 0 &&
            ((uintptr_t)P % 8) == 0 && ((uintptr_t)scales % 16) == 0 &&
            ((uintptr_t)zeros % 16) == 0 && K / 32 < (1 << 24);
 }
 
-size_t i4_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs) {
-    const I4GemvCfg c = i4_gemv_config(K, N, gs);
+size_t i4_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs, int wb) {
+    const I4GemvCfg c = i4_gemv_config(K, N, gs, wb == 4 ? 32 : 16);
     if (c.S == 1) return 0;
     const int64_t tc = 16 * c.nc;
     return COUNTER_BYTES + (size_t)((N + tc - 1) / tc) * c.S * M * tc * sizeof(float);
 }
 
-template <int SZ, int D, int NC>
+template <int SZ, int D, int NC, int WB>
 static hipError_t launch_gemv_sz(const I4GemvArgs &a, int ntiles, int act, hipStream_t s) {
     const dim3 grid(ntiles, a.S), block(I4vShape<NC>::IW * 64);
-    if (act == ACT_SILU) hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_SILU, D, NC>), grid, block, 0, s, a);
-    else if (act == ACT_GELU) hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_GELU, D, NC>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_NONE, D, NC>), grid, block, 0, s, a);
+    if (act == ACT_SILU) hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_SILU, D, NC, WB>), grid, block, 0, s, a);
+    else if (act == ACT_GELU) hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_GELU, D, NC, WB>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_NONE, D, NC, WB>), grid, block, 0, s, a);
     if (a.S > 1 && !a.counters) {
         constexpr int tc = I4vShape<NC>::TC;
         const int64_t n = (int64_t)ntiles * a.M * tc;
@@ -437,20 +470,21 @@ static hipError_t launch_gemv_sz(const I4GemvArgs &a, int ntiles, int act, hipSt
     return hipGetLastError();
 }
 
-template <int NC>
+template <int NC, int WB>
 static hipError_t launch_gemv_nc(const I4GemvArgs &a, int ntiles, int sz_dt, int act, hipStream_t s) {
-    if (sz_dt == DT_F32) return launch_gemv_sz<DT_F32, 4, NC>(a, ntiles, act, s);
-    if (sz_dt == DT_F16) return launch_gemv_sz<DT_F16, 4, NC>(a, ntiles, act, s);
-    return launch_gemv_sz<DT_BF16, 4, NC>(a, ntiles, act, s);
+    if (sz_dt == DT_F32) return launch_gemv_sz<DT_F32, 4, NC, WB>(a, ntiles, act, s);
+    if (sz_dt == DT_F16) return launch_gemv_sz<DT_F16, 4, NC, WB>(a, ntiles, act, s);
+    return launch_gemv_sz<DT_BF16, 4, NC, WB>(a, ntiles, act, s);
 }
 
 hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K,
-                          int N, int gs, int act, void *ws, hipStream_t s) {
-    const I4GemvCfg c = i4_gemv_config(K, N, gs);
+                          int N, int gs, int act, void *ws, hipStream_t s, int wb) {
+    const int ks = wb == 4 ? 32 : 16;
+    const I4GemvCfg c = i4_gemv_config(K, N, gs, ks);
     I4GemvArgs a;
     a.X = X; a.ldx = ldx; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y; a.ldy = ldy;
-    a.M = M; a.N = N; a.nsteps = K / 32; a.spg = gs / 32;
+    a.M = M; a.N = N; a.nsteps = K / ks; a.spg = gs / ks;
     a.spw = c.spw; a.S = c.S;
     a.part = nullptr; a.counters = nullptr;
     if (c.S > 1) {
@@ -460,8 +494,12 @@ hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, cons
         if (!(red && red[0] == 'k')) a.counters = (uint32_t *)ws;
     }
     const int ntiles = (N + 16 * c.nc - 1) / (16 * c.nc);
-    if (c.nc == 8) return launch_gemv_nc<8>(a, ntiles, sz_dt, act, s);
-    return launch_gemv_nc<4>(a, ntiles, sz_dt, act, s);
+    if (wb == 8) {
+        if (c.nc == 8) return launch_gemv_nc<8, 8>(a, ntiles, sz_dt, act, s);
+        return launch_gemv_nc<4, 8>(a, ntiles, sz_dt, act, s);
+    }
+    if (c.nc == 8) return launch_gemv_nc<8, 4>(a, ntiles, sz_dt, act, s);
+    return launch_gemv_nc<4, 4>(a, ntiles, sz_dt, act, s);
 }
 
 }  // namespace mcq4

@@ -20,27 +20,29 @@
 namespace mcq4 {
 hipError_t launch_i4_quantize(const void *W, int w_dt, int64_t ldw, int64_t K, int64_t N,
                               int64_t gs, uint8_t *packed, void *scales, void *zeros,
-                              hipStream_t s);
+                              hipStream_t s, int away);
 hipError_t launch_i4_dequant(const uint8_t *packed, const void *scales, const void *zeros,
                              int sz_dt, int64_t K, int64_t N, int64_t gs, void *out,
                              int64_t ldo, int out_dt, hipStream_t s);
 hipError_t launch_i4_generic(const void *X, int x_dt, int64_t ldx, const uint8_t *packed,
                              const void *scales, const void *zeros, int sz_dt, void *Y,
                              int64_t ldy, int64_t M, int64_t K, int64_t N, int64_t gs, int act,
-                             hipStream_t s);
+                             hipStream_t s, int wb);
 bool i4_gemv_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
-                       const void *P, const void *scales, const void *zeros);
-size_t i4_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs);
+                       const void *P, const void *scales, const void *zeros, int wb);
+size_t i4_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs, int wb);
 hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K,
-                          int N, int gs, int act, void *ws, hipStream_t s);
+                          int N, int gs, int act, void *ws, hipStream_t s, int wb);
 bool i4_gemm_supported(int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
                        const void *P, const void *scales, const void *zeros, const void *Y,
                        int64_t ldy);
 size_t i4_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N);
 hipError_t launch_i4_gemm(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K,
-                          int N, int gs, int act, void *ws, hipStream_t s);
+                          int N, int gs, int act, void *ws, hipStream_t s, int wb);
+hipError_t launch_i4_rmsnorm(const _Float16 *X, int64_t ldx, const _Float16 *w, float eps, int M,
+                             int K, _Float16 *out, int64_t ldo, hipStream_t s);
 // Records the message returned by mcq4_last_error (mcq4_capi.cpp); returns code.
 int set_error(int code, const char *msg);
 }  // namespace mcq4
@@ -78,32 +80,40 @@ int check_kng(int64_t K, int64_t N, int64_t gs) {
 enum class I4Path { Generic, Gemv, Gemm };
 I4Path i4_path(const void *X, int x_dt, int64_t ldx, const uint8_t *P, const void *s,
                const void *z, const void *Y, int64_t ldy, int64_t M, int64_t K, int64_t N,
-               int64_t gs) {
+               int64_t gs, int wb) {
     if (const char *env = getenv("MCQ4_I4_PATH"))
         if (env[0] == 'g') return I4Path::Generic;
     if (x_dt != MCQ4_DTYPE_F16) return I4Path::Generic;
-    if (M <= 16) return mcq4::i4_gemv_supported(M, K, N, gs, X, ldx, P, s, z) ? I4Path::Gemv
-                                                                              : I4Path::Generic;
+    if (M <= 16) return mcq4::i4_gemv_supported(M, K, N, gs, X, ldx, P, s, z, wb) ? I4Path::Gemv
+                                                                                  : I4Path::Generic;
     return mcq4::i4_gemm_supported(K, N, gs, X, ldx, P, s, z, Y, ldy) ? I4Path::Gemm
                                                                      : I4Path::Generic;
 }
 
-size_t ws_bytes(int64_t M, int64_t K, int64_t N, int64_t gs, int x_dt) {
-    if (M <= 0 || K <= 0 || N <= 0 || gs <= 0 || K % 32 || gs % 32 || x_dt != MCQ4_DTYPE_F16)
+// Upper bound over the kernels a shape can take (the general kernel needs none).
+size_t ws_bytes(int64_t M, int64_t K, int64_t N, int64_t gs, int x_dt, int wb = 4) {
+    const int ks = wb == 4 ? 32 : 16;
+    if (M <= 0 || K <= 0 || N <= 0 || gs <= 0 || K % ks || gs % ks || x_dt != MCQ4_DTYPE_F16)
         return 0;
-    if (M <= 16) return mcq4::i4_gemv_workspace_bytes(M, K, N, gs);
+    if (M <= 16) return mcq4::i4_gemv_workspace_bytes(M, K, N, gs, wb);
+    if (K % 32 || gs % 32) return 0;
     return mcq4::i4_gemm_workspace_bytes(M, K, N);
 }
 
 int matmul_common(int act, const void *X, int x_dtype, int64_t ldx, const uint8_t *packed,
                   const void *scales, const void *zeros, int sz_dtype, void *Y, int64_t ldy,
                   int64_t M, int64_t K, int64_t N, int64_t gs, void *workspace,
-                  size_t workspace_bytes, void *stream) {
+                  size_t workspace_bytes, void *stream, int wb = 4) {
     if (!X || !packed || !scales || !zeros || !Y) return fail(MCQ4_ERR_INVALID_ARG, "null pointer");
     if (!valid_dt(x_dtype) || !valid_dt(sz_dtype))
         return fail(MCQ4_ERR_INVALID_ARG, "x_dtype / sz_dtype must be MCQ4_DTYPE_F32, F16 or BF16");
     if (M <= 0 || M > kMaxDim) return fail(MCQ4_ERR_SHAPE, "M (%lld) out of range", (long long)M);
-    if (int st = check_kng(K, N, gs)) return st;
+    if (wb == 4) {
+        if (int st = check_kng(K, N, gs)) return st;
+    } else if (K <= 0 || N <= 0 || gs <= 0 || K > kMaxDim || N > kMaxDim || K * N > ((int64_t)1 << 40)) {
+        return fail(MCQ4_ERR_SHAPE, "K=%lld N=%lld group_size=%lld out of range", (long long)K,
+                    (long long)N, (long long)gs);
+    }
     if ((M + 7) / 8 > 65535) return fail(MCQ4_ERR_SHAPE, "M (%lld) too large", (long long)M);
     if (ldx < K) return fail(MCQ4_ERR_SHAPE, "ldx (%lld) < K (%lld)", (long long)ldx, (long long)K);
     if (ldy < N) return fail(MCQ4_ERR_SHAPE, "ldy (%lld) < N (%lld)", (long long)ldy, (long long)N);
@@ -111,8 +121,9 @@ int matmul_common(int act, const void *X, int x_dtype, int64_t ldx, const uint8_
         return fail(MCQ4_ERR_ALIGNMENT, "X and Y must be aligned to their element size");
     if (!aligned(scales, dt_size(sz_dtype)) || !aligned(zeros, dt_size(sz_dtype)))
         return fail(MCQ4_ERR_ALIGNMENT, "scales and zeros must be aligned to their element size");
-    const I4Path path = i4_path(X, x_dtype, ldx, packed, scales, zeros, Y, ldy, M, K, N, gs);
-    const size_t need = path == I4Path::Generic ? 0 : ws_bytes(M, K, N, gs, x_dtype);
+    I4Path path = i4_path(X, x_dtype, ldx, packed, scales, zeros, Y, ldy, M, K, N, gs, wb);
+    if (path == I4Path::Gemm && (K % 32 || gs % 32)) path = I4Path::Generic;
+    const size_t need = path == I4Path::Generic ? 0 : ws_bytes(M, K, N, gs, x_dtype, wb);
     if (need && (!workspace || workspace_bytes < need))
         return fail(MCQ4_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
                     workspace ? workspace_bytes : (size_t)0);
@@ -124,16 +135,16 @@ int matmul_common(int act, const void *X, int x_dtype, int64_t ldx, const uint8_
         case I4Path::Gemv:
             e = mcq4::launch_i4_gemv((const _Float16 *)X, ldx, packed, scales, zeros, sz_dtype,
                                      (_Float16 *)Y, ldy, (int)M, (int)K, (int)N, (int)gs, act,
-                                     workspace, st);
+                                     workspace, st, wb);
             break;
         case I4Path::Gemm:
             e = mcq4::launch_i4_gemm((const _Float16 *)X, ldx, packed, scales, zeros, sz_dtype,
                                      (_Float16 *)Y, ldy, (int)M, (int)K, (int)N, (int)gs, act,
-                                     workspace, st);
+                                     workspace, st, wb);
             break;
         default:
             e = mcq4::launch_i4_generic(X, x_dtype, ldx, packed, scales, zeros, sz_dtype, Y, ldy,
-                                        M, K, N, gs, act, st);
+                                        M, K, N, gs, act, st, wb);
             break;
     }
     return hip_status(e, "int4 matmul launch");
@@ -156,8 +167,37 @@ int mcq4_quantize_int4(const void *W, int w_dtype, int64_t ldw, int64_t K, int64
     if (!aligned(W, es) || !aligned(scales, es) || !aligned(zeros, es))
         return fail(MCQ4_ERR_ALIGNMENT, "W, scales and zeros must be aligned to their element size");
     return hip_status(mcq4::launch_i4_quantize(W, w_dtype, ldw, K, N, group_size, packed, scales,
-                                               zeros, (hipStream_t)stream),
+                                               zeros, (hipStream_t)stream, 0),
                       "int4 quantize launch");
+}
+
+int mcq4_quantize_to_int4(const float *W, int64_t ldw, int64_t K, int64_t N, int64_t group_size,
+                          uint8_t *packed, float *scales, float *zeros, void *stream) {
+    fail(MCQ4_OK, "");
+    if (!W || !packed || !scales || !zeros) return fail(MCQ4_ERR_INVALID_ARG, "null pointer");
+    if (int st = check_kng(K, N, group_size)) return st;
+    if (group_size % 2)
+        return fail(MCQ4_ERR_SHAPE, "group_size (%lld) must be even", (long long)group_size);
+    if (ldw < N) return fail(MCQ4_ERR_SHAPE, "ldw (%lld) < N (%lld)", (long long)ldw, (long long)N);
+    if (!aligned(W, 4) || !aligned(scales, 4) || !aligned(zeros, 4))
+        return fail(MCQ4_ERR_ALIGNMENT, "W, scales and zeros must be 4-byte aligned");
+    return hip_status(mcq4::launch_i4_quantize(W, MCQ4_DTYPE_F32, ldw, K, N, group_size, packed,
+                                               scales, zeros, (hipStream_t)stream, 1),
+                      "quantize_to_int4 launch");
+}
+
+size_t mcq4_matmul_int8_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t group_size,
+                                        int x_dtype) {
+    return ws_bytes(M, K, N, group_size, x_dtype, 8);
+}
+
+int mcq4_matmul_int8(const void *X, int x_dtype, int64_t ldx, const int8_t *W, const void *scales,
+                     const void *zeros, int sz_dtype, void *Y, int64_t ldy, int64_t M, int64_t K,
+                     int64_t N, int64_t group_size, void *workspace, size_t workspace_bytes,
+                     void *stream) {
+    fail(MCQ4_OK, "");
+    return matmul_common(0, X, x_dtype, ldx, (const uint8_t *)W, scales, zeros, sz_dtype, Y, ldy,
+                         M, K, N, group_size, workspace, workspace_bytes, stream, 8);
 }
 
 int mcq4_dequantize_int4(const uint8_t *packed, const void *scales, const void *zeros,
@@ -207,6 +247,52 @@ int mcq4_matmul_int4_gelu(const void *X, int x_dtype, int64_t ldx, const uint8_t
     fail(MCQ4_OK, "");
     return matmul_common(2, X, x_dtype, ldx, packed, scales, zeros, sz_dtype, Y, ldy, M, K, N,
                          group_size, workspace, workspace_bytes, stream);
+}
+
+// Workspace layout: the matmul's own workspace (its zero-filled 256 KiB counter
+// area first, then split-K partials), then X_norm (M x K fp16) from
+// max(matmul workspace, 256 KiB) on, so the counter area is never written with
+// activations and one zero-filled buffer keeps serving every entry point.
+constexpr size_t kCounterArea = (size_t)65536 * 4;
+static size_t norm_offset(int64_t M, int64_t K, int64_t N, int64_t gs) {
+    const size_t w = std::max(ws_bytes(M, K, N, gs, MCQ4_DTYPE_F16), kCounterArea);
+    return (w + 255) / 256 * 256;
+}
+
+size_t mcq4_fused_rmsnorm_linear_int4_workspace_bytes(int64_t M, int64_t K, int64_t N,
+                                                      int64_t group_size) {
+    if (M <= 0 || K <= 0 || N <= 0 || group_size <= 0) return 0;
+    return norm_offset(M, K, N, group_size) + (size_t)M * K * 2;
+}
+
+int mcq4_fused_rmsnorm_linear_int4(const void *X, int64_t ldx, const void *w_norm, float eps,
+                                   const uint8_t *packed, const void *scales, const void *zeros,
+                                   int sz_dtype, void *Y, int64_t ldy, int64_t M, int64_t K,
+                                   int64_t N, int64_t group_size, void *workspace,
+                                   size_t workspace_bytes, void *stream) {
+    fail(MCQ4_OK, "");
+    if (!X || !w_norm || !packed || !scales || !zeros || !Y)
+        return fail(MCQ4_ERR_INVALID_ARG, "null pointer");
+    if (M <= 0 || M > kMaxDim) return fail(MCQ4_ERR_SHAPE, "M (%lld) out of range", (long long)M);
+    if (int st = check_kng(K, N, group_size)) return st;
+    if (M > 65535 * 8) return fail(MCQ4_ERR_SHAPE, "M (%lld) too large", (long long)M);
+    if (ldx < K) return fail(MCQ4_ERR_SHAPE, "ldx (%lld) < K (%lld)", (long long)ldx, (long long)K);
+    if (!aligned(X, 2) || !aligned(w_norm, 2))
+        return fail(MCQ4_ERR_ALIGNMENT, "X and w_norm must be 2-byte aligned (fp16)");
+    const size_t need = mcq4_fused_rmsnorm_linear_int4_workspace_bytes(M, K, N, group_size);
+    if (!workspace || workspace_bytes < need)
+        return fail(MCQ4_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                    workspace ? workspace_bytes : (size_t)0);
+    if (!aligned(workspace, 256)) return fail(MCQ4_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
+    _Float16 *xn = (_Float16 *)((char *)workspace + norm_offset(M, K, N, group_size));
+    if (int st = hip_status(mcq4::launch_i4_rmsnorm((const _Float16 *)X, ldx,
+                                                    (const _Float16 *)w_norm, eps, (int)M, (int)K,
+                                                    xn, K, (hipStream_t)stream),
+                            "rmsnorm launch"))
+        return st;
+    // The matmul validates the rest (scales/zeros, Y, its own workspace share).
+    return matmul_common(0, xn, MCQ4_DTYPE_F16, K, packed, scales, zeros, sz_dtype, Y, ldy, M, K,
+                         N, group_size, workspace, norm_offset(M, K, N, group_size), stream);
 }
 
 }  // extern "C"

@@ -8,6 +8,11 @@ Mirrors metalcore's per-group INT4 API
 * ``matmul_int4(X, W_packed, scales, zeros, group_size=128)``     -- :156-239
 * ``matmul_int4_silu`` / ``matmul_int4_gelu`` (the native bindings of
   ``native/core_mps.mm:5780-5914``, registered at :6936-6937)
+* ``fused_rmsnorm_linear_int4`` (native binding ``core_mps.mm:3017-3103``,
+  registered at :6885)
+* ``quantize_to_int4(weight, group_size)`` (GPU-side quantizer binding,
+  ``native/core_mps.mm:4655-4700``, registered at :6887)
+* ``matmul_int8(X, W_packed, scales, zeros, group_size=128)``     -- :242-286
 * ``Int4Linear``                                                  -- :457-613
 
 Same names, argument order, defaults, layouts (``W_packed [K/2, N]`` uint8,
@@ -32,6 +37,9 @@ __all__ = [
     "matmul_int4",
     "matmul_int4_silu",
     "matmul_int4_gelu",
+    "fused_rmsnorm_linear_int4",
+    "quantize_to_int4",
+    "matmul_int8",
     "Int4Linear",
 ]
 
@@ -99,6 +107,38 @@ def quantize_int4(
                                                group_size, packed.data_ptr(), scales.data_ptr(),
                                                zeros.data_ptr(), _stream(w.device)),
                    "mcq4_quantize_int4")
+    return packed, scales, zeros
+
+
+def quantize_to_int4(weight: torch.Tensor, group_size: int = 128):
+    """GPU-side INT4 quantization (the reference's native ``quantize_to_int4``).
+
+    The ``quantize_int4`` computation in fp32 with Metal's ``round`` (half away
+    from zero), as quant_kernels.metal:634-686; scales and zeros are fp32.  The
+    reference kernel reads the weight as fp32 (core_mps.mm:4671-4677), so other
+    dtypes are upcast first.  K and the group size must be even.
+    """
+    if weight.dim() != 2:
+        raise RuntimeError("weight must be 2D [K, N]")
+    K, N = weight.shape
+    if K % 2:
+        raise RuntimeError("K must be even for INT4 packing")
+    if group_size % 2:
+        raise RuntimeError(f"group_size ({group_size}) must be even")
+    _require_device(weight)
+    w = weight.float()
+    if w.stride(1) != 1 or w.stride(0) < N or w.data_ptr() % 4:
+        w = w.contiguous()
+    G = (K + group_size - 1) // group_size
+    packed = torch.empty((K // 2, N), dtype=torch.uint8, device=w.device)
+    scales = torch.empty((G, N), dtype=torch.float32, device=w.device)
+    zeros = torch.empty((G, N), dtype=torch.float32, device=w.device)
+    if K and N:
+        with torch.cuda.device(w.device):
+            _lib.check(_lib.lib.mcq4_quantize_to_int4(w.data_ptr(), w.stride(0), K, N, group_size,
+                                                      packed.data_ptr(), scales.data_ptr(),
+                                                      zeros.data_ptr(), _stream(w.device)),
+                       "mcq4_quantize_to_int4")
     return packed, scales, zeros
 
 
@@ -230,6 +270,97 @@ def matmul_int4_silu(X, W_packed, scales, zeros, group_size: int = 128) -> torch
 def matmul_int4_gelu(X, W_packed, scales, zeros, group_size: int = 128) -> torch.Tensor:
     """``gelu(X @ dequant(W))`` (tanh form, as the fused reference kernel) fused into the store."""
     return _fused(X, W_packed, scales, zeros, group_size, 2)
+
+
+def fused_rmsnorm_linear_int4(X, W_norm, W_packed, scales, zeros, eps, group_size):
+    """``matmul_int4(rmsnorm(X, W_norm, eps), W_packed, scales, zeros, group_size)`` (fp16).
+
+    RMSNorm as the reference's half kernel (training_kernels.metal:425-488):
+    ``rstd = 1/sqrt(mean(x^2) + eps)`` in fp32, ``X_norm = fp16(x * rstd * w)``;
+    the normalization kernel and the INT4 matmul run back to back on the current
+    stream with ``X_norm`` in the shared workspace.  ``X`` is ``[B, K]`` fp16 and
+    ``W_norm`` ``[K]`` fp16, as the reference binding requires (core_mps.mm:3029).
+    """
+    if X.dtype != torch.float16:
+        raise RuntimeError("Fused kernel requires half precision")
+    if X.dim() != 2:
+        raise RuntimeError(f"X must be [B, K], got shape {tuple(X.shape)}")
+    _require_device(X, W_norm, W_packed, scales, zeros)
+    K, N = _check_shapes(W_packed, scales, zeros, group_size)
+    if X.shape[1] != K or W_norm.numel() != K:
+        raise RuntimeError(f"X [B, {X.shape[1]}] and W_norm [{W_norm.numel()}] must match K={K}")
+    x = X if (X.stride(1) == 1 and X.data_ptr() % 2 == 0) else X.contiguous()
+    wn = W_norm.to(torch.float16).contiguous()
+    s, z = _sz_pair(scales, zeros)
+    p = _dense(W_packed, 16)
+    M = x.shape[0]
+    Y = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    if M == 0:
+        return Y
+    need = int(_lib.lib.mcq4_fused_rmsnorm_linear_int4_workspace_bytes(M, K, N, group_size))
+    stream = _stream(x.device)
+    ws = _workspace.get(x.device, stream, need + 256)
+    base = (ws.data_ptr() + 255) // 256 * 256
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.lib.mcq4_fused_rmsnorm_linear_int4(
+            x.data_ptr(), x.stride(0), wn.data_ptr(), float(eps), p.data_ptr(), s.data_ptr(),
+            z.data_ptr(), _DT[s.dtype], Y.data_ptr(), N, M, K, N, group_size, base,
+            ws.numel() - (base - ws.data_ptr()), stream),
+            "mcq4_fused_rmsnorm_linear_int4")
+    return Y
+
+
+def matmul_int8(
+    X: torch.Tensor,
+    W_packed: torch.Tensor,
+    scales: torch.Tensor,
+    zeros: torch.Tensor,
+    group_size: int = 128,
+) -> torch.Tensor:
+    """``Y = X @ dequant(W)`` with int8 weights ``W_packed [K, N]`` (quantization.py:242-286).
+
+    ``W[k, n] = (q - zero) * scale`` per group of ``group_size`` rows; fp32
+    accumulation, result in ``X``'s dtype.  fp16 activations run the MFMA
+    kernels, other dtypes the general kernel (weights rounded to ``X``'s dtype
+    as the reference's fallback builds ``W`` in ``X.dtype``).
+    """
+    _require_device(X, W_packed, scales, zeros)
+    if X.dim() != 2:
+        raise RuntimeError(f"X must be [M, K], got shape {tuple(X.shape)}")
+    if W_packed.dtype not in (torch.int8, torch.uint8):
+        raise RuntimeError("W_packed must be int8 [K, N]")
+    K, N = W_packed.shape
+    G = (K + group_size - 1) // group_size
+    if tuple(scales.shape) != (G, N) or tuple(zeros.shape) != (G, N):
+        raise RuntimeError(f"scales/zeros must be [{G}, {N}] for K={K}, group_size={group_size}")
+    if X.shape[1] != K:
+        raise RuntimeError(f"X K dim ({X.shape[1]}) must match weight K ({K})")
+    out_dtype = X.dtype
+    x = X if X.dtype in _DT else X.float()
+    if x.stride(1) != 1 or x.stride(0) < K or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = _dense(x, 16)
+    M = x.shape[0]
+    s, z = _sz_pair(scales, zeros)
+    w = _dense(W_packed.view(torch.int8), 16)
+    Y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    if M and N:
+        if K == 0:
+            Y.zero_()
+        else:
+            xdt = _DT[x.dtype]
+            need = int(_lib.lib.mcq4_matmul_int8_workspace_bytes(M, K, N, group_size, xdt))
+            stream = _stream(x.device)
+            ws_ptr, ws_bytes = None, 0
+            if need:
+                ws = _workspace.get(x.device, stream, need)
+                ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+            with torch.cuda.device(x.device):
+                _lib.check(_lib.lib.mcq4_matmul_int8(x.data_ptr(), xdt, x.stride(0), w.data_ptr(),
+                                                     s.data_ptr(), z.data_ptr(), _DT[s.dtype],
+                                                     Y.data_ptr(), N, M, K, N, group_size, ws_ptr,
+                                                     ws_bytes, stream),
+                           "mcq4_matmul_int8")
+    return Y if Y.dtype == out_dtype else Y.to(out_dtype)
 
 
 class Int4Linear(nn.Module):

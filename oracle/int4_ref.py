@@ -77,8 +77,13 @@ def from_bf16_bits(b: np.ndarray) -> np.ndarray:
     return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
-def quantize(weight: np.ndarray, group_size: int = DEFAULT_GROUP, dtype: str = F32):
-    """Restates quantization.py:49-92.
+def quantize(weight: np.ndarray, group_size: int = DEFAULT_GROUP, dtype: str = F32,
+             rounding: str = "even"):
+    """Restates quantization.py:49-92 (``rounding="even"``: torch.round).
+
+    ``rounding="away"`` with fp32 gives the GPU-side quantizer quantize_to_int4
+    (quant_kernels.metal:634-686: the same fp32 steps, Metal round() = half
+    away from zero; even group sizes).
 
     ``weight`` holds values representable in ``dtype`` (as fp32).  Returns
     ``(packed uint8 [K/2, N], scales fp32 [G, N], zeros fp32 [G, N])``; scales
@@ -104,7 +109,8 @@ def quantize(weight: np.ndarray, group_size: int = DEFAULT_GROUP, dtype: str = F
             zero = R(-mn / scale)                                         # :76
             scales[g], zeros[g] = scale, zero
             t = R(R(grp / scale) + zero)                                  # :83
-            q_all[k0:k1] = np.clip(np.round(t), 0, 15).astype(np.uint8)   # half to even
+            r = np.round(t) if rounding == "even" else np.sign(t) * np.floor(np.abs(t) + 0.5)
+            q_all[k0:k1] = np.clip(np.nan_to_num(r, nan=0.0), 0, 15).astype(np.uint8)
     packed = (q_all[0::2] | (q_all[1::2] << 4)).astype(np.uint8)          # :85-90
     return packed, scales, zeros
 
@@ -166,3 +172,53 @@ def fallback_torch_cpu(X, packed, scales, zeros, group_size: int = DEFAULT_GROUP
     W = dequantize(packed, scales, zeros, group_size, F32)
     Wt = torch.from_numpy(W).to(X.dtype)
     return X @ Wt
+
+
+def rmsnorm_f16(X, w, eps):
+    """RMSNorm of fused_rmsnorm_linear_int4 (training_kernels.metal:425-488):
+    rstd = 1/sqrt(sum(x^2)/K + eps) per row, X_norm = fp16((x * rstd) * w), with
+    fp16 inputs.  The sum is taken in float64 here (the kernels' fp32 sums differ
+    in the last bits, which can move an fp16 result by one ulp)."""
+    x = np.asarray(X, dtype=np.float16).astype(np.float32)
+    wf = np.asarray(w, dtype=np.float16).astype(np.float32)
+    ss = (x.astype(np.float64) ** 2).sum(axis=1)
+    rstd = (1.0 / np.sqrt(ss / x.shape[1] + eps)).astype(np.float32)
+    return ((x * rstd[:, None]).astype(np.float32) * wf).astype(np.float16)
+
+
+# ---- per-group INT8 (quantization.py:242-286) ----------------------------------
+
+def dequantize_int8(W_q, scales, zeros, group_size: int = DEFAULT_GROUP, out: str = F32):
+    """``W = (q.float() - zero) * scale`` per group of rows (quantization.py:276-284)."""
+    q = np.asarray(W_q, dtype=np.int8).astype(np.float32)
+    K = q.shape[0]
+    g = np.arange(K) // group_size
+    s = np.asarray(scales, dtype=np.float32)[g]
+    z = np.asarray(zeros, dtype=np.float32)[g]
+    with np.errstate(over="ignore", invalid="ignore"):
+        w = ((q - z).astype(np.float32) * s).astype(np.float32)
+    return round_to(w, out)
+
+
+def matmul_int8_f32(X, W_q, scales, zeros, group_size: int = DEFAULT_GROUP):
+    """``X.float() @ dequant_int8_f32(W)``: the tolerance reference."""
+    X = np.asarray(X, dtype=np.float32)
+    W = dequantize_int8(W_q, scales, zeros, group_size, F32)
+    return (X.astype(np.float64) @ W.astype(np.float64)).astype(np.float32)
+
+
+def matmul_int8_f64(X, W_q, scales, zeros, group_size: int = DEFAULT_GROUP):
+    """Brute-force float64 loops on tiny shapes."""
+    q = np.asarray(W_q, dtype=np.int8)
+    X = np.asarray(X, dtype=np.float64)
+    M, K = X.shape
+    N = q.shape[1]
+    Y = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            acc = 0.0
+            for k in range(K):
+                g = k // group_size
+                acc += X[m, k] * (float(q[k, n]) - float(zeros[g, n])) * float(scales[g, n])
+            Y[m, n] = acc
+    return Y

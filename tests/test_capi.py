@@ -143,3 +143,25 @@ def test_int4_workspace_sizes():
     for M, K, N in ((1, 4096, 4096), (16, 14336, 4096), (128, 4096, 4096)):
         ws = L.mcq4_matmul_int4_workspace_bytes(M, K, N, 128, F16)
         assert ws == 0 or ws > 256 * 1024
+
+
+def test_int8_and_fused_validation_codes():
+    L = _lib.lib
+    F32, F16 = _lib.MCQ4_DTYPE_F32, _lib.MCQ4_DTYPE_F16
+    X, P, S, Z, Y, W = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000, 0x60000
+    m8 = L.mcq4_matmul_int8
+    assert m8(None, F16, 64, P, S, Z, F32, Y, 8, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert m8(X, F16, 64, P, S, Z, F32, Y, 8, 1, 0, 8, 32, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert m8(X, F16, 32, P, S, Z, F32, Y, 8, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert m8(X + 1, F16, 64, P, S, Z, F32, Y, 8, 1, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_ALIGNMENT
+    q = L.mcq4_quantize_to_int4
+    assert q(None, 8, 64, 8, 32, P, S, Z, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert q(X, 8, 64, 8, 33, P, S, Z, None) == _lib.MCQ4_ERR_SHAPE
+    assert q(X + 2, 8, 64, 8, 32, P, S, Z, None) == _lib.MCQ4_ERR_ALIGNMENT
+    f = L.mcq4_fused_rmsnorm_linear_int4
+    need = L.mcq4_fused_rmsnorm_linear_int4_workspace_bytes(4, 64, 8, 32)
+    assert need >= 256 * 1024 + 4 * 64 * 2
+    assert f(None, 64, W, 1e-6, P, S, Z, F16, Y, 8, 4, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert f(X, 64, W, 1e-6, P, S, Z, F16, Y, 8, 4, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_WORKSPACE
+    assert f(X, 32, W, 1e-6, P, S, Z, F16, Y, 8, 4, 64, 8, 32, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+    assert f(X, 64, W, 1e-6, P, S, Z, F16, Y, 8, 4, 64, 8, 32, 0x70080, need, None) == _lib.MCQ4_ERR_ALIGNMENT  # 128-, not 256-aligned

@@ -262,3 +262,83 @@ def test_int4_linear(mo, dev, dequant_on_load):
     _check_rows(y2.reshape(28, 256).float().detach().cpu().numpy(), ref)
     q.dequantize()
     assert "fast_fp16" in q.extra_repr()
+
+
+@pytest.mark.parametrize("M,K,N,gs,sz", [(1, 4096, 4096, 128, R.F16), (4, 1024, 768, 64, R.F32),
+                                         (16, 2048, 512, 128, R.F16), (64, 512, 256, 128, R.F16),
+                                         (300, 1024, 512, 32, R.F32), (3, 256, 200, 128, R.F16)])
+def test_fused_rmsnorm_linear_int4(mo, dev, M, K, N, gs, sz):
+    """Y = matmul_int4(rmsnorm(X, w, eps)) against the oracle's fp16 X_norm and matmul."""
+    print(f"fused rmsnorm+int4 M={M} K={K} N={N} gs={gs} sz={sz}", flush=True)
+    w, packed, s, z = _quant(mo, dev, K, N, gs, sz, seed=40 + M)
+    g = torch.Generator().manual_seed(M)
+    X = (torch.randn(M, K, generator=g) * 3).half()
+    wn = (1 + 0.1 * torch.randn(K, generator=g)).half()
+    Y = mo.fused_rmsnorm_linear_int4(X.to(dev), wn.to(dev), packed, s, z, 1e-5, gs)
+    assert Y.dtype == torch.float16 and tuple(Y.shape) == (M, N)
+    xn = R.rmsnorm_f16(X.numpy(), wn.numpy(), 1e-5)
+    Yref = R.matmul_f32(xn.astype(np.float32), packed.cpu().numpy(), s.float().cpu().numpy(),
+                        z.float().cpu().numpy(), gs)
+    _check_rows(Y.float().cpu().numpy(), Yref)
+    # the plain matmul afterwards still sees a clean workspace (split-K counters)
+    X2 = torch.randn(1, K, generator=g).half().to(dev)
+    _check_rows(mo.matmul_int4(X2, packed, s, z, gs).float().cpu().numpy(), _ref(X2, packed, s, z, gs))
+
+
+def test_fused_rmsnorm_requires_half(mo, dev):
+    w, packed, s, z = _quant(mo, dev, 64, 16, 32)
+    with pytest.raises(RuntimeError, match="half precision"):
+        mo.fused_rmsnorm_linear_int4(torch.zeros(2, 64, device=dev), torch.ones(64, device=dev),
+                                     packed, s, z, 1e-6, 32)
+
+
+# ---- GPU-side quantize_to_int4 and INT8 matmul ----------------------------------
+
+@pytest.mark.parametrize("K,N,gs", [(256, 96, 128), (96, 40, 64), (4096, 512, 128), (24, 10, 2)])
+def test_quantize_to_int4_bit_exact(mo, dev, K, N, gs):
+    w = _weights(K, N, K + 3 * N)
+    packed, s, z = mo.quantize_to_int4(torch.from_numpy(w).to(dev), gs)
+    rp, rs, rz = R.quantize(w, gs, R.F32, rounding="away")
+    assert s.dtype == torch.float32
+    np.testing.assert_array_equal(packed.cpu().numpy(), rp)
+    assert _bits_equal(s.cpu().numpy(), rs) and _bits_equal(z.cpu().numpy(), rz)
+
+
+def _int8_weights(K, N, gs, sz, seed):
+    rng = np.random.default_rng(seed)
+    q = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    G = (K + gs - 1) // gs
+    s = R.round_to(rng.uniform(0.0005, 0.005, (G, N)).astype(np.float32), sz)
+    z = R.round_to(rng.uniform(-20, 20, (G, N)).astype(np.float32), sz)
+    return q, s, z
+
+
+I8_CASES = [
+    (1, 4096, 4096, 128), (3, 1024, 392, 16), (16, 2048, 1024, 64), (8, 48, 24, 16),
+    (1, 14336, 512, 128),
+    (17, 512, 256, 128), (128, 4096, 1024, 128), (300, 1024, 768, 32), (512, 1024, 2048, 128),
+    (40, 256, 200, 128), (5, 100, 21, 25),
+]
+
+
+@pytest.mark.parametrize("M,K,N,gs", I8_CASES)
+@pytest.mark.parametrize("sz", [R.F32, R.F16])
+def test_matmul_int8_fp16(mo, dev, M, K, N, gs, sz):
+    print(f"matmul_int8 fp16 M={M} K={K} N={N} gs={gs} sz={sz}", flush=True)
+    q, s, z = _int8_weights(K, N, gs, sz, M + K + N)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).half()
+    Y = mo.matmul_int8(X.to(dev), torch.from_numpy(q).to(dev),
+                       torch.from_numpy(s).to(TDT[sz]).to(dev), torch.from_numpy(z).to(TDT[sz]).to(dev), gs)
+    assert Y.dtype == torch.float16 and tuple(Y.shape) == (M, N)
+    _check_rows(Y.float().cpu().numpy(), R.matmul_int8_f32(X.float().numpy(), q, s, z, gs))
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+def test_matmul_int8_other_dtypes(mo, dev, xdt):
+    M, K, N, gs = 6, 512, 136, 64
+    q, s, z = _int8_weights(K, N, gs, R.F32, 1)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(2)).to(xdt)
+    Y = mo.matmul_int8(X.to(dev), torch.from_numpy(q).to(dev), torch.from_numpy(s).to(dev),
+                       torch.from_numpy(z).to(dev), gs)
+    assert Y.dtype == xdt
+    _check_rows(Y.float().cpu().numpy(), R.matmul_int8_f32(X.float().numpy(), q, s, z, gs))

@@ -210,3 +210,69 @@ def test_matmul_batched_shape():
     Y = R.matmul_f32(X, packed, s, z, 32)
     assert Y.shape == (2, 3, 8)
     np.testing.assert_allclose(Y[1], R.matmul_f64(X[1], packed, s, z, 32), rtol=1e-5, atol=1e-5)
+
+
+# ---- RMSNorm prologue of fused_rmsnorm_linear_int4 ------------------------------
+
+def test_rmsnorm_closed_forms():
+    """Constant rows: x * rstd = c / sqrt(c^2 + eps); a zero row stays zero."""
+    K = 64
+    X = np.zeros((3, K), np.float16)
+    X[0] = 2.0
+    X[1] = -0.5
+    w = np.full(K, 1.5, np.float16)
+    got = R.rmsnorm_f16(X, w, 1e-6)
+    assert np.all(got[2] == 0)
+    for r, c in ((0, 2.0), (1, -0.5)):
+        want = np.float16(c / np.sqrt(c * c + 1e-6) * 1.5)
+        assert np.all(np.abs(got[r].astype(np.float32) - np.float32(want)) <= 2 ** -10 * 1.5)
+
+
+def test_rmsnorm_matches_torch_functional():
+    """torch.nn.functional.rms_norm in float64 (an independent implementation),
+    rounded to fp16 once, agrees within one fp16 ulp."""
+    rng = np.random.default_rng(0)
+    X = (rng.normal(0, 1, (5, 256)) * rng.uniform(0.1, 10, (5, 1))).astype(np.float16)
+    w = rng.normal(1, 0.1, 256).astype(np.float16)
+    got = R.rmsnorm_f16(X, w, 1e-5).astype(np.float64)
+    ref = torch.nn.functional.rms_norm(torch.from_numpy(X.astype(np.float64)), (256,),
+                                       torch.from_numpy(w.astype(np.float64)), eps=1e-5)
+    ref = ref.numpy()
+    ulp = np.abs(ref.astype(np.float16).astype(np.float64)) * 2.0 ** -10 + 2.0 ** -24
+    assert np.all(np.abs(got - ref) <= ulp)
+
+
+# ---- GPU-side quantizer rounding (quantize_to_int4) and INT8 --------------------
+
+def test_quantize_away_rounding_ties():
+    """quantize_to_int4 rounds half away from zero (Metal round()): with scale 0.125
+    and zero 0 the codes of 0.5, 1.5, 2.5, 3.5 are 1, 2, 3, 4 (torch.round: 0, 2, 2, 4)."""
+    w = np.array([0.0, 1.875, 0.0625, 0.1875, 0.3125, 0.4375, 0.5625, 1.8125], np.float32)
+    packed, s, z = R.quantize(w[:, None], 8, rounding="away")
+    np.testing.assert_array_equal(R.unpack(packed)[:, 0], [0, 15, 1, 2, 3, 4, 5, 15])
+    # away and even agree everywhere except on exact ties
+    rng = np.random.default_rng(2)
+    w2 = rng.normal(0, 1, (256, 9)).astype(np.float32)
+    pa = R.unpack(R.quantize(w2, 64, rounding="away")[0]).astype(int)
+    pe = R.unpack(R.quantize(w2, 64)[0]).astype(int)
+    assert np.all(np.abs(pa - pe) <= 1) and np.mean(pa != pe) < 0.01
+
+
+def test_int8_dequant_known_answers():
+    q = np.array([[-128, 127], [0, -1], [5, 100]], np.int8)
+    s = np.array([[0.5, 2.0]], np.float32)
+    z = np.array([[-2.0, 1.5]], np.float32)
+    W = R.dequantize_int8(q, s, z, 4)
+    np.testing.assert_array_equal(W, [[-63.0, 251.0], [1.0, -5.0], [3.5, 197.0]])
+
+
+@pytest.mark.parametrize("M,K,N,gs", [(1, 32, 3, 16), (4, 48, 5, 32), (2, 20, 7, 3)])
+def test_int8_matmul_bruteforce(M, K, N, gs):
+    rng = np.random.default_rng(K + N)
+    q = rng.integers(-128, 128, (K, N)).astype(np.int8)
+    G = (K + gs - 1) // gs
+    s = rng.uniform(0.001, 0.02, (G, N)).astype(np.float32)
+    z = rng.uniform(-3, 3, (G, N)).astype(np.float32)
+    X = rng.normal(0, 1, (M, K)).astype(np.float32)
+    np.testing.assert_allclose(R.matmul_int8_f32(X, q, s, z, gs), R.matmul_int8_f64(X, q, s, z, gs),
+                               rtol=1e-5, atol=1e-5)
