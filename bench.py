@@ -52,10 +52,11 @@ DECODE_LAYER = [  # (name, K, N) -- Llama-2-7B projections, configs[1]
 ]
 PREFILL = [("up", 2048, 4096, 14336), ("down", 2048, 14336, 4096)]
 I4_GROUP = 128
-# HBM bytes per launch of the INT4 kernels (rocprofv3 FETCH_SIZE / WRITE_SIZE,
-# scaled as above); None until measured.
-I4_DECODE_TRAFFIC_BYTES = None
-I4_PREFILL_UP_TRAFFIC_BYTES = None
+# HBM bytes per launch of the INT4 kernels (rocprofv3 FETCH_SIZE / WRITE_SIZE over
+# bench.py --part int4-decode|int4-prefill, scaled as above; profiles/i4_gemv_llama7b_m1.md,
+# profiles/i4_gemm_llama7b_m2048.md).
+I4_DECODE_TRAFFIC_BYTES = 22276567        # average over the five projections
+I4_PREFILL_UP_TRAFFIC_BYTES = 378583965   # 307.9 MB read + 70.6 MB written
 
 
 def wbytes(K, N):
@@ -222,13 +223,17 @@ def i4_decode_bench(mo, torch, dev, args):
     with torch.cuda.stream(stream):
         one_step(0)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        for r in range(R):
-            one_step(r)
-    reps = max(1, args.steps // R)
-    secs, _ = time_region(torch, stream, lambda i: graph.replay(), reps, max(1, args.warmup // R))
-    steps = reps * R
+    if args.no_graph:
+        secs, _ = time_region(torch, stream, one_step, args.steps, args.warmup)
+        steps = args.steps
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for r in range(R):
+                one_step(r)
+        reps = max(1, args.steps // R)
+        secs, _ = time_region(torch, stream, lambda i: graph.replay(), reps, max(1, args.warmup // R))
+        steps = reps * R
     bytes_step = sum(i4_wbytes(K, N) for _, K, N in DECODE_LAYER)
     return {"seconds": secs, "steps": steps, "bytes_step": bytes_step,
             "launches_step": len(DECODE_LAYER), "copies": R}

@@ -52,7 +52,6 @@ constexpr int GV_LOADS = 3;                  // copies per item (chunks 0..143 o
 constexpr int GV_SLOT = GV_WCH * 16 + 64;    // 2304 strip bytes + read overhang
 constexpr int GV_TPW_MAX = 4;                // tiles per workgroup
 constexpr int GV_XB_MAX = 4;                 // batches per wave (K <= 16*4*8*32 = 16384)
-constexpr int GV_XW = GV_XB_MAX * GV_B * 64; // activation bytes per wave in LDS
 constexpr int GV_NT = 2;                     // cache policy of the weight copies: non-temporal
 
 struct GemvArgs {
@@ -60,6 +59,9 @@ struct GemvArgs {
     const uint8_t *W;
     _Float16 *Y;
     int nb, N, ntiles, nbt;                  // nbt = batches per tile
+    int adj;                                 // 1: a workgroup's tiles are adjacent (wg*tpw + j)
+    int tpw;                                 // tiles per workgroup (<= TPW)
+    int xw;                                  // activation bytes per wave in LDS
 };
 
 template <int R>
@@ -82,15 +84,19 @@ q4_gemv_dma_kernel(GemvArgs a) {
     const int c = lane & 15, g = lane >> 4;
     const uint32_t grow = (uint32_t)a.N * BLOCK_BYTES;
 
-    // LDS: [16 waves x R slots][16 waves x activations][partials: TPW x 16 waves x 16]
+    // LDS: [16 waves x R slots][16 waves x activations]; after the last item the
+    // ring's space holds the partials (TPW x 16 waves x 16).
     uint8_t *ring = smem + wave * (R * GV_SLOT);
-    uint8_t *xs = smem + GV_WAVES * R * GV_SLOT + wave * GV_XW;
-    float *red = (float *)(smem + GV_WAVES * (R * GV_SLOT + GV_XW));
+    uint8_t *xs = smem + GV_WAVES * R * GV_SLOT + wave * a.xw;
+    float *red = (float *)smem;
 
     const int G = (int)gridDim.x, G8 = G & ~7;
     int wg = (int)blockIdx.x;
     if (wg < G8) wg = (wg & 7) * (G8 >> 3) + (wg >> 3);
-    const int ntl = min(TPW, (a.ntiles - wg + G - 1) / G);         // >= 1 (grid <= ntiles)
+    // Tile j of this workgroup: adjacent (wg*tpw + j) or strided (wg + j*G).
+    const int ntl = a.adj ? min(a.tpw, a.ntiles - wg * a.tpw)
+                          : min(TPW, (a.ntiles - wg + G - 1) / G);   // >= 1 (grid covers ntiles)
+    auto tile = [&](int j) { return a.adj ? wg * a.tpw + j : wg + j * G; };
     const int nbm = a.nbt > wave ? (a.nbt - wave + GV_WAVES - 1) / GV_WAVES : 0;  // my batches
     const int nmine = nbm * ntl;
 
@@ -108,7 +114,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
     auto issue = [&](int m, int j, int slot) {
         const int row0 = (wave + GV_WAVES * m) * GV_B;
         const int rows = min(GV_B, a.nb - row0);
-        const uint8_t *wb = a.W + (int64_t)(wg + j * G) * GV_ROW + (int64_t)row0 * grow;
+        const uint8_t *wb = a.W + (int64_t)tile(j) * GV_ROW + (int64_t)row0 * grow;
 #pragma unroll
         for (int i = 0; i < GV_LOADS; ++i) {
             // Rows past K re-copy row 0 (valid memory, never read back).
@@ -219,6 +225,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
     }
 
     // Partials (lanes 0..15 hold column c = lane), then the ordered wave sum.
+    __syncthreads();                          // every wave is done with its ring slots
     if (lane < 16) {
 #pragma unroll
         for (int j = 0; j < TPW; ++j)
@@ -230,17 +237,19 @@ q4_gemv_dma_kernel(GemvArgs a) {
         float s = 0.f;
 #pragma unroll
         for (int w = 0; w < GV_WAVES; ++w) s += red[(j * GV_WAVES + w) * 16 + col];
-        a.Y[(wg + j * G) * 16 + col] = (_Float16)s;
+        a.Y[tile(j) * 16 + col] = (_Float16)s;
     }
 }
 
-static size_t gemv_lds_bytes(int R, int tpw) {
-    return (size_t)GV_WAVES * (R * GV_SLOT + GV_XW) + (size_t)tpw * GV_WAVES * 16 * sizeof(float);
+static size_t gemv_lds_bytes(int R, int tpw, int xw) {
+    const size_t main = (size_t)GV_WAVES * (R * GV_SLOT + xw);
+    const size_t red = (size_t)tpw * GV_WAVES * 16 * sizeof(float);
+    return main > red ? main : red;
 }
 
 template <int R, int TPW>
 static hipError_t launch_gemv_t(const GemvArgs &a, int grid, hipStream_t s) {
-    const size_t lds = gemv_lds_bytes(R, TPW);
+    const size_t lds = gemv_lds_bytes(R, TPW, a.xw);
     static std::atomic<uint64_t> done{0};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -291,7 +300,16 @@ hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int
     // (lm_head) runs more workgroups of GV_TPW_MAX tiles, backfilled as CUs free up.
     int grid = std::min(a.ntiles, 256);
     if (a.ntiles > 256 * GV_TPW_MAX) grid = (a.ntiles + GV_TPW_MAX - 1) / GV_TPW_MAX;
-    const int tpw = (a.ntiles + grid - 1) / grid;
+    int tpw = (a.ntiles + grid - 1) / grid;
+    a.adj = 0;
+    if (const char *env = getenv("MCQ4_GEMV_ADJ")) a.adj = atoi(env) != 0;
+    if (const char *env = getenv("MCQ4_GEMV_TPW")) {
+        tpw = std::max(1, std::min(GV_TPW_MAX, atoi(env)));
+        a.adj = 1;
+    }
+    if (a.adj) grid = (a.ntiles + tpw - 1) / tpw;
+    a.tpw = tpw;
+    a.xw = ((a.nbt + GV_WAVES - 1) / GV_WAVES) * GV_B * 64;       // my batches' activations
     int ring = 2;
     if (const char *env = getenv("MCQ4_GEMV_RING")) ring = std::max(1, std::min(3, atoi(env)));
     switch (ring) {
