@@ -126,7 +126,7 @@ template <> struct WRow<4> { typedef uint32_t T; };
 // (int8 [K][N], 16 K per step, 16x16x16 MFMA).  A step is 16 byte rows of the
 // tile in both formats.
 template <int SZ, int ACT, int D, int NC, int WB>
-__global__ void __launch_bounds__(I4vShape<NC>::IW * 64)
+__global__ void __launch_bounds__(I4vShape<NC>::IW * 64) __attribute__((amdgpu_waves_per_eu(3)))
 i4_gemv_kernel(I4GemvArgs a) {
     constexpr int IW = I4vShape<NC>::IW, TC = I4vShape<NC>::TC, SLOT = I4vShape<NC>::SLOT;
     constexpr int KS = WB == 4 ? 32 : 16;                // K per step
