@@ -73,8 +73,8 @@ __device__ __forceinline__ void gv_wait(int pending) {
     wait_vmcnt<0>();
 }
 
-template <int R, int TPW>
-__global__ void __launch_bounds__(GV_WAVES * 64)
+template <int R, int TPW, int NW>
+__global__ void __launch_bounds__(NW * 64)
 q4_gemv_dma_kernel(GemvArgs a) {
     static_assert(R >= 1 && R <= 3 && TPW >= 1 && TPW <= GV_TPW_MAX, "config");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -87,7 +87,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
     // LDS: [16 waves x R slots][16 waves x activations]; after the last item the
     // ring's space holds the partials (TPW x 16 waves x 16).
     uint8_t *ring = smem + wave * (R * GV_SLOT);
-    uint8_t *xs = smem + GV_WAVES * R * GV_SLOT + wave * a.xw;
+    uint8_t *xs = smem + NW * R * GV_SLOT + wave * a.xw;
     float *red = (float *)smem;
 
     const int G = (int)gridDim.x, G8 = G & ~7;
@@ -97,7 +97,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
     const int ntl = a.adj ? min(a.tpw, a.ntiles - wg * a.tpw)
                           : min(TPW, (a.ntiles - wg + G - 1) / G);   // >= 1 (grid covers ntiles)
     auto tile = [&](int j) { return a.adj ? wg * a.tpw + j : wg + j * G; };
-    const int nbm = a.nbt > wave ? (a.nbt - wave + GV_WAVES - 1) / GV_WAVES : 0;  // my batches
+    const int nbm = a.nbt > wave ? (a.nbt - wave + NW - 1) / NW : 0;  // my batches
     const int nmine = nbm * ntl;
 
     // Copy geometry per lane and copy i: strip chunk q = lane + 64 i of an item
@@ -112,7 +112,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
     }
     // Item (batch index m of this wave, tile j) into ring slot `slot`.
     auto issue = [&](int m, int j, int slot) {
-        const int row0 = (wave + GV_WAVES * m) * GV_B;
+        const int row0 = (wave + NW * m) * GV_B;
         const int rows = min(GV_B, a.nb - row0);
         const uint8_t *wb = a.W + (int64_t)tile(j) * GV_ROW + (int64_t)row0 * grow;
 #pragma unroll
@@ -138,7 +138,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
     // lane/4, piece lane%4; rows past K clamp to the last row), so they are
     // older than every weight copy and land before the first item does.
     for (int m = 0; m < nbm; ++m) {
-        const int r = min((wave + GV_WAVES * m) * GV_B + (lane >> 2), a.nb - 1);
+        const int r = min((wave + NW * m) * GV_B + (lane >> 2), a.nb - 1);
         if (lane < 32)
             __builtin_amdgcn_global_load_lds(
                 (void *)((const uint8_t *)a.X + (int64_t)r * (QK * 2) + 16 * (lane & 3)),
@@ -166,7 +166,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
 
     int k = 0, slot = 0;
     for (int m = 0; m < nbm; ++m) {
-        const int row0 = (wave + GV_WAVES * m) * GV_B;
+        const int row0 = (wave + NW * m) * GV_B;
         const int rows = min(GV_B, a.nb - row0);
         half8_t xq[GV_B];
         float4_t negs[GV_B];
@@ -229,49 +229,58 @@ q4_gemv_dma_kernel(GemvArgs a) {
     if (lane < 16) {
 #pragma unroll
         for (int j = 0; j < TPW; ++j)
-            if (j < ntl) red[(j * GV_WAVES + wave) * 16 + lane] = nbm > 0 ? acc[j] : 0.f;
+            if (j < ntl) red[(j * NW + wave) * 16 + lane] = nbm > 0 ? acc[j] : 0.f;
     }
     __syncthreads();
-    for (int v = tid; v < ntl * 16; v += GV_WAVES * 64) {
+    for (int v = tid; v < ntl * 16; v += NW * 64) {
         const int j = v >> 4, col = v & 15;
         float s = 0.f;
 #pragma unroll
-        for (int w = 0; w < GV_WAVES; ++w) s += red[(j * GV_WAVES + w) * 16 + col];
+        for (int w = 0; w < NW; ++w) s += red[(j * NW + w) * 16 + col];
         a.Y[tile(j) * 16 + col] = (_Float16)s;
     }
 }
 
-static size_t gemv_lds_bytes(int R, int tpw, int xw) {
-    const size_t main = (size_t)GV_WAVES * (R * GV_SLOT + xw);
-    const size_t red = (size_t)tpw * GV_WAVES * 16 * sizeof(float);
+static size_t gemv_lds_bytes(int R, int tpw, int xw, int nw) {
+    const size_t main = (size_t)nw * (R * GV_SLOT + xw);
+    const size_t red = (size_t)tpw * nw * 16 * sizeof(float);
     return main > red ? main : red;
 }
 
-template <int R, int TPW>
+template <int R, int TPW, int NW>
 static hipError_t launch_gemv_t(const GemvArgs &a, int grid, hipStream_t s) {
-    const size_t lds = gemv_lds_bytes(R, TPW, a.xw);
+    const size_t lds = gemv_lds_bytes(R, TPW, a.xw, NW);
     static std::atomic<uint64_t> done{0};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)q4_gemv_dma_kernel<R, TPW>,
+        e = hipFuncSetAttribute((const void *)q4_gemv_dma_kernel<R, TPW, NW>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL((q4_gemv_dma_kernel<R, TPW>), dim3(grid), dim3(GV_WAVES * 64), lds, s, a);
+    hipLaunchKernelGGL((q4_gemv_dma_kernel<R, TPW, NW>), dim3(grid), dim3(NW * 64), lds, s, a);
     return hipGetLastError();
 }
 
-template <int R>
+template <int R, int NW>
 static hipError_t launch_gemv_r(const GemvArgs &a, int grid, int tpw, hipStream_t s) {
     switch (tpw) {
-        case 1: return launch_gemv_t<R, 1>(a, grid, s);
-        case 2: return launch_gemv_t<R, 2>(a, grid, s);
-        case 3: return launch_gemv_t<R, 3>(a, grid, s);
-        default: return launch_gemv_t<R, 4>(a, grid, s);
+        case 1: return launch_gemv_t<R, 1, NW>(a, grid, s);
+        case 2: return launch_gemv_t<R, 2, NW>(a, grid, s);
+        case 3: return launch_gemv_t<R, 3, NW>(a, grid, s);
+        default: return launch_gemv_t<R, 4, NW>(a, grid, s);
+    }
+}
+
+template <int NW>
+static hipError_t launch_gemv_nw(const GemvArgs &a, int grid, int tpw, int ring, hipStream_t s) {
+    switch (ring) {
+        case 3: return launch_gemv_r<3, NW>(a, grid, tpw, s);
+        case 2: return launch_gemv_r<2, NW>(a, grid, tpw, s);
+        default: return launch_gemv_r<1, NW>(a, grid, tpw, s);
     }
 }
 
@@ -296,10 +305,15 @@ hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int
     a.ntiles = N / 16;
     a.nbt = (a.nb + GV_B - 1) / GV_B;
     *n_done = a.ntiles * 16;
-    // One 16-wave workgroup per CU and up to GV_TPW_MAX tiles each; larger N
-    // (lm_head) runs more workgroups of GV_TPW_MAX tiles, backfilled as CUs free up.
-    int grid = std::min(a.ntiles, 256);
-    if (a.ntiles > 256 * GV_TPW_MAX) grid = (a.ntiles + GV_TPW_MAX - 1) / GV_TPW_MAX;
+    // One 16-wave workgroup per CU and up to GV_TPW_MAX tiles each.  Larger N
+    // (lm_head: more than 1024 tiles) runs 8-wave workgroups of GV_TPW_MAX tiles,
+    // two per CU, backfilled as they finish (measured 56 vs 66 us at N = 128256;
+    // 16 waves stay faster on the layer shapes).  MCQ4_GEMV_WAVES=8|16 forces one.
+    int nw = a.ntiles > 256 * GV_TPW_MAX ? 8 : 16;
+    if (const char *env = getenv("MCQ4_GEMV_WAVES")) nw = atoi(env) == 8 ? 8 : 16;
+    const int per_round = nw == 16 ? 256 : 512;
+    int grid = std::min(a.ntiles, per_round);
+    if (a.ntiles > per_round * GV_TPW_MAX) grid = (a.ntiles + GV_TPW_MAX - 1) / GV_TPW_MAX;
     int tpw = (a.ntiles + grid - 1) / grid;
     a.adj = 0;
     if (const char *env = getenv("MCQ4_GEMV_ADJ")) a.adj = atoi(env) != 0;
@@ -309,14 +323,11 @@ hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int
     }
     if (a.adj) grid = (a.ntiles + tpw - 1) / tpw;
     a.tpw = tpw;
-    a.xw = ((a.nbt + GV_WAVES - 1) / GV_WAVES) * GV_B * 64;       // my batches' activations
+    a.xw = ((a.nbt + nw - 1) / nw) * GV_B * 64;                   // my batches' activations
     int ring = 2;
     if (const char *env = getenv("MCQ4_GEMV_RING")) ring = std::max(1, std::min(3, atoi(env)));
-    switch (ring) {
-        case 3: return launch_gemv_r<3>(a, grid, tpw, s);
-        case 2: return launch_gemv_r<2>(a, grid, tpw, s);
-        default: return launch_gemv_r<1>(a, grid, tpw, s);
-    }
+    if (nw == 8) return launch_gemv_nw<8>(a, grid, tpw, ring, s);
+    return launch_gemv_nw<16>(a, grid, tpw, ring, s);
 }
 
 }  // namespace mcq4
