@@ -59,8 +59,6 @@ struct GemvArgs {
     const uint8_t *W;
     _Float16 *Y;
     int nb, N, ntiles, nbt;                  // nbt = batches per tile
-    int adj;                                 // 1: a workgroup's tiles are adjacent (wg*tpw + j)
-    int tpw;                                 // tiles per workgroup (<= TPW)
     int xw;                                  // activation bytes per wave in LDS
 };
 
@@ -84,19 +82,17 @@ q4_gemv_dma_kernel(GemvArgs a) {
     const int c = lane & 15, g = lane >> 4;
     const uint32_t grow = (uint32_t)a.N * BLOCK_BYTES;
 
-    // LDS: [16 waves x R slots][16 waves x activations]; after the last item the
-    // ring's space holds the partials (TPW x 16 waves x 16).
+    // LDS: [NW waves x R slots][NW waves x activations][partials: TPW x NW waves x 16]
     uint8_t *ring = smem + wave * (R * GV_SLOT);
     uint8_t *xs = smem + NW * R * GV_SLOT + wave * a.xw;
-    float *red = (float *)smem;
+    float *red = (float *)(smem + NW * (R * GV_SLOT + a.xw));
 
     const int G = (int)gridDim.x, G8 = G & ~7;
     int wg = (int)blockIdx.x;
     if (wg < G8) wg = (wg & 7) * (G8 >> 3) + (wg >> 3);
-    // Tile j of this workgroup: adjacent (wg*tpw + j) or strided (wg + j*G).
-    const int ntl = a.adj ? min(a.tpw, a.ntiles - wg * a.tpw)
-                          : min(TPW, (a.ntiles - wg + G - 1) / G);   // >= 1 (grid covers ntiles)
-    auto tile = [&](int j) { return a.adj ? wg * a.tpw + j : wg + j * G; };
+    // Tile j of this workgroup: wg + j*G.
+    const int ntl = min(TPW, (a.ntiles - wg + G - 1) / G);         // >= 1 (grid <= ntiles)
+    auto tile = [&](int j) { return wg + j * G; };
     const int nbm = a.nbt > wave ? (a.nbt - wave + NW - 1) / NW : 0;  // my batches
     const int nmine = nbm * ntl;
 
@@ -225,7 +221,6 @@ q4_gemv_dma_kernel(GemvArgs a) {
     }
 
     // Partials (lanes 0..15 hold column c = lane), then the ordered wave sum.
-    __syncthreads();                          // every wave is done with its ring slots
     if (lane < 16) {
 #pragma unroll
         for (int j = 0; j < TPW; ++j)
@@ -242,9 +237,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
 }
 
 static size_t gemv_lds_bytes(int R, int tpw, int xw, int nw) {
-    const size_t main = (size_t)nw * (R * GV_SLOT + xw);
-    const size_t red = (size_t)tpw * nw * 16 * sizeof(float);
-    return main > red ? main : red;
+    return (size_t)nw * (R * GV_SLOT + xw) + (size_t)tpw * nw * 16 * sizeof(float);
 }
 
 template <int R, int TPW, int NW>
@@ -314,15 +307,7 @@ hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int
     const int per_round = nw == 16 ? 256 : 512;
     int grid = std::min(a.ntiles, per_round);
     if (a.ntiles > per_round * GV_TPW_MAX) grid = (a.ntiles + GV_TPW_MAX - 1) / GV_TPW_MAX;
-    int tpw = (a.ntiles + grid - 1) / grid;
-    a.adj = 0;
-    if (const char *env = getenv("MCQ4_GEMV_ADJ")) a.adj = atoi(env) != 0;
-    if (const char *env = getenv("MCQ4_GEMV_TPW")) {
-        tpw = std::max(1, std::min(GV_TPW_MAX, atoi(env)));
-        a.adj = 1;
-    }
-    if (a.adj) grid = (a.ntiles + tpw - 1) / tpw;
-    a.tpw = tpw;
+    const int tpw = (a.ntiles + grid - 1) / grid;
     a.xw = ((a.nbt + nw - 1) / nw) * GV_B * 64;                   // my batches' activations
     int ring = 2;
     if (const char *env = getenv("MCQ4_GEMV_RING")) ring = std::max(1, std::min(3, atoi(env)));

@@ -182,8 +182,7 @@ PATHS = {
     "gemv_dma_ring3": {"MCQ4_GEMV_RING": "3"},
     "gemv_dma_w8": {"MCQ4_GEMV_WAVES": "8"},
     "gemv_dma_w16": {"MCQ4_GEMV_WAVES": "16"},
-    "gemv_dma_adj2": {"MCQ4_GEMV_TPW": "2"},
-    "gemv_dma_adj3_w8": {"MCQ4_GEMV_TPW": "3", "MCQ4_GEMV_WAVES": "8"},
+
     "decode_lds_m1": {"MCQ4_GEMV_PATH": "off"},
     "gemvm": {},
     "gemvm_w8": {"MCQ4_GEMVM_WAVES": "8"},
@@ -209,8 +208,7 @@ PATH_SHAPES = {
     "gemv_dma_ring3": [(1, 352, 264), (1, 11008, 4096), (1, 4096, 12288)],
     "gemv_dma_w8": [(1, 352, 264), (1, 16384, 272), (1, 4096, 4096), (1, 11008, 2064)],
     "gemv_dma_w16": [(1, 1024, 20480), (1, 352, 16400)],
-    "gemv_dma_adj2": [(1, 352, 264), (1, 4096, 12288), (1, 16384, 272)],
-    "gemv_dma_adj3_w8": [(1, 352, 264), (1, 2048, 20496)],
+
     "decode_lds_m1": [(1, 352, 264), (1, 4096, 1032)],
     "gemvm": [(2, 32, 16), (3, 352, 264), (4, 1024, 4104), (5, 11008, 512), (8, 4096, 14336),
               (11, 2048, 1040), (16, 14336, 4096), (16, 352, 8200)],
@@ -238,7 +236,7 @@ PATH_SHAPES = {
 def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM", "MCQ4_GEMV_PATH",
               "MCQ4_GEMV_RING", "MCQ4_GEMVM_WAVES", "MCQ4_GEMM4_SPLIT", "MCQ4_GEMM4_WGM",
-              "MCQ4_GEMV_WAVES", "MCQ4_GEMV_TPW", "MCQ4_GEMV_ADJ"):
+              "MCQ4_GEMV_WAVES"):
         monkeypatch.delenv(k, raising=False)
     for k, v in PATHS[path].items():
         monkeypatch.setenv(k, v)
