@@ -37,6 +37,7 @@
 // column l%16, K 8(l/16)..+8; D lane l = rows 4(l/16)+i, column l%16.
 #include <algorithm>
 #include <stdlib.h>
+#include <atomic>
 #include <type_traits>
 
 #include "i4_common.h"
@@ -52,9 +53,9 @@ constexpr int I4V_LPS = 5;                // vector-memory loads per step
 constexpr int I4V_GMAX = 8;               // groups per wave held in LDS
 constexpr int I4V_SMAX = 16;              // K splits at most
 
-template <int NC>
+template <int NC, int IW_ = (NC == 8 ? 4 : 16)>
 struct I4vShape {
-    static constexpr int IW = NC == 8 ? 4 : 16;                 // waves per workgroup
+    static constexpr int IW = IW_;                              // waves per workgroup
     static constexpr int TC = 16 * NC;                          // tile columns
     static constexpr int SLOT = TC * 4 * 2;                     // fp32 scales + zeros of a tile row
     static constexpr int SZ_BYTES = IW * I4V_GMAX * SLOT;
@@ -125,15 +126,16 @@ template <> struct WRow<4> { typedef uint32_t T; };
 // WB = weight bits: 4 (packed[K/2][N], 32 K per step, 16x16x32 MFMA) or 8
 // (int8 [K][N], 16 K per step, 16x16x16 MFMA).  A step is 16 byte rows of the
 // tile in both formats.
-template <int SZ, int ACT, int D, int NC, int WB>
-__global__ void __launch_bounds__(I4vShape<NC>::IW * 64) __attribute__((amdgpu_waves_per_eu(3)))
+template <int SZ, int ACT, int D, int NC, int WB, int IWT>
+__global__ void __launch_bounds__(IWT * 64) __attribute__((amdgpu_waves_per_eu(3)))
 i4_gemv_kernel(I4GemvArgs a) {
-    constexpr int IW = I4vShape<NC>::IW, TC = I4vShape<NC>::TC, SLOT = I4vShape<NC>::SLOT;
+    typedef I4vShape<NC, IWT> Shape;
+    constexpr int IW = Shape::IW, TC = Shape::TC, SLOT = Shape::SLOT;
     constexpr int KS = WB == 4 ? 32 : 16;                // K per step
     constexpr float OFF = WB == 4 ? 1024.0f : 1152.0f;  // fp16 value of code 0 in the B operand
     typedef typename std::conditional<WB == 4, uint4_t, u32x2>::type xv_t;
     typedef typename WRow<NC>::T wrow_t;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[I4vShape<NC>::LDS];
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];    // Shape::LDS bytes
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -393,7 +395,7 @@ __global__ void __launch_bounds__(256) i4_gemv_reduce_kernel(I4GemvArgs a, int t
 }
 
 struct I4GemvCfg {
-    int nc, spw, S;
+    int nc, iw, spw, S;
 };
 
 // Tile shape and K split.  Default: 128-column tiles of 4 waves, K split so
@@ -414,9 +416,10 @@ static I4GemvCfg i4_gemv_config(int64_t K, int64_t N, int64_t gs, int ks) {
         return std::min<int64_t>((w + spg - 1) / spg * spg, I4V_GMAX * spg);
     };
     const char *mode = getenv("MCQ4_I4_MODE");
-    const bool wide = !(mode && mode[0] == 'n');
-    const int nc = wide ? 8 : 4;
-    const int64_t iw = wide ? 4 : 16;
+    const bool narrow = mode && mode[0] == 'n';
+    const bool wide = !narrow;
+    const int nc = narrow ? 4 : 8;
+    const int64_t iw = narrow ? 16 : 4;
     const int64_t ntiles = (N + 16 * nc - 1) / (16 * nc);
     int64_t S;
     if (wide) {
@@ -433,7 +436,7 @@ static I4GemvCfg i4_gemv_config(int64_t K, int64_t N, int64_t gs, int ks) {
     if (const char *env = getenv("MCQ4_I4_SPLIT")) S = std::max(1, std::min(I4V_SMAX, atoi(env)));
     int64_t spw = fit((nsteps + iw * S - 1) / (iw * S));
     S = (nsteps + iw * spw - 1) / (iw * spw);
-    return {nc, (int)spw, (int)S};
+    return {nc, (int)iw, (int)spw, (int)S};
 }
 
 // wb = weight bits (4: packed[K/2][N]; 8: int8 [K][N]).
@@ -453,14 +456,38 @@ size_t i4_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs, int 
     return COUNTER_BYTES + (size_t)((N + tc - 1) / tc) * c.S * M * tc * sizeof(float);
 }
 
-template <int SZ, int D, int NC, int WB>
+// Launches one instance; raises its dynamic-LDS limit once per device when the
+// shape needs more than the default 64 KiB.
+template <int SZ, int ACT, int D, int NC, int WB, int IW>
+static hipError_t launch_one(const I4GemvArgs &a, dim3 grid, hipStream_t s) {
+    constexpr size_t lds = I4vShape<NC, IW>::LDS;
+    if (lds > 64 * 1024) {
+        static std::atomic<uint64_t> done{0};
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        const uint64_t bit = 1ull << (dev & 63);
+        if (!(done.load(std::memory_order_acquire) & bit)) {
+            e = hipFuncSetAttribute((const void *)i4_gemv_kernel<SZ, ACT, D, NC, WB, IW>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) return e;
+            done.fetch_or(bit, std::memory_order_acq_rel);
+        }
+    }
+    hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT, D, NC, WB, IW>), grid, dim3(IW * 64), lds, s, a);
+    return hipSuccess;
+}
+
+template <int SZ, int D, int NC, int WB, int IW>
 static hipError_t launch_gemv_sz(const I4GemvArgs &a, int ntiles, int act, hipStream_t s) {
-    const dim3 grid(ntiles, a.S), block(I4vShape<NC>::IW * 64);
-    if (act == ACT_SILU) hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_SILU, D, NC, WB>), grid, block, 0, s, a);
-    else if (act == ACT_GELU) hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_GELU, D, NC, WB>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((i4_gemv_kernel<SZ, ACT_NONE, D, NC, WB>), grid, block, 0, s, a);
+    const dim3 grid(ntiles, a.S);
+    hipError_t e;
+    if (act == ACT_SILU) e = launch_one<SZ, ACT_SILU, D, NC, WB, IW>(a, grid, s);
+    else if (act == ACT_GELU) e = launch_one<SZ, ACT_GELU, D, NC, WB, IW>(a, grid, s);
+    else e = launch_one<SZ, ACT_NONE, D, NC, WB, IW>(a, grid, s);
+    if (e != hipSuccess) return e;
     if (a.S > 1 && !a.counters) {
-        constexpr int tc = I4vShape<NC>::TC;
+        constexpr int tc = I4vShape<NC, IW>::TC;
         const int64_t n = (int64_t)ntiles * a.M * tc;
         const dim3 rg((unsigned)((n + 255) / 256));
         if (act == ACT_SILU) hipLaunchKernelGGL((i4_gemv_reduce_kernel<ACT_SILU>), rg, dim3(256), 0, s, a, tc);
@@ -470,11 +497,11 @@ static hipError_t launch_gemv_sz(const I4GemvArgs &a, int ntiles, int act, hipSt
     return hipGetLastError();
 }
 
-template <int NC, int WB>
+template <int NC, int WB, int IW>
 static hipError_t launch_gemv_nc(const I4GemvArgs &a, int ntiles, int sz_dt, int act, hipStream_t s) {
-    if (sz_dt == DT_F32) return launch_gemv_sz<DT_F32, 4, NC, WB>(a, ntiles, act, s);
-    if (sz_dt == DT_F16) return launch_gemv_sz<DT_F16, 4, NC, WB>(a, ntiles, act, s);
-    return launch_gemv_sz<DT_BF16, 4, NC, WB>(a, ntiles, act, s);
+    if (sz_dt == DT_F32) return launch_gemv_sz<DT_F32, 4, NC, WB, IW>(a, ntiles, act, s);
+    if (sz_dt == DT_F16) return launch_gemv_sz<DT_F16, 4, NC, WB, IW>(a, ntiles, act, s);
+    return launch_gemv_sz<DT_BF16, 4, NC, WB, IW>(a, ntiles, act, s);
 }
 
 hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
@@ -495,11 +522,11 @@ hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, cons
     }
     const int ntiles = (N + 16 * c.nc - 1) / (16 * c.nc);
     if (wb == 8) {
-        if (c.nc == 8) return launch_gemv_nc<8, 8>(a, ntiles, sz_dt, act, s);
-        return launch_gemv_nc<4, 8>(a, ntiles, sz_dt, act, s);
+        if (c.nc == 8) return launch_gemv_nc<8, 8, 4>(a, ntiles, sz_dt, act, s);
+        return launch_gemv_nc<4, 8, 16>(a, ntiles, sz_dt, act, s);
     }
-    if (c.nc == 8) return launch_gemv_nc<8, 4>(a, ntiles, sz_dt, act, s);
-    return launch_gemv_nc<4, 4>(a, ntiles, sz_dt, act, s);
+    if (c.nc == 8) return launch_gemv_nc<8, 4, 4>(a, ntiles, sz_dt, act, s);
+    return launch_gemv_nc<4, 4, 16>(a, ntiles, sz_dt, act, s);
 }
 
 }  // namespace mcq4
