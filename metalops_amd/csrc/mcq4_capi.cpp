@@ -32,6 +32,10 @@ hipError_t launch_gemm3(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
                         int64_t ldy, int M, int K, int N, hipStream_t s);
 bool gemm4_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
 size_t gemm4_workspace_bytes(int64_t M, int64_t K, int64_t N);
+bool gemm5_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
+size_t gemm5_workspace_bytes(int64_t M, int64_t K, int64_t N);
+hipError_t launch_gemm5(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
 hipError_t launch_gemm4(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
 }  // namespace mcq4
@@ -58,12 +62,13 @@ constexpr int64_t kMaxDim = (int64_t)1 << 30;  // keeps 32-bit lane offsets safe
 
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Prefill kernel choice (M > 64).  Default: the barrier-free GEMM (q4_gemm4)
-// when N % 128 == 0 and the pointers are 16-byte aligned; otherwise the
+// Prefill kernel choice (M > 64).  Default, when N % 128 == 0 and the pointers
+// are 16-byte aligned: the LDS-staged GEMM (q4_gemm5) for M > 128, the
+// barrier-free GEMM (q4_gemm4, 128-row tiles) for M <= 128.  Otherwise the
 // async-copy GEMM (q4_gemm2) when its alignment needs hold and the output has
 // at least 128 tiles of 128x256; otherwise the register-staged split-K kernel.
-// MCQ4_GEMM_PATH=sync|async|3|4 forces one kernel (tests, experiments).
-enum class Prefill { Sync, Async2, Async3, Free4 };
+// MCQ4_GEMM_PATH=sync|async|3|4|5 forces one kernel (tests, experiments).
+enum class Prefill { Sync, Async2, Async3, Free4, Staged5 };
 Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
                        int64_t N) {
     const bool ok2 = mcq4::gemm2_supported(X, ldx, W, K, N);
@@ -73,8 +78,9 @@ Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t
         if (env[0] == 'a' && ok2) return Prefill::Async2;
         if (env[0] == '3' && ok2) return Prefill::Async3;
         if (env[0] == '4' && ok4) return Prefill::Free4;
+        if (env[0] == '5' && ok4) return Prefill::Staged5;
     }
-    if (ok4) return Prefill::Free4;
+    if (ok4) return M > 128 ? Prefill::Staged5 : Prefill::Free4;
     if (ok2 && ((M + 127) / 128) * ((N + 255) / 256) >= 128) return Prefill::Async2;
     return Prefill::Sync;
 }
@@ -158,8 +164,9 @@ int mcq4_dequantize_q4_0(const uint8_t *blocks, int64_t K, int64_t N, void *out,
 size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M <= 0 || K <= 0 || N <= 0 || K % 32) return 0;
     if (M <= 64) return mcq4::skinny_workspace_bytes(M, K, N);
-    // The larger of the two split-K kernels' needs: an upper bound for any prefill kernel.
-    return std::max(mcq4::gemm_workspace_bytes(M, K, N), mcq4::gemm4_workspace_bytes(M, K, N));
+    // The largest of the split-K kernels' needs: an upper bound for any prefill kernel.
+    return std::max({mcq4::gemm_workspace_bytes(M, K, N), mcq4::gemm4_workspace_bytes(M, K, N),
+                     mcq4::gemm5_workspace_bytes(M, K, N)});
 }
 
 int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, int64_t ldy,
@@ -191,6 +198,7 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
         _Float16 *y = (_Float16 *)Y;
         hipStream_t st = (hipStream_t)stream;
         switch (prefill_kernel(x, ldx, W, M, K, N)) {
+            case Prefill::Staged5: e = mcq4::launch_gemm5(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
             case Prefill::Free4: e = mcq4::launch_gemm4(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
             case Prefill::Async3: e = mcq4::launch_gemm3(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;
             case Prefill::Async2: e = mcq4::launch_gemm2(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;

@@ -32,11 +32,10 @@
 #include <algorithm>
 #include <atomic>
 
-#include "q4_common.h"
+#include "q4_gemm4.h"
 
 namespace mcq4 {
 
-constexpr int G4_BN = 256;
 #ifndef MCQ4_G4_P
 #define MCQ4_G4_P 3
 #endif
@@ -45,17 +44,7 @@ constexpr int G4_R = G4_P + 1;                 // raw ring slots per wave
 constexpr int G4_RAW_W = 18 * 128;             // raw bytes per wave and step (2304)
 constexpr int G4_RAW_SLOT = G4_RAW_W + 64;     // + read overhang
 
-struct Gemm4Args {
-    const _Float16 *X;
-    int64_t ldx;
-    const uint8_t *W;
-    _Float16 *Y;
-    int64_t ldy;
-    int M, nb, N;
-    int tiles_m, tiles_n;
-    int S;               // K splits (grid.z)
-    float *partials;     // [tiles][S][BM*256] when S > 1
-};
+
 
 template <int BM, int WGM>
 __global__ void __launch_bounds__(WGM * 128, 1)
@@ -281,6 +270,14 @@ q4_gemm4_reduce_kernel(Gemm4Args a) {
         if (n + c < a.N) a.Y[(int64_t)m * a.ldy + n + c] = (_Float16)sum[c];
 }
 
+hipError_t launch_gemm4_reduce(const Gemm4Args &a, int bm, hipStream_t s) {
+    const int64_t n4 = (int64_t)a.tiles_m * a.tiles_n * (bm * G4_BN / 4);
+    const dim3 grid((unsigned)((n4 + 255) / 256));
+    if (bm == 256) hipLaunchKernelGGL((q4_gemm4_reduce_kernel<256>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((q4_gemm4_reduce_kernel<128>), grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
 template <int BM, int WGM>
 static hipError_t launch_g4(const Gemm4Args &a, hipStream_t s) {
     constexpr size_t lds = (size_t)(2 * WGM) * G4_R * G4_RAW_SLOT;
@@ -297,11 +294,7 @@ static hipError_t launch_g4(const Gemm4Args &a, hipStream_t s) {
     }
     hipLaunchKernelGGL((q4_gemm4_kernel<BM, WGM>), dim3(a.tiles_m * a.tiles_n, 1, a.S),
                        dim3(WGM * 128), lds, s, a);
-    if (a.S > 1) {
-        const int64_t n4 = (int64_t)a.tiles_m * a.tiles_n * (BM * G4_BN / 4);
-        hipLaunchKernelGGL((q4_gemm4_reduce_kernel<BM>), dim3((unsigned)((n4 + 255) / 256)), dim3(256),
-                           0, s, a);
-    }
+    if (a.S > 1) return launch_gemm4_reduce(a, BM, s);
     return hipGetLastError();
 }
 
@@ -312,14 +305,10 @@ bool gemm4_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K
            K >= QK;
 }
 
-struct G4Cfg {
-    int bm, S;
-};
-
 // Row-tile height and K splits: BM = 128 when 256-row tiles would leave fewer
 // than 192 tiles; K is split (powers of two, at least 16 steps per split) until
 // about 192 workgroups have work.
-static G4Cfg gemm4_config(int64_t M, int64_t K, int64_t N) {
+G4Cfg gemm4_config(int64_t M, int64_t K, int64_t N) {
     const int64_t tn = (N + G4_BN - 1) / G4_BN;
     G4Cfg c{256, 1};
     if (((M + 255) / 256) * tn < 192) c.bm = 128;

@@ -200,6 +200,10 @@ PATHS = {
     "gemm4_wgm4_bm256": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM4_WGM": "4", "MCQ4_GEMM2_BM": "256"},
     "gemm4_wgm4_bm128": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM4_WGM": "4", "MCQ4_GEMM2_BM": "128"},
     "gemm4_split5_bm256": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM4_SPLIT": "5", "MCQ4_GEMM2_BM": "256"},
+    "gemm5_bm256": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM2_BM": "256"},
+    "gemm5_bm128": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM2_BM": "128"},
+    "gemm5_split3": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM4_SPLIT": "3"},
+    "gemm5_split5_bm256": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM4_SPLIT": "5", "MCQ4_GEMM2_BM": "256"},
 }
 PATH_SHAPES = {
     "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
@@ -229,6 +233,12 @@ PATH_SHAPES = {
     "gemm4_wgm4_bm256": [(65, 352, 128), (257, 1024, 384), (512, 4096, 768), (2048, 4096, 1024), (128, 4096, 512)],
     "gemm4_wgm4_bm128": [(65, 352, 128), (300, 2048, 512), (384, 4096, 896), (512, 11008, 512)],
     "gemm4_split5_bm256": [(257, 352, 256), (100, 2048, 512)],
+    "gemm5_bm256": [(65, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
+                    (100, 32, 256), (70, 64, 384), (513, 96, 256)],
+    "gemm5_bm128": [(65, 352, 128), (129, 1024, 384), (300, 2048, 512), (384, 4096, 896), (100, 96, 256),
+                    (128, 4096, 4096), (512, 11008, 512)],
+    "gemm5_split3": [(200, 352, 384), (129, 1024, 256), (300, 4096, 640)],
+    "gemm5_split5_bm256": [(257, 352, 256), (100, 2048, 512)],
 }
 
 
