@@ -39,9 +39,9 @@ FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
 # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the same
 # workloads (bench.py --part decode|prefill), each counter scaled by what it reads
 # for a plain 256 MiB device copy (FETCH_SIZE x 2, WRITE_SIZE x 1).  Figures and
-# commands: profiles/gemv_dma_llama7b_m1.md, profiles/gemm4_llama7b_m2048.md.
+# commands: profiles/gemv_dma_llama7b_m1.md, profiles/gemm5_llama7b_m2048.md.
 DECODE_TRAFFIC_BYTES = 22985587       # average over the five projections
-PREFILL_UP_TRAFFIC_BYTES = 361800000  # 302.5 MB read + 59.3 MB written
+PREFILL_UP_TRAFFIC_BYTES = 360943002  # 302.1 MB read + 58.8 MB written
 
 DECODE_LAYER = [  # (name, K, N) -- Llama-2-7B projections, configs[1]
     ("qkv", 4096, 12288),
