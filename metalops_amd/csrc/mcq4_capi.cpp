@@ -13,6 +13,7 @@
 #include <stdio.h>
 
 #include "../../include/mcq4.h"
+#include "q4_gemm4.h"
 
 namespace mcq4 {
 hipError_t launch_quantize(bool llama_rule, const float *W, int64_t ldw, int nb, int N,
@@ -34,6 +35,8 @@ bool gemm4_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K
 size_t gemm4_workspace_bytes(int64_t M, int64_t K, int64_t N);
 bool gemm5_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
 size_t gemm5_workspace_bytes(int64_t M, int64_t K, int64_t N);
+hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
 hipError_t launch_gemm5(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
 hipError_t launch_gemm4(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
@@ -63,12 +66,12 @@ constexpr int64_t kMaxDim = (int64_t)1 << 30;  // keeps 32-bit lane offsets safe
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
 // Prefill kernel choice (M > 64).  Default, when N % 128 == 0 and the pointers
-// are 16-byte aligned: the LDS-staged GEMM (q4_gemm5) for M > 128, the
-// barrier-free GEMM (q4_gemm4, 128-row tiles) for M <= 128.  Otherwise the
+// are 16-byte aligned: the LDS-staged GEMM with two waves per SIMD (q4_gemm6)
+// for M > 128, the barrier-free GEMM (q4_gemm4, 128-row tiles) for M <= 128.  Otherwise the
 // async-copy GEMM (q4_gemm2) when its alignment needs hold and the output has
 // at least 128 tiles of 128x256; otherwise the register-staged split-K kernel.
-// MCQ4_GEMM_PATH=sync|async|3|4|5 forces one kernel (tests, experiments).
-enum class Prefill { Sync, Async2, Async3, Free4, Staged5 };
+// MCQ4_GEMM_PATH=sync|async|3|4|5|6 forces one kernel (tests, experiments).
+enum class Prefill { Sync, Async2, Async3, Free4, Staged5, Staged6 };
 Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
                        int64_t N) {
     const bool ok2 = mcq4::gemm2_supported(X, ldx, W, K, N);
@@ -79,8 +82,9 @@ Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t
         if (env[0] == '3' && ok2) return Prefill::Async3;
         if (env[0] == '4' && ok4) return Prefill::Free4;
         if (env[0] == '5' && ok4) return Prefill::Staged5;
+        if (env[0] == '6' && ok4 && mcq4::gemm5_config(M, K, N).bm == 256) return Prefill::Staged6;
     }
-    if (ok4) return M > 128 ? Prefill::Staged5 : Prefill::Free4;
+    if (ok4) return M > 128 && mcq4::gemm5_config(M, K, N).bm == 256 ? Prefill::Staged6 : Prefill::Free4;
     if (ok2 && ((M + 127) / 128) * ((N + 255) / 256) >= 128) return Prefill::Async2;
     return Prefill::Sync;
 }
@@ -198,6 +202,7 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
         _Float16 *y = (_Float16 *)Y;
         hipStream_t st = (hipStream_t)stream;
         switch (prefill_kernel(x, ldx, W, M, K, N)) {
+            case Prefill::Staged6: e = mcq4::launch_gemm6(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
             case Prefill::Staged5: e = mcq4::launch_gemm5(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
             case Prefill::Free4: e = mcq4::launch_gemm4(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
             case Prefill::Async3: e = mcq4::launch_gemm3(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;

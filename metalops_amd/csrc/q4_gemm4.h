@@ -26,6 +26,8 @@ struct G4Cfg {
     int bm, S;
 };
 G4Cfg gemm4_config(int64_t M, int64_t K, int64_t N);
+// Plan of the LDS-staged kernels (q4_gemm5, q4_gemm6): 256-row tiles, split-K.
+G4Cfg gemm5_config(int64_t M, int64_t K, int64_t N);
 
 // Sums the S partial tiles per output tile in split order and stores fp16.
 hipError_t launch_gemm4_reduce(const Gemm4Args &a, int bm, hipStream_t s);

@@ -408,7 +408,7 @@ bool gemm5_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K
 // beats a 128-row tile on these shapes (2048x14336x4096: 262 vs 350 us; the
 // fp32 partials cost one extra pass over M x N x S floats).
 // MCQ4_GEMM2_BM=128 and MCQ4_GEMM4_SPLIT override (experiments, tests).
-static G4Cfg gemm5_config(int64_t M, int64_t K, int64_t N) {
+G4Cfg gemm5_config(int64_t M, int64_t K, int64_t N) {
     G4Cfg c{256, 1};
     if (const char *env = getenv("MCQ4_GEMM2_BM")) c.bm = atoi(env) == 128 ? 128 : 256;
     const int64_t t = ((M + c.bm - 1) / c.bm) * ((N + G4_BN - 1) / G4_BN);

@@ -1,0 +1,310 @@
+// Prefill-shaped q4_0 matmul (M > 128) on gfx950: the LDS-staged GEMM of
+// q4_gemm5 with two waves per SIMD.
+//
+//   * WG = 512 threads = 8 waves in a 2 (M) x 4 (N) grid; WG tile 256 x 256;
+//     wave tile 128 x 64 of v_mfma_f32_32x32x16_f16 (128 fp32 accumulators),
+//     so two waves share each SIMD and one wave's LDS, copy and barrier stalls
+//     are covered by the other's MFMAs.
+//   * Activations: as q4_gemm5 (one 256 x 128-byte stage per slot, 3 slots,
+//     swizzled chunk positions 8r + (c ^ (r & 7))); each wave copies 32 rows.
+//     A operands are reloaded in place: operand (ks, i) of the next step is
+//     read right after the last MFMA of this step that uses it.
+//   * Weights: each wave copies the raw bytes of its 64 columns (1152 bytes per
+//     step: one 16-byte-per-lane and one 4-byte-per-lane copy, no lane masks)
+//     into a private 6-slot ring and builds its B operands (natural-order
+//     unpack to 1024 + q, minus 1032, times d: the reference's fp16 dequant
+//     value) one step ahead, in 12 chunks spread over the step's 16 MFMAs.
+//   * Barrier between the two steps of a stage; stage s+3's copies go out
+//     during the second step, one per two MFMAs.  Plan, split-K partials and
+//     the reduction kernel are q4_gemm5's.
+//
+// MFMA 32x32 output layout: lane l holds D[8*(r/4) + 4*(l/32) + r%4][l%32], r = 0..15.
+#include <algorithm>
+#include <atomic>
+#include <type_traits>
+
+#include "q4_gemm4.h"
+
+namespace mcq4 {
+
+constexpr int G6_NS = 3;                       // stages (A slots) in flight
+constexpr int G6_ROWB = 128;                   // A bytes per row and stage (2 steps)
+constexpr int G6_WAVES = 8;
+constexpr int G6_WN = 64;                      // columns per wave
+constexpr int G6_RAW_W = 18 * G6_WN;           // raw weight bytes per wave and step (1152)
+constexpr int G6_RAW_SLOT = 1280;              // 1024 + 256 (remainder copy); covers the read overhang
+constexpr int G6_RAW_N = 2 * G6_NS;            // raw ring slots per wave (steps)
+constexpr int G6_BM = 256;
+constexpr size_t G6_LDS = (size_t)G6_NS * G6_BM * G6_ROWB + (size_t)G6_WAVES * G6_RAW_N * G6_RAW_SLOT;
+static_assert(G6_LDS <= 160 * 1024, "LDS budget");
+static_assert(G6_RAW_SLOT >= 1024 + 64 * 4 && G6_RAW_SLOT >= G6_RAW_W + 16, "raw slot covers the remainder copy and the read overhang");
+
+__global__ void __launch_bounds__(512, 1)
+q4_gemm6_kernel(Gemm4Args a) {
+    constexpr int BM = G6_BM;
+    constexpr int WM = BM / 2, WN = G6_WN;
+    constexpr int TM = WM / 32, TN = WN / 32;    // 4 x 2
+    constexpr int A_SLOT = BM * G6_ROWB;
+    constexpr int A_LD = BM * 8 / (64 * G6_WAVES);   // A copies per wave and stage (4)
+    constexpr int GROUP = A_LD + 4;              // vector-memory instructions per wave and stage
+    constexpr int NMF = 2 * TM * TN;             // MFMAs per step (16)
+    static_assert(2 * GROUP < 64, "vmcnt range");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+
+    const int ntiles = a.tiles_m * a.tiles_n;
+    const int bid = blockIdx.x;
+    int tile_id = bid;
+    if (ntiles % 8 == 0) tile_id = (bid % 8) * (ntiles / 8) + bid / 8;
+    const int tm = tile_id % a.tiles_m;
+    const int tn = tile_id / a.tiles_m;
+    const int m0 = tm * BM, n0 = tn * G4_BN;
+    const int z = (int)blockIdx.z;
+    const int k_lo = (int)((int64_t)a.nb * z / a.S);
+    const int nk = (int)((int64_t)a.nb * (z + 1) / a.S) - k_lo;
+    const int nst = (nk + 1) >> 1;
+
+    uint8_t *const sA = smem;
+    uint8_t *const ring = smem + G6_NS * A_SLOT + wave * (G6_RAW_N * G6_RAW_SLOT);
+
+    // A copy u of this wave: positions 64(wave*A_LD+u) + lane = row 8(wave*A_LD+u) + lane/8,
+    // chunk (lane ^ lane/8) & 7 (the same for every u).
+    const int a_c = (lane ^ (lane >> 3)) & 7;
+    const int a_t = a_c >> 2;
+    const int a_r0 = m0 + 8 * wave * A_LD + (lane >> 3);
+    const _Float16 *a_col = a.X + (int64_t)k_lo * QK + 8 * (a_c & 3);
+
+    const int64_t row_bytes = (int64_t)a.N * BLOCK_BYTES;
+    const uint8_t *w_k = a.W + (int64_t)k_lo * row_bytes;
+    const bool wcols = n0 + wn * WN < a.N;
+    const uint8_t *w_seg = wcols ? w_k + (int64_t)(n0 + wn * WN) * BLOCK_BYTES : w_k;
+
+    // Copy ci (0 .. GROUP-1) of stage s_dst: A copies, then per step t the raw
+    // bytes 0..1023 (16 per lane) and 1024..1151 (4 per lane for lanes 0..31;
+    // lanes 32..63 re-read lane 31's dword into the slot's unused tail, so no
+    // lane is masked and nothing past the segment is read).  LDS-DMA copies of
+    // fewer than 4 bytes per lane still fill 4 bytes per lane, so 2-byte copies
+    // cannot pack the remainder.  Stages past the end re-copy the last stage.
+    auto issue_one = [&](int s_dst, int ci) {
+        const int s_src = min(s_dst, nst - 1);
+        if (ci < A_LD) {
+            uint8_t *dst = sA + (s_dst % G6_NS) * A_SLOT + wave * (A_LD * 1024) + 1024 * ci;
+            const int64_t koff = (int64_t)min(2 * s_src + a_t, nk - 1) * QK;
+            const int m = min(a_r0 + 8 * ci, a.M - 1);
+            __builtin_amdgcn_global_load_lds(
+                (void *)(a_col + (int64_t)m * a.ldx + koff),
+                (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+            return;
+        }
+        const int r = ci - A_LD, t = r >> 1;
+        const uint8_t *src = w_seg + (int64_t)min(2 * s_src + t, nk - 1) * row_bytes;
+        uint8_t *dst = ring + ((2 * s_dst + t) % G6_RAW_N) * G6_RAW_SLOT;
+        if ((r & 1) == 0)
+            __builtin_amdgcn_global_load_lds((void *)(src + 16 * lane),
+                                             (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds((void *)(src + 1024 + 4 * min(lane, 31)),
+                                             (__attribute__((address_space(3))) void *)(dst + 1024), 4, 0, 0);
+    };
+    auto issue_stage = [&](int s_dst) {
+#pragma unroll
+        for (int ci = 0; ci < GROUP; ++ci) issue_one(s_dst, ci);
+    };
+
+    const int lrow = lane & 31, lhi = lane >> 5;
+    // A operand (i, ks) of step t: row wm*WM + 32 i + lrow, chunk 4t + 2ks + lhi.
+    uint32_t a_off[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            a_off[t][ks] = (uint32_t)((wm * WM + lrow) * G6_ROWB + (((4 * t + 2 * ks + lhi) ^ (lrow & 7)) << 4));
+    auto read_a1 = [&](int s, int t, int ks, int i) {
+        const uint32_t base = lds_addr(sA + (s % G6_NS) * A_SLOT);
+        return *(const lds_half8 *)(lds_ptr(base + a_off[t][ks]) + i * 32 * G6_ROWB);
+    };
+    const int qoff0 = 18 * lrow + 2 + 4 * lhi;
+    const int q_al = qoff0 & ~3;
+    const uint32_t q_sh = (uint32_t)(qoff0 & 3) * 8;
+    const int d_off = 18 * lrow;
+    auto load_b = [&](int k, half8_t (&bv)[2][TN]) {
+        const lds_u8 *Rs = lds_ptr(lds_addr(ring + (k % G6_RAW_N) * G6_RAW_SLOT));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const lds_u32 *qp = (const lds_u32 *)(Rs + q_al + j * 32 * 18);
+            uint32_t qd[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) qd[t] = qp[t];
+            const uint32_t dd = *(const lds_u16 *)(Rs + d_off + j * 32 * 18);
+            const half2_t d2 = bitcast<half2_t>(__builtin_amdgcn_perm(dd, dd, 0x01000100u));
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+                bv[ks][j] = dequant8_nat(__builtin_amdgcn_alignbit(qd[2 * ks + 1], qd[2 * ks], q_sh), d2);
+        }
+    };
+
+    float16_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // One step: the NMF MFMAs of (A, B).  After MFMA idx: dequant chunk idx of
+    // the next B (12 chunks: 3 per 8-weight unit), the in-place reload of the A
+    // operand whose last use this was (next step's A: stage a_s, step a_t), and
+    // with copies, copy idx/2 of stage cs after every odd MFMA.
+    half8_t A[2][TM];
+    auto step = [&](auto with_copies, int cs, const half8_t (&B)[2][TN], int k_next,
+                    half8_t (&Bn)[2][TN], int a_s, int a_t) {
+#pragma clang fp contract(off)
+        const lds_u8 *Rs = lds_ptr(lds_addr(ring + (k_next % G6_RAW_N) * G6_RAW_SLOT));
+        uint32_t qd[TN][4], dd[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const lds_u32 *qp = (const lds_u32 *)(Rs + q_al + j * 32 * 18);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) qd[j][t] = qp[t];
+            dd[j] = *(const lds_u16 *)(Rs + d_off + j * 32 * 18);
+        }
+        const half2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
+        const uint32_t C64 = 0x64646464u;
+        uint32_t lo[2 * TN], hi[2 * TN];
+        uint4_t uu[2 * TN];
+        half2_t d2[TN];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int idx = 0; idx < NMF; ++idx) {
+            const int ks = idx / (TM * TN), i = (idx / TN) % TM, j = idx % TN;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ks][i], B[ks][j], acc[i][j], 0, 0, 0);
+            if (j == TN - 1) A[ks][i] = read_a1(a_s, a_t, ks, i);
+            if constexpr (decltype(with_copies)::value) {
+                if ((idx & 1) == 1 && (idx >> 1) < GROUP) issue_one(cs, idx >> 1);
+            }
+            if (idx < 3 * 2 * TN) {
+                const int c = idx, unit = c / 3, part = c % 3, uj = unit >> 1, uk = unit & 1;
+                if (part == 0) {
+                    if (uk == 0) d2[uj] = bitcast<half2_t>(__builtin_amdgcn_perm(dd[uj], dd[uj], 0x01000100u));
+                    const uint32_t w = __builtin_amdgcn_alignbit(qd[uj][2 * uk + 1], qd[uj][2 * uk], q_sh);
+                    lo[unit] = w & 0x0F0F0F0Fu;
+                    hi[unit] = (w >> 4) & 0x0F0F0F0Fu;
+                } else if (part == 1) {
+                    const uint32_t e03 = __builtin_amdgcn_perm(hi[unit], lo[unit], 0x05010400u);
+                    const uint32_t e47 = __builtin_amdgcn_perm(hi[unit], lo[unit], 0x07030602u);
+                    uu[unit] = uint4_t{__builtin_amdgcn_perm(C64, e03, 0x04010400u),
+                                       __builtin_amdgcn_perm(C64, e03, 0x04030402u),
+                                       __builtin_amdgcn_perm(C64, e47, 0x04010400u),
+                                       __builtin_amdgcn_perm(C64, e47, 0x04030402u)};
+                } else {
+                    uint4_t r;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                        r[t] = bitcast<uint32_t>((bitcast<half2_t>(uu[unit][t]) - off) * d2[uj]);
+                    Bn[uk][uj] = bitcast<half8_t>(r);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // Prologue: stages 0, 1, 2 in flight; stage 0 landed for every wave.
+    issue_stage(0);
+    issue_stage(1);
+    issue_stage(2);
+    wait_vmcnt<2 * GROUP>();
+    lds_barrier();
+    half8_t B0[2][TN], B1[2][TN];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int i = 0; i < TM; ++i) A[ks][i] = read_a1(0, 0, ks, i);
+    load_b(0, B0);
+    const int nfull = nk >> 1;
+    for (int s = 0; s < nfull; ++s) {
+        // Step 2s: builds B(2s+1) (stage s), reloads A(s, step 1).
+        step(std::false_type{}, 0, B0, 2 * s + 1, B1, s, 1);
+        wait_vmcnt<GROUP>();                     // stage s+1 (own copies) landed
+        lds_barrier();                           // stage s+1 visible; stage s's slot read by all
+        // Step 2s+1 with stage s+3's copies: builds B(2s+2) (stage s+1), reloads
+        // A(s+1, step 0).  Past the last step both are clamped re-reads of valid slots.
+        step(std::true_type{}, s + 3, B1, min(2 * s + 2, nk - 1), B0, s + 1, 0);
+    }
+    if (nk & 1) {                                // last step alone (A and B already loaded)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ks][i], B0[ks][j], acc[i][j], 0, 0, 0);
+    }
+    wait_vmcnt<0>();
+
+    const int rsub = 4 * lhi;
+    if (a.S == 1) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int n = n0 + wn * WN + j * 32 + lrow;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
+                    if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (_Float16)acc[i][j][r];
+                }
+            }
+        return;
+    }
+    float *part = a.partials + ((int64_t)tile_id * a.S + z) * (BM * G4_BN);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int nl = wn * WN + j * 32 + lrow;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int ml = wm * WM + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
+                part[ml * G4_BN + nl] = acc[i][j][r];
+            }
+        }
+}
+
+// Same requirements as q4_gemm5 (N % 128 == 0, 16-byte aligned W and X rows)
+// and the same plan; used with 256-row tiles only.
+hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s) {
+    G4Cfg c = gemm5_config(M, K, N);
+    if (c.bm != G6_BM) return hipErrorInvalidValue;
+    Gemm4Args a;
+    a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
+    a.M = M; a.nb = K / QK; a.N = N;
+    a.tiles_n = (N + G4_BN - 1) / G4_BN;
+    a.tiles_m = (M + G6_BM - 1) / G6_BM;
+    a.S = c.S;
+    a.partials = nullptr;
+    if (c.S > 1) {
+        if (!ws) return hipErrorInvalidValue;
+        a.partials = (float *)((char *)ws + COUNTER_BYTES);
+    }
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(done.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void *)q4_gemm6_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)G6_LDS);
+        if (e != hipSuccess) return e;
+        done.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    hipLaunchKernelGGL(q4_gemm6_kernel, dim3(a.tiles_m * a.tiles_n, 1, a.S), dim3(512), G6_LDS, s, a);
+    if (a.S > 1) return launch_gemm4_reduce(a, G6_BM, s);
+    return hipGetLastError();
+}
+
+}  // namespace mcq4

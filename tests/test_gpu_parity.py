@@ -40,6 +40,7 @@ def _acts(M, K, seed):
 def _check_rows(Y, Yref, tol=TOL):
     Y = np.asarray(Y, dtype=np.float64)
     Yref = np.asarray(Yref, dtype=np.float64)
+    assert np.isfinite(Y).all(), f"non-finite outputs at {np.argwhere(~np.isfinite(Y))[:4].tolist()}"
     err = np.abs(Y - Yref).max(axis=1)
     bound = tol * np.abs(Yref).max(axis=1)
     bad = np.nonzero(err > bound)[0]
@@ -204,6 +205,8 @@ PATHS = {
     "gemm5_bm128": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM2_BM": "128"},
     "gemm5_split3": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM4_SPLIT": "3"},
     "gemm5_split5_bm256": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM4_SPLIT": "5", "MCQ4_GEMM2_BM": "256"},
+    "gemm6": {"MCQ4_GEMM_PATH": "6"},
+    "gemm6_split3": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "3"},
 }
 PATH_SHAPES = {
     "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
@@ -239,6 +242,9 @@ PATH_SHAPES = {
                     (128, 4096, 4096), (512, 11008, 512)],
     "gemm5_split3": [(200, 352, 384), (129, 1024, 256), (300, 4096, 640)],
     "gemm5_split5_bm256": [(257, 352, 256), (100, 2048, 512)],
+    "gemm6": [(129, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
+              (200, 32, 256), (130, 64, 384), (513, 96, 256), (2048, 11008, 512)],
+    "gemm6_split3": [(200, 352, 384), (300, 4096, 640)],
 }
 
 
