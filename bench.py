@@ -434,7 +434,7 @@ def main():
                 "unit": "TFLOP/s",
                 "frac": round(pre_up["tflops"] / FP16_PEAK_TFLOPS, 4),
                 "traffic": PREFILL_UP_TRAFFIC_BYTES,
-                "kernel": "q4_gemm6_kernel (M=2048 K=4096 N=14336)",
+                "kernel": "q4_gemm6_kernel<1> (M=2048 K=4096 N=14336)",
             },
         },
         "cpu_baseline": cpu,

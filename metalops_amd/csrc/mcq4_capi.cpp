@@ -37,6 +37,7 @@ bool gemm5_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K
 size_t gemm5_workspace_bytes(int64_t M, int64_t K, int64_t N);
 hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
+size_t gemm6_workspace_bytes(int64_t M, int64_t K, int64_t N);
 hipError_t launch_gemm5(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
 hipError_t launch_gemm4(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
@@ -66,8 +67,7 @@ constexpr int64_t kMaxDim = (int64_t)1 << 30;  // keeps 32-bit lane offsets safe
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
 // Prefill kernel choice (M > 64).  Default, when N % 128 == 0 and the pointers
-// are 16-byte aligned: the LDS-staged GEMM with two waves per SIMD (q4_gemm6)
-// for M > 128, the barrier-free GEMM (q4_gemm4, 128-row tiles) for M <= 128.  Otherwise the
+// are 16-byte aligned: the LDS-staged GEMM with two waves per SIMD (q4_gemm6).  Otherwise the
 // async-copy GEMM (q4_gemm2) when its alignment needs hold and the output has
 // at least 128 tiles of 128x256; otherwise the register-staged split-K kernel.
 // MCQ4_GEMM_PATH=sync|async|3|4|5|6 forces one kernel (tests, experiments).
@@ -82,9 +82,9 @@ Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t
         if (env[0] == '3' && ok2) return Prefill::Async3;
         if (env[0] == '4' && ok4) return Prefill::Free4;
         if (env[0] == '5' && ok4) return Prefill::Staged5;
-        if (env[0] == '6' && ok4 && mcq4::gemm5_config(M, K, N).bm == 256) return Prefill::Staged6;
+        if (env[0] == '6' && ok4) return Prefill::Staged6;
     }
-    if (ok4) return M > 128 && mcq4::gemm5_config(M, K, N).bm == 256 ? Prefill::Staged6 : Prefill::Free4;
+    if (ok4) return Prefill::Staged6;
     if (ok2 && ((M + 127) / 128) * ((N + 255) / 256) >= 128) return Prefill::Async2;
     return Prefill::Sync;
 }
@@ -170,7 +170,7 @@ size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M <= 64) return mcq4::skinny_workspace_bytes(M, K, N);
     // The largest of the split-K kernels' needs: an upper bound for any prefill kernel.
     return std::max({mcq4::gemm_workspace_bytes(M, K, N), mcq4::gemm4_workspace_bytes(M, K, N),
-                     mcq4::gemm5_workspace_bytes(M, K, N)});
+                     mcq4::gemm5_workspace_bytes(M, K, N), mcq4::gemm6_workspace_bytes(M, K, N)});
 }
 
 int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, int64_t ldy,

@@ -1,11 +1,12 @@
-// Prefill-shaped q4_0 matmul (M > 128) on gfx950: the LDS-staged GEMM of
+// Prefill-shaped q4_0 matmul (M > 64) on gfx950: the LDS-staged GEMM of
 // q4_gemm5 with two waves per SIMD.
 //
-//   * WG = 512 threads = 8 waves in a 2 (M) x 4 (N) grid; WG tile 256 x 256;
-//     wave tile 128 x 64 of v_mfma_f32_32x32x16_f16 (128 fp32 accumulators),
-//     so two waves share each SIMD and one wave's LDS, copy and barrier stalls
-//     are covered by the other's MFMAs.
-//   * Activations: as q4_gemm5 (one 256 x 128-byte stage per slot, 3 slots,
+//   * Wave tile 128 x 64 of v_mfma_f32_32x32x16_f16 (128 fp32 accumulators), so
+//     two waves share each SIMD and one wave's LDS, copy and barrier stalls are
+//     covered by the other's MFMAs.  Default form (WGM = 1): WG = 4 waves along
+//     N, WG tile 128 x 256, two workgroups per CU, each barrier among 4 waves.
+//     WGM = 2: WG = 8 waves in a 2 (M) x 4 (N) grid, WG tile 256 x 256.
+//   * Activations: as q4_gemm5 (one BM x 128-byte stage per slot, 3 slots,
 //     swizzled chunk positions 8r + (c ^ (r & 7))); each wave copies 32 rows.
 //     A operands are reloaded in place: operand (ks, i) of the next step is
 //     read right after the last MFMA of this step that uses it.
@@ -29,23 +30,27 @@ namespace mcq4 {
 
 constexpr int G6_NS = 3;                       // stages (A slots) in flight
 constexpr int G6_ROWB = 128;                   // A bytes per row and stage (2 steps)
-constexpr int G6_WAVES = 8;
 constexpr int G6_WN = 64;                      // columns per wave
 constexpr int G6_RAW_W = 18 * G6_WN;           // raw weight bytes per wave and step (1152)
 constexpr int G6_RAW_SLOT = 1280;              // 1024 + 256 (remainder copy); covers the read overhang
 constexpr int G6_RAW_N = 2 * G6_NS;            // raw ring slots per wave (steps)
-constexpr int G6_BM = 256;
-constexpr size_t G6_LDS = (size_t)G6_NS * G6_BM * G6_ROWB + (size_t)G6_WAVES * G6_RAW_N * G6_RAW_SLOT;
-static_assert(G6_LDS <= 160 * 1024, "LDS budget");
+// WGM rows of four waves: WG tile (128 WGM) x 256, 4 WGM waves.  WGM = 2 runs
+// one 8-wave workgroup per CU; WGM = 1 two 4-wave workgroups per CU.
+template <int WGM>
+constexpr size_t g6_lds_bytes() {
+    return (size_t)G6_NS * (128 * WGM) * G6_ROWB + (size_t)(4 * WGM) * G6_RAW_N * G6_RAW_SLOT;
+}
+static_assert(g6_lds_bytes<2>() <= 160 * 1024 && 2 * g6_lds_bytes<1>() <= 160 * 1024, "LDS budget");
 static_assert(G6_RAW_SLOT >= 1024 + 64 * 4 && G6_RAW_SLOT >= G6_RAW_W + 16, "raw slot covers the remainder copy and the read overhang");
 
-__global__ void __launch_bounds__(512, 1)
+template <int WGM>
+__global__ void __launch_bounds__(256 * WGM, 2 / WGM)
 q4_gemm6_kernel(Gemm4Args a) {
-    constexpr int BM = G6_BM;
-    constexpr int WM = BM / 2, WN = G6_WN;
+    constexpr int BM = 128 * WGM, NWAVES = 4 * WGM;
+    constexpr int WM = BM / WGM, WN = G6_WN;   // 128 x 64 wave tiles in both forms
     constexpr int TM = WM / 32, TN = WN / 32;    // 4 x 2
     constexpr int A_SLOT = BM * G6_ROWB;
-    constexpr int A_LD = BM * 8 / (64 * G6_WAVES);   // A copies per wave and stage (4)
+    constexpr int A_LD = BM * 8 / (64 * NWAVES);     // A copies per wave and stage (4)
     constexpr int GROUP = A_LD + 4;              // vector-memory instructions per wave and stage
     constexpr int NMF = 2 * TM * TN;             // MFMAs per step (16)
     static_assert(2 * GROUP < 64, "vmcnt range");
@@ -274,37 +279,76 @@ q4_gemm6_kernel(Gemm4Args a) {
         }
 }
 
-// Same requirements as q4_gemm5 (N % 128 == 0, 16-byte aligned W and X rows)
-// and the same plan; used with 256-row tiles only.
-hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
-                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s) {
-    G4Cfg c = gemm5_config(M, K, N);
-    if (c.bm != G6_BM) return hipErrorInvalidValue;
-    Gemm4Args a;
-    a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
-    a.M = M; a.nb = K / QK; a.N = N;
-    a.tiles_n = (N + G4_BN - 1) / G4_BN;
-    a.tiles_m = (M + G6_BM - 1) / G6_BM;
-    a.S = c.S;
-    a.partials = nullptr;
-    if (c.S > 1) {
-        if (!ws) return hipErrorInvalidValue;
-        a.partials = (float *)((char *)ws + COUNTER_BYTES);
-    }
+// Plan of the 4-wave form (two workgroups per CU): 128-row tiles, K split
+// (powers of two, at least 16 steps per split) until about 384 workgroups have
+// work.  MCQ4_GEMM4_SPLIT overrides.
+static G4Cfg gemm6_config1(int64_t M, int64_t K, int64_t N) {
+    G4Cfg c{128, 1};
+    const int64_t t = ((M + 127) / 128) * ((N + G4_BN - 1) / G4_BN);
+    const int64_t nb = K / QK;
+    while (t * c.S < 384 && nb / (c.S * 2) >= 16 && c.S < 16) c.S *= 2;
+    if (const char *env = getenv("MCQ4_GEMM4_SPLIT")) c.S = std::max(1, std::min(16, atoi(env)));
+    if (c.S > nb) c.S = 1;
+    return c;
+}
+
+// Workgroup rows: MCQ4_GEMM6_WGM=1|2 (default 1: two 4-wave workgroups per CU
+// match or beat one 8-wave workgroup on every shape measured -- M=128
+// K=N=4096: 23 vs 31 us; M=512 K=11008 N=4096: 64 vs 70 us; M=2048: equal).
+static int gemm6_wgm() {
+    if (const char *env = getenv("MCQ4_GEMM6_WGM")) return atoi(env) == 2 ? 2 : 1;
+    return 1;
+}
+
+size_t gemm6_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    const G4Cfg c = gemm6_config1(M, K, N);
+    if (c.S == 1) return 0;
+    const int64_t t = ((M + 127) / 128) * ((N + G4_BN - 1) / G4_BN);
+    return COUNTER_BYTES + (size_t)t * c.S * 128 * G4_BN * sizeof(float);
+}
+
+template <int WGM>
+static hipError_t launch_g6(Gemm4Args &a, hipStream_t s) {
+    constexpr size_t lds = g6_lds_bytes<WGM>();
     static std::atomic<uint64_t> done{0};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)q4_gemm6_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)G6_LDS);
+        e = hipFuncSetAttribute((const void *)q4_gemm6_kernel<WGM>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL(q4_gemm6_kernel, dim3(a.tiles_m * a.tiles_n, 1, a.S), dim3(512), G6_LDS, s, a);
-    if (a.S > 1) return launch_gemm4_reduce(a, G6_BM, s);
+    hipLaunchKernelGGL((q4_gemm6_kernel<WGM>), dim3(a.tiles_m * a.tiles_n, 1, a.S), dim3(256 * WGM), lds, s, a);
+    if (a.S > 1) return launch_gemm4_reduce(a, 128 * WGM, s);
     return hipGetLastError();
+}
+
+// Same requirements as q4_gemm5 (N % 128 == 0, 16-byte aligned W and X rows).
+// WGM = 2 uses q4_gemm5's plan (256-row tiles); WGM = 1 its own.  The
+// workspace bound covers both (gemm5_workspace_bytes, gemm6_workspace_bytes).
+hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s) {
+    int wgm = gemm6_wgm();
+    G4Cfg c = wgm == 2 ? gemm5_config(M, K, N) : gemm6_config1(M, K, N);
+    if (c.bm != 128 * wgm) {                     // the 8-wave form needs 256-row tiles
+        wgm = 1;
+        c = gemm6_config1(M, K, N);
+    }
+    Gemm4Args a;
+    a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
+    a.M = M; a.nb = K / QK; a.N = N;
+    a.tiles_n = (N + G4_BN - 1) / G4_BN;
+    a.tiles_m = (M + c.bm - 1) / c.bm;
+    a.S = c.S;
+    a.partials = nullptr;
+    if (c.S > 1) {
+        if (!ws) return hipErrorInvalidValue;
+        a.partials = (float *)((char *)ws + COUNTER_BYTES);
+    }
+    return wgm == 2 ? launch_g6<2>(a, s) : launch_g6<1>(a, s);
 }
 
 }  // namespace mcq4

@@ -207,6 +207,8 @@ PATHS = {
     "gemm5_split5_bm256": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM4_SPLIT": "5", "MCQ4_GEMM2_BM": "256"},
     "gemm6": {"MCQ4_GEMM_PATH": "6"},
     "gemm6_split3": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "3"},
+    "gemm6_wgm1": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_WGM": "1"},
+    "gemm6_wgm1_split3": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_WGM": "1", "MCQ4_GEMM4_SPLIT": "3"},
 }
 PATH_SHAPES = {
     "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
@@ -245,6 +247,9 @@ PATH_SHAPES = {
     "gemm6": [(129, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
               (200, 32, 256), (130, 64, 384), (513, 96, 256), (2048, 11008, 512)],
     "gemm6_split3": [(200, 352, 384), (300, 4096, 640)],
+    "gemm6_wgm1": [(129, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
+                   (200, 32, 256), (130, 64, 384), (513, 96, 256), (2048, 11008, 512)],
+    "gemm6_wgm1_split3": [(200, 352, 384), (300, 4096, 640)],
 }
 
 
@@ -252,7 +257,7 @@ PATH_SHAPES = {
 def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM", "MCQ4_GEMV_PATH",
               "MCQ4_GEMV_RING", "MCQ4_GEMVM_WAVES", "MCQ4_GEMM4_SPLIT", "MCQ4_GEMM4_WGM",
-              "MCQ4_GEMV_WAVES"):
+              "MCQ4_GEMV_WAVES", "MCQ4_GEMM6_WGM", "MCQ4_GEMM5_SCHED"):
         monkeypatch.delenv(k, raising=False)
     for k, v in PATHS[path].items():
         monkeypatch.setenv(k, v)
