@@ -452,7 +452,7 @@ def main():
                 "frac": round(i4_gbs / HBM_PEAK_GBS, 4),
                 "traffic": I4_DECODE_TRAFFIC_BYTES,
                 "algorithmic_bytes_per_launch": i4_dec["bytes_step"] // i4_dec["launches_step"],
-                "kernel": "i4_gemv_kernel (decode GEMV, M=1)",
+                "kernel": "i4_gemv1_kernel (decode GEMV, M=1)",
                 "avg_launch_us": round(i4_t / i4_dec["launches_step"] * 1e6, 3),
             },
             "prefill": {

@@ -1,0 +1,353 @@
+// Single-row (M == 1) per-group INT4 GEMV on gfx950 with the weight stream in
+// asynchronous global->LDS copies.
+//
+// Y[1][N] = x[K] @ W, W[k][n] = (q - z) * s per (group, column), packed[K/2][N]
+// (byte row k/2: even k in the low nibble), fp16 activations, fp32 sums.  The
+// roofline is HBM bandwidth: 0.5 byte per weight plus the group's scale/zero.
+//
+// Work decomposition
+//   * Tile = 128 columns (whole 128-byte pieces of each byte row); step = 32 K
+//     (16 byte rows, 2 KiB of the tile).  Workgroup (tile, split sp) = 8 waves;
+//     wave w owns steps [(8 sp + w) spw, +spw).  Two workgroups share a CU.
+//   * Per wave, oldest first: one copy per group of the group's scale and zero
+//     rows (128 columns each, one 1 KiB slot), one copy of the range's activations (up to 16
+//     steps), then the steps: two global_load_lds_dwordx4 each (byte rows 0..7
+//     and 8..15; lane l -> row l/8, 16-byte piece l%8) into a ring of I1_R
+//     slots.  Step k+R-1 is issued into the slot step k-1 freed before the
+//     wave waits for step k; steps past the range re-copy the last one, so the
+//     vmcnt waits are exact.
+//   * Lane (c = l%16, g = l/16): columns 8c..8c+7 of the tile, byte rows
+//     4g..4g+3 of the step, i.e. K elements 8g..8g+7.  The K order inside the
+//     MFMA is [e0, e2, e1, e3, e4, e6, e5, e7] (e = 8g + i): for column 8c+j, one
+//     v_perm_b32 puts byte j of rows 4g and 4g+1 into bytes 0 and 2, and two
+//     v_and_or_b32 give the fp16 pairs {1024 + q(e0), 1024 + q(e2)} (low
+//     nibbles) and {1024 + 16 q(e1), 1024 + 16 q(e3)} (high nibbles in place).
+//     The activations x' = [x0, x2, x1/16, x3/16, x4, x6, x5/16, x7/16] are
+//     built once per step for all eight MFMAs.
+//   * Per group: P_j = sum x' B_j (MFMA chain), C = sum x' (-1024) and
+//     S = sum x' [1,1,16,16,1,1,16,16] = sum x; then acc_j += s_j (P_j + C - z_j S)
+//     = s_j sum x (q - z) in fp32.  All 16 MFMA rows are the same activation
+//     row, so element 0 of each result is used.
+//   * Epilogue: the 8 waves' sums in wave order through LDS; with K split over
+//     workgroups, the splits are summed by the last-arriving workgroup of the
+//     tile in split order (agent-scope stores and loads, no fence), as in the
+//     general INT4 GEMV.  Store act(sum) as fp16.
+#include <algorithm>
+#include <atomic>
+#include <stdlib.h>
+
+#include "i4_common.h"
+
+namespace mcq4 {
+
+constexpr int I1_W = 8;          // waves per workgroup
+constexpr int I1_TC = 128;       // tile columns
+constexpr int I1_STEP = 2048;    // bytes per step and tile (16 byte rows x 128)
+constexpr int I1_R = 3;          // ring slots (steps) per wave
+constexpr int I1_XB = 1024;      // activation bytes per wave (16 steps)
+constexpr int I1_SMAX = 16;      // K splits at most
+
+struct I4Gemv1Args {
+    const _Float16 *X;
+    const uint8_t *P;
+    const void *scales, *zeros;
+    _Float16 *Y;
+    int K, N, nsteps, spg, spw, S;
+    int ngr_max;          // scale/zero slots per wave
+    int wave_bytes;       // LDS bytes per wave
+    float *part;          // [tiles][S][128] when S > 1
+    uint32_t *counters;   // [tiles]
+};
+
+constexpr int I1_SZSLOT = 1024; // scale/zero bytes per group (one 16-byte-per-lane copy)
+
+template <int SZ, int ACT>
+__global__ void __launch_bounds__(I1_W * 64, 2)
+i4_gemv1_kernel(I4Gemv1Args a) {
+    constexpr int ESZ = SZ == DT_F32 ? 4 : 2;
+    constexpr int SLOT = I1_SZSLOT;
+    constexpr int PPR = I1_TC * ESZ / 16;        // 16-byte pieces per scale (or zero) row
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c = lane & 15, g = lane >> 4;
+    const int G = (int)gridDim.x, G8 = G & ~7;
+    int t = (int)blockIdx.x;
+    if (t < G8) t = (t & 7) * (G8 >> 3) + (t >> 3);      // consecutive tiles on one XCD
+    const int sp = (int)blockIdx.y;
+    const int N = a.N;
+    const int col0 = t * I1_TC;
+    const int s_begin = (sp * I1_W + wave) * a.spw;
+    const int ns = max(0, min(a.spw, a.nsteps - s_begin));
+
+    uint8_t *const wl = smem + wave * a.wave_bytes;      // [ring R x 2 KiB][x 1 KiB][s/z slots]
+    uint8_t *const ring = wl;
+    uint8_t *const xs = wl + I1_R * I1_STEP;
+    uint8_t *const szs = xs + I1_XB;
+
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+
+    if (ns > 0) {
+        // ---- scale/zero rows of the wave's groups, then its activations ----
+        const int g_first = s_begin / a.spg;
+        const int ngr = (s_begin + ns - 1) / a.spg - g_first + 1;      // <= ngr_max by launch
+        {
+            // One 16-byte-per-lane copy per group: the scale row's PPR pieces, then
+            // the zero row's (slot bytes 0 .. 2*128*ESZ); for 16-bit dtypes lanes
+            // 32..63 re-read lanes 0..31's pieces into the slot's unused half.
+            const int li = lane % (2 * PPR);
+            const bool is_z = li >= PPR;
+            const uint8_t *src = (const uint8_t *)(is_z ? a.zeros : a.scales) +
+                                 ((int64_t)g_first * N + col0) * ESZ + 16 * (li % PPR);
+            for (int gl = 0; gl < ngr; ++gl)
+                __builtin_amdgcn_global_load_lds(
+                    (void *)(src + (int64_t)gl * N * ESZ),
+                    (__attribute__((address_space(3))) void *)(szs + gl * SLOT), 16, 0, 0);
+        }
+        {
+            // 16 halves-pieces of 8 activations; pieces past K re-read the last one.
+            const int e = min(s_begin * 32 + 8 * lane, a.K - 8);
+            __builtin_amdgcn_global_load_lds((void *)(a.X + e),
+                                             (__attribute__((address_space(3))) void *)xs, 16, 0, 0);
+        }
+
+        // ---- weight steps ----
+        const uint8_t *wsrc = a.P + ((int64_t)s_begin * 16 + (lane >> 3)) * N + col0 + 16 * (lane & 7);
+        auto issue = [&](int k) {                     // step k of the range into slot k % R
+            const int kk = min(k, ns - 1);
+            const uint8_t *src = wsrc + (int64_t)kk * 16 * N;
+            uint8_t *dst = ring + (k % I1_R) * I1_STEP;
+            __builtin_amdgcn_global_load_lds((void *)src, (__attribute__((address_space(3))) void *)dst,
+                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds((void *)(src + (int64_t)8 * N),
+                                             (__attribute__((address_space(3))) void *)(dst + 1024), 16, 0, 0);
+        };
+#pragma unroll
+        for (int k = 0; k < I1_R - 1; ++k) issue(k);
+
+        const uint32_t c64 = opaque_vgpr(0x64006400u);
+        const uint32_t mlo = opaque_sgpr(0x000F000Fu), mhi = opaque_sgpr(0x00F000F0u);
+        const half8_t negc = bitcast<half8_t>(uint4_t{0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u});
+        const half8_t ew = bitcast<half8_t>(uint4_t{0x3C003C00u, 0x4C004C00u, 0x3C003C00u, 0x4C004C00u});
+        const half2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+        const float4_t zf = {0.f, 0.f, 0.f, 0.f};
+        float4_t P[8], Cc = zf, Sx = zf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) P[j] = zf;
+
+        auto flush = [&](int gl) {
+            const lds_u8 *sl = lds_ptr(lds_addr(szs + gl * SLOT));
+            float sv[8], zv[8];
+            if constexpr (SZ == DT_F32) {
+                typedef __attribute__((address_space(3))) float4_t lds_f4;
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const float4_t s4 = *(const lds_f4 *)(sl + 32 * c + 16 * h);
+                    const float4_t z4 = *(const lds_f4 *)(sl + 4 * I1_TC + 32 * c + 16 * h);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) { sv[4 * h + i] = s4[i]; zv[4 * h + i] = z4[i]; }
+                }
+            } else {
+                const uint4_t s4 = *(const __attribute__((address_space(3))) uint4_t *)(sl + 16 * c);
+                const uint4_t z4 = *(const __attribute__((address_space(3))) uint4_t *)(sl + 2 * I1_TC + 16 * c);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if constexpr (SZ == DT_F16) {
+                        const half2_t sh = bitcast<half2_t>(s4[i]), zh = bitcast<half2_t>(z4[i]);
+                        sv[2 * i] = (float)sh[0]; sv[2 * i + 1] = (float)sh[1];
+                        zv[2 * i] = (float)zh[0]; zv[2 * i + 1] = (float)zh[1];
+                    } else {
+                        sv[2 * i] = __uint_as_float(s4[i] << 16); sv[2 * i + 1] = __uint_as_float(s4[i] & 0xFFFF0000u);
+                        zv[2 * i] = __uint_as_float(z4[i] << 16); zv[2 * i + 1] = __uint_as_float(z4[i] & 0xFFFF0000u);
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float tq = __builtin_fmaf(-zv[j], Sx[0], P[j][0] + Cc[0]);
+                acc[j] = __builtin_fmaf(sv[j], tq, acc[j]);
+                P[j] = zf;
+            }
+            Cc = zf;
+            Sx = zf;
+        };
+
+        for (int k = 0; k < ns; ++k) {
+            issue(k + I1_R - 1);
+            wait_vmcnt<(I1_R - 1) * 2>();          // step k (and everything older) landed
+            // x' for this step: elements 8g..8g+7 of the step.
+            const uint4_t xv = *(const __attribute__((address_space(3))) uint4_t *)(
+                lds_ptr(lds_addr(xs + k * 64 + 16 * g)));
+            const uint32_t x02 = __builtin_amdgcn_perm(xv[1], xv[0], 0x05040100u);     // x0, x2
+            const uint32_t x13 = __builtin_amdgcn_perm(xv[1], xv[0], 0x07060302u);     // x1, x3
+            const uint32_t x46 = __builtin_amdgcn_perm(xv[3], xv[2], 0x05040100u);     // x4, x6
+            const uint32_t x57 = __builtin_amdgcn_perm(xv[3], xv[2], 0x07060302u);     // x5, x7
+            const half8_t xq = bitcast<half8_t>(uint4_t{x02, bitcast<uint32_t>(bitcast<half2_t>(x13) * s16),
+                                                        x46, bitcast<uint32_t>(bitcast<half2_t>(x57) * s16)});
+            Cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq, negc, Cc, 0, 0, 0);
+            Sx = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq, ew, Sx, 0, 0, 0);
+            // Byte rows 4g..4g+3, columns 8c..8c+7.
+            const lds_u8 *rs = lds_ptr(lds_addr(ring + (k % I1_R) * I1_STEP + (4 * g) * I1_TC + 8 * c));
+            u32x2 r[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[i] = *(const __attribute__((address_space(3))) u32x2 *)(rs + i * I1_TC);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int h = j >> 2, b = j & 3;
+                // bytes 0 and 2 <- byte b of the first and second row of the pair
+                // (v_perm_b32 selector values 0-3 pick bytes of the second operand, 4-7 of the first)
+                const uint32_t sel = (uint32_t)b | (uint32_t)(4 + b) << 16 | 0x0C000C00u;
+                const uint32_t p01 = __builtin_amdgcn_perm(r[1][h], r[0][h], sel);
+                const uint32_t p23 = __builtin_amdgcn_perm(r[3][h], r[2][h], sel);
+                const uint4_t bq = {and_or(p01, mlo, c64), and_or(p01, mhi, c64),
+                                    and_or(p23, mlo, c64), and_or(p23, mhi, c64)};
+                P[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq, bitcast<half8_t>(bq), P[j], 0, 0, 0);
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");     // slot reads done before its refill
+            const int sg = s_begin + k;
+            if ((sg + 1) % a.spg == 0 || k == ns - 1) flush(sg / a.spg - g_first);
+        }
+        wait_vmcnt<0>();
+    }
+
+    // ---- ordered sum over the waves ----
+    __syncthreads();
+    float *red = (float *)smem;                   // [8 waves][128]
+    if (g == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) red[wave * I1_TC + 8 * c + j] = acc[j];
+    }
+    __syncthreads();
+    if (a.S == 1) {
+        if (tid < I1_TC) {
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < I1_W; ++w) sum += red[w * I1_TC + tid];
+            a.Y[col0 + tid] = (_Float16)activate<ACT>(sum);
+        }
+        return;
+    }
+    // Split K: write-through partial stores, a ticket on the tile's counter, and
+    // the last workgroup sums every split's partial (L2-bypassing loads) in order.
+    float *part = a.part + ((int64_t)t * a.S + sp) * I1_TC;
+    if (tid < I1_TC) {
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < I1_W; ++w) sum += red[w * I1_TC + tid];
+        __hip_atomic_store(part + tid, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    uint32_t *last_flag = (uint32_t *)smem;
+    if (tid == 0) {
+        const uint32_t prev =
+            __hip_atomic_fetch_add(&a.counters[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last_flag = prev == (uint32_t)(a.S - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!*last_flag) return;
+    if (tid < I1_TC) {
+        const float *base = a.part + (int64_t)t * a.S * I1_TC + tid;
+        float sum = 0.f;
+        for (int q0 = 0; q0 < a.S; q0 += 8) {
+            float pv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                pv[i] = __hip_atomic_load(base + (int64_t)min(q0 + i, a.S - 1) * I1_TC, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (q0 + i < a.S) sum += pv[i];
+        }
+        a.Y[col0 + tid] = (_Float16)activate<ACT>(sum);
+    }
+    if (tid == 0) __hip_atomic_store(&a.counters[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+struct I1Cfg {
+    int spw, S, ngr_max;
+};
+
+// Steps per wave: about 4096 waves in flight (16 per CU), 2..16 steps each;
+// MCQ4_I4_SPW1 overrides.  Then the split count and the scale/zero slots a
+// wave's range can touch.
+static I1Cfg i4_gemv1_config(int64_t K, int64_t N, int64_t gs) {
+    const int64_t nsteps = K / 32, spg = gs / 32, ntiles = N / I1_TC;
+    int64_t spw = (ntiles * nsteps + 4095) / 4096;
+    if (const char *env = getenv("MCQ4_I4_SPW1")) spw = atoi(env);
+    spw = std::max<int64_t>(spw, (nsteps + I1_W * I1_SMAX - 1) / (I1_W * I1_SMAX));
+    spw = std::min<int64_t>(std::max<int64_t>(spw, 2), 16);
+    const int64_t S = (nsteps + I1_W * spw - 1) / (I1_W * spw);
+    const int64_t ngr = spw % spg == 0 ? spw / spg : (spw + spg - 1) / spg + 1;
+    return {(int)spw, (int)S, (int)ngr};
+}
+
+// M == 1, 4-bit weights, whole 128-column tiles, group size a multiple of 32,
+// 16-byte aligned operands, and a split count within bounds.
+bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, const void *P,
+                        const void *scales, const void *zeros) {
+    if (const char *env = getenv("MCQ4_I4_GEMV1"))
+        if (env[0] == '0') return false;
+    if (M != 1 || K < 32 || K % 32 || gs % 32 || N % I1_TC || N / I1_TC > COUNTER_SLOTS) return false;
+    if (((uintptr_t)X % 16) || ((uintptr_t)P % 16) || ((uintptr_t)scales % 16) || ((uintptr_t)zeros % 16))
+        return false;
+    const I1Cfg c = i4_gemv1_config(K, N, gs);
+    return c.S <= I1_SMAX && (size_t)I1_W * (I1_R * I1_STEP + I1_XB + c.ngr_max * I1_SZSLOT) <= 160 * 1024;
+}
+
+size_t i4_gemv1_workspace_bytes(int64_t K, int64_t N, int64_t gs) {
+    const I1Cfg c = i4_gemv1_config(K, N, gs);
+    if (c.S == 1) return 0;
+    return COUNTER_BYTES + (size_t)(N / I1_TC) * c.S * I1_TC * sizeof(float);
+}
+
+template <int SZ, int ACT>
+static hipError_t launch_i1(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
+    const size_t lds = (size_t)I1_W * a.wave_bytes;
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(done.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void *)i4_gemv1_kernel<SZ, ACT>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        done.fetch_or(bit, std::memory_order_acq_rel);
+    }
+    hipLaunchKernelGGL((i4_gemv1_kernel<SZ, ACT>), dim3(ntiles, a.S), dim3(I1_W * 64), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int SZ>
+static hipError_t launch_i1_act(const I4Gemv1Args &a, int ntiles, int act, hipStream_t s) {
+    if (act == ACT_SILU) return launch_i1<SZ, ACT_SILU>(a, ntiles, s);
+    if (act == ACT_GELU) return launch_i1<SZ, ACT_GELU>(a, ntiles, s);
+    return launch_i1<SZ, ACT_NONE>(a, ntiles, s);
+}
+
+hipError_t launch_i4_gemv1(const _Float16 *X, const uint8_t *P, const void *scales, const void *zeros,
+                           int sz_dt, _Float16 *Y, int K, int N, int gs, int act, void *ws, hipStream_t s) {
+    const I1Cfg c = i4_gemv1_config(K, N, gs);
+    I4Gemv1Args a;
+    a.X = X; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y;
+    a.K = K; a.N = N; a.nsteps = K / 32; a.spg = gs / 32; a.spw = c.spw; a.S = c.S;
+    a.ngr_max = c.ngr_max;
+    a.wave_bytes = I1_R * I1_STEP + I1_XB + c.ngr_max * I1_SZSLOT;
+    a.part = nullptr; a.counters = nullptr;
+    if (c.S > 1) {
+        if (!ws) return hipErrorInvalidValue;
+        a.counters = (uint32_t *)ws;
+        a.part = (float *)((char *)ws + COUNTER_BYTES);
+    }
+    if ((size_t)I1_W * a.wave_bytes > 160 * 1024) return hipErrorInvalidValue;
+    const int ntiles = N / I1_TC;
+    if (sz_dt == DT_F32) return launch_i1_act<DT_F32>(a, ntiles, act, s);
+    if (sz_dt == DT_F16) return launch_i1_act<DT_F16>(a, ntiles, act, s);
+    return launch_i1_act<DT_BF16>(a, ntiles, act, s);
+}
+
+}  // namespace mcq4

@@ -342,3 +342,49 @@ def test_matmul_int8_other_dtypes(mo, dev, xdt):
                        torch.from_numpy(z).to(dev), gs)
     assert Y.dtype == xdt
     _check_rows(Y.float().cpu().numpy(), R.matmul_int8_f32(X.float().numpy(), q, s, z, gs))
+
+
+# ---- M == 1 async-copy GEMV (i4_gemv1.hip) ----------------------------------------
+
+GEMV1_CASES = [
+    # (K, N, gs, steps per wave of the split-K GEMV or None for its default plan)
+    (4096, 4096, 128, None), (4096, 12288, 128, None), (11008, 4096, 128, None),
+    (4096, 1024, 32, None), (2048, 512, 64, 3), (4096, 256, 128, 2), (4096, 384, 128, 16),
+    (160, 128, 32, 2), (32, 128, 32, None), (14336, 512, 256, 5), (16384, 256, 512, None),
+    (4096, 4112, 128, None), (11008, 1040, 64, None), (288, 144, 32, None), (1024, 16400, 128, None),
+]
+
+
+@pytest.mark.parametrize("K,N,gs,spw", GEMV1_CASES)
+@pytest.mark.parametrize("sz", [R.F32, R.F16, R.BF16])
+def test_gemv1_paths(mo, dev, monkeypatch, K, N, gs, spw, sz):
+    """The M == 1 async-copy GEMV and the register-ring GEMV against the oracle:
+    split and unsplit plans, ragged step ranges, group sizes 32..512, N not a
+    multiple of 128 (register ring only), all scale dtypes."""
+    print(f"gemv1 K={K} N={N} gs={gs} spw={spw} sz={sz}", flush=True)
+    for k in ("MCQ4_I4_SPW1", "MCQ4_I4_GEMV1", "MCQ4_I4_PATH"):
+        monkeypatch.delenv(k, raising=False)
+    if spw is not None:
+        monkeypatch.setenv("MCQ4_I4_SPW1", str(spw))
+    w, packed, s, z = _quant(mo, dev, K, N, gs, sz, seed=K + N + gs)
+    X = torch.randn(1, K, generator=torch.Generator().manual_seed(K)).half().to(dev)
+    Yref = _ref(X, packed, s, z, gs)
+    for rep in range(2):                       # split-K counters are left at zero
+        _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
+    # the register-ring GEMV
+    monkeypatch.setenv("MCQ4_I4_GEMV1", "0")
+    _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu"])
+def test_gemv1_fused_activation(mo, dev, act):
+    K, N, gs = 4096, 1024, 128
+    w, packed, s, z = _quant(mo, dev, K, N, gs, seed=41)
+    X = (torch.randn(1, K, generator=torch.Generator().manual_seed(9)) * 4).half().to(dev)
+    fn = mo.matmul_int4_silu if act == "silu" else mo.matmul_int4_gelu
+    Y = fn(X, packed, s, z, gs).float().cpu().numpy().astype(np.float64)
+    base = _ref(X, packed, s, z, gs).astype(np.float64)
+    want = _silu(base) if act == "silu" else _gelu_tanh(base)
+    assert np.isfinite(Y).all()
+    scale = np.maximum(np.abs(base).max(axis=-1, keepdims=True), 1e-6)
+    assert (np.abs(Y - want) / scale).max() <= 1e-2
