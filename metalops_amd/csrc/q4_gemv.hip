@@ -65,6 +65,7 @@ struct GemvArgs {
 template <int R>
 __device__ __forceinline__ void gv_wait(int pending) {
     // Wait until at most `pending` items (LOADS copies each) are still in flight.
+    if (R > 4 && pending >= 4) { wait_vmcnt<4 * GV_LOADS>(); return; }
     if (R > 3 && pending >= 3) { wait_vmcnt<3 * GV_LOADS>(); return; }
     if (R > 2 && pending >= 2) { wait_vmcnt<2 * GV_LOADS>(); return; }
     if (R > 1 && pending >= 1) { wait_vmcnt<1 * GV_LOADS>(); return; }
@@ -170,9 +171,11 @@ q4_gemv_dma_kernel(GemvArgs a) {
         for (int j = 0; j < TPW; ++j) {
             if (j < ntl) {
                 if (k + R - 1 < nmine) issue_next();
-                gv_wait<R>(min(R - 1, nmine - 1 - k));
                 if (j == 0) {
-                    // The batch's activations (copied before any weights, so landed).
+                    // The batch's activations, built while item k is still in flight:
+                    // they were copied before any weights, so at most the items in
+                    // flight (this one included) are newer.
+                    gv_wait<R + 1>(min(R, nmine - k));
                     const uint32_t xa = lds_addr(xs + m * (GV_B * 64) + 16 * g);
 #pragma unroll
                     for (int u = 0; u < GV_B; ++u) {
@@ -187,6 +190,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
                         negs[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], negc, z, 0, 0, 0);
                     }
                 }
+                gv_wait<R>(min(R - 1, nmine - 1 - k));
                 const uint32_t base = lds_addr(ring + slot * GV_SLOT);
                 const uint32_t qa = base + qal, da = base + doff;
                 auto row = [&](int u) {
