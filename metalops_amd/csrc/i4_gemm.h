@@ -1,0 +1,29 @@
+// Shared arguments of the per-group INT4 / INT8 prefill GEMMs (i4_gemm,
+// i4_gemm6): output tiles of BM x 256, optional split-K over grid.z with fp32
+// partial tiles [tile][split][BM x 256] in the caller's workspace, summed by
+// i4_gemm_reduce_kernel (which applies the fused activation).
+#pragma once
+
+#include "i4_common.h"
+
+namespace mcq4 {
+
+constexpr int I4G_BN = 256;
+
+struct I4GemmArgs {
+    const _Float16 *X;
+    int64_t ldx;
+    const uint8_t *P;
+    const void *scales, *zeros;
+    void *Y;
+    int64_t ldy;
+    int M, nsteps, N, spg;
+    int tiles_m, tiles_n;
+    int S;               // K splits (grid.z)
+    float *partials;     // [tiles][S][BM*256] when S > 1
+};
+
+// Sums the S partial tiles per output tile in split order and stores act(sum) as fp16.
+hipError_t launch_i4_gemm_reduce(const I4GemmArgs &a, int bm, int act, hipStream_t s);
+
+}  // namespace mcq4

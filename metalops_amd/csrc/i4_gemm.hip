@@ -33,11 +33,10 @@
 #include <atomic>
 #include <type_traits>
 
-#include "i4_common.h"
+#include "i4_gemm.h"
 
 namespace mcq4 {
 
-constexpr int I4G_BN = 256;
 constexpr int I4G_P = 3;                       // steps in flight ahead of the MFMAs
 constexpr int I4G_R = I4G_P + 1;               // raw ring slots per wave
 
@@ -52,18 +51,7 @@ struct I4gFmt {
     static constexpr size_t LDS = (size_t)4 * I4G_R * SLOT;  // 4 waves
 };
 
-struct I4GemmArgs {
-    const _Float16 *X;
-    int64_t ldx;
-    const uint8_t *P;
-    const void *scales, *zeros;
-    void *Y;
-    int64_t ldy;
-    int M, nsteps, N, spg;
-    int tiles_m, tiles_n;
-    int S;               // K splits (grid.z)
-    float *partials;     // [tiles][S][BM*256] when S > 1
-};
+
 
 template <int BM, int SZ, int ACT, int WB>
 __global__ void __launch_bounds__(256, 1)
@@ -360,6 +348,21 @@ i4_gemm_reduce_kernel(I4GemmArgs a) {
     *(half4_t *)((_Float16 *)a.Y + (int64_t)m * a.ldy + n) = v;
 }
 
+hipError_t launch_i4_gemm_reduce(const I4GemmArgs &a, int bm, int act, hipStream_t s) {
+    const int64_t n4 = (int64_t)a.tiles_m * a.tiles_n * (bm * I4G_BN / 4);
+    const dim3 grid((unsigned)((n4 + 255) / 256));
+    if (bm == 256) {
+        if (act == ACT_SILU) hipLaunchKernelGGL((i4_gemm_reduce_kernel<256, ACT_SILU>), grid, dim3(256), 0, s, a);
+        else if (act == ACT_GELU) hipLaunchKernelGGL((i4_gemm_reduce_kernel<256, ACT_GELU>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((i4_gemm_reduce_kernel<256, ACT_NONE>), grid, dim3(256), 0, s, a);
+    } else {
+        if (act == ACT_SILU) hipLaunchKernelGGL((i4_gemm_reduce_kernel<128, ACT_SILU>), grid, dim3(256), 0, s, a);
+        else if (act == ACT_GELU) hipLaunchKernelGGL((i4_gemm_reduce_kernel<128, ACT_GELU>), grid, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((i4_gemm_reduce_kernel<128, ACT_NONE>), grid, dim3(256), 0, s, a);
+    }
+    return hipGetLastError();
+}
+
 template <int BM, int SZ, int ACT, int WB>
 static hipError_t launch_i4g(const I4GemmArgs &a, hipStream_t s) {
     constexpr size_t lds = I4gFmt<WB>::LDS;
@@ -379,11 +382,7 @@ static hipError_t launch_i4g(const I4GemmArgs &a, hipStream_t s) {
     }
     hipLaunchKernelGGL((i4_gemm_kernel<BM, SZ, ACT, WB>), dim3(a.tiles_m * a.tiles_n, 1, a.S),
                        dim3(256), lds, s, a);
-    if (a.S > 1) {
-        const int64_t n4 = (int64_t)a.tiles_m * a.tiles_n * (BM * I4G_BN / 4);
-        hipLaunchKernelGGL((i4_gemm_reduce_kernel<BM, ACT>), dim3((unsigned)((n4 + 255) / 256)),
-                           dim3(256), 0, s, a);
-    }
+    if (a.S > 1) return launch_i4_gemm_reduce(a, BM, ACT, s);
     return hipGetLastError();
 }
 
@@ -428,16 +427,26 @@ static I4GCfg i4_gemm_config(int64_t M, int64_t K, int64_t N) {
     return c;
 }
 
+bool i4_gemm6_supported(int wb, int sz_dt, int64_t K, int64_t N, int64_t gs, const void *Y, int64_t ldy);
+size_t i4_gemm6_workspace_bytes(int64_t M, int64_t K, int64_t N);
+hipError_t launch_i4_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
+                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K, int N,
+                           int gs, int act, void *ws, hipStream_t s);
+
+// Covers both prefill kernels (i4_gemm6 for 4-bit weights with 16-bit
+// scales/zeros, this one otherwise).
 size_t i4_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     const I4GCfg c = i4_gemm_config(M, K, N);
-    if (c.S == 1) return 0;
     const int64_t t = ((M + c.bm - 1) / c.bm) * ((N + I4G_BN - 1) / I4G_BN);
-    return COUNTER_BYTES + (size_t)t * c.S * c.bm * I4G_BN * sizeof(float);
+    const size_t own = c.S == 1 ? 0 : COUNTER_BYTES + (size_t)t * c.S * c.bm * I4G_BN * sizeof(float);
+    return std::max(own, i4_gemm6_workspace_bytes(M, K, N));
 }
 
 hipError_t launch_i4_gemm(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K,
                           int N, int gs, int act, void *ws, hipStream_t s, int wb) {
+    if (i4_gemm6_supported(wb, sz_dt, K, N, gs, Y, ldy))
+        return launch_i4_gemm6(X, ldx, P, scales, zeros, sz_dt, Y, ldy, M, K, N, gs, act, ws, s);
     const I4GCfg c = i4_gemm_config(M, K, N);
     I4GemmArgs a;
     a.X = X; a.ldx = ldx; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y; a.ldy = ldy;

@@ -388,3 +388,23 @@ def test_gemv1_fused_activation(mo, dev, act):
     assert np.isfinite(Y).all()
     scale = np.maximum(np.abs(base).max(axis=-1, keepdims=True), 1e-6)
     assert (np.abs(Y - want) / scale).max() <= 1e-2
+
+
+# ---- prefill GEMM with the activation tile in LDS (i4_gemm6.hip) --------------------
+
+@pytest.mark.parametrize("M,K,N,gs", [(17, 512, 256, 128), (130, 96, 384, 32), (300, 2048, 768, 64),
+                                      (512, 4096, 1024, 128), (2048, 1024, 512, 128), (129, 11008, 256, 128),
+                                      (64, 160, 640, 32)])
+@pytest.mark.parametrize("sz", [R.F16, R.BF16])
+def test_gemm6_paths(mo, dev, monkeypatch, M, K, N, gs, sz):
+    """i4_gemm6 and i4_gemm against the oracle: split K, odd step counts, ragged M."""
+    print(f"gemm6 M={M} K={K} N={N} gs={gs} sz={sz}", flush=True)
+    monkeypatch.delenv("MCQ4_I4_GEMM6", raising=False)
+    monkeypatch.delenv("MCQ4_I4_PATH", raising=False)
+    w, packed, s, z = _quant(mo, dev, K, N, gs, sz, seed=M + K + gs)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).half().to(dev)
+    Yref = _ref(X, packed, s, z, gs)
+    for rep in range(2):
+        _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
+    monkeypatch.setenv("MCQ4_I4_GEMM6", "0")
+    _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
