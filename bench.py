@@ -39,9 +39,9 @@ FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
 # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the same
 # workloads (bench.py --part decode|prefill), each counter scaled by what it reads
 # for a plain 256 MiB device copy (FETCH_SIZE x 2, WRITE_SIZE x 1).  Figures and
-# commands: profiles/gemv_dma_llama7b_m1.md, profiles/gemm5_llama7b_m2048.md.
-DECODE_TRAFFIC_BYTES = 22985587       # average over the five projections
-PREFILL_UP_TRAFFIC_BYTES = 360943002  # 302.1 MB read + 58.8 MB written
+# commands: profiles/gemv_dma_llama7b_m1.md, profiles/gemm6_llama7b_m2048.md.
+DECODE_TRAFFIC_BYTES = 22995538       # average over the five projections
+PREFILL_UP_TRAFFIC_BYTES = 596460441  # 537.5 MB read + 59.0 MB written
 
 DECODE_LAYER = [  # (name, K, N) -- Llama-2-7B projections, configs[1]
     ("qkv", 4096, 12288),
@@ -53,10 +53,10 @@ DECODE_LAYER = [  # (name, K, N) -- Llama-2-7B projections, configs[1]
 PREFILL = [("up", 2048, 4096, 14336), ("down", 2048, 14336, 4096)]
 I4_GROUP = 128
 # HBM bytes per launch of the INT4 kernels (rocprofv3 FETCH_SIZE / WRITE_SIZE over
-# bench.py --part int4-decode|int4-prefill, scaled as above; profiles/i4_gemv_llama7b_m1.md,
-# profiles/i4_gemm_llama7b_m2048.md).
-I4_DECODE_TRAFFIC_BYTES = 22276567        # average over the five projections
-I4_PREFILL_UP_TRAFFIC_BYTES = 378583965   # 307.9 MB read + 70.6 MB written
+# bench.py --part int4-decode|int4-prefill, scaled as above; profiles/i4_gemv1_llama7b_m1.md,
+# profiles/i4_gemm6_llama7b_m2048.md).
+I4_DECODE_TRAFFIC_BYTES = 22208041        # average over the five projections
+I4_PREFILL_UP_TRAFFIC_BYTES = 584072806   # 525.4 MB read + 58.7 MB written
 
 
 def wbytes(K, N):
