@@ -39,6 +39,8 @@ struct GemvMArgs {
     _Float16 *Y;
     int64_t ldy;
     int M, nb, N, ntiles, nbt;
+    int S, bps;          // K splits (grid.y) and batches per split
+    float *part;         // [S][M][16 * ntiles] fp32 partials when S > 1 (after the counter area)
 };
 
 template <int WAVES, int TPW>
@@ -59,7 +61,11 @@ q4_gemvm_kernel(GemvMArgs a) {
     int wg = (int)blockIdx.x;
     if (wg < G8) wg = (wg & 7) * (G8 >> 3) + (wg >> 3);
     const int ntl = min(TPW, (a.ntiles - wg + G - 1) / G);
-    const int nbm = a.nbt > wave ? (a.nbt - wave + WAVES - 1) / WAVES : 0;
+    // This split's batches [b0, b0 + nbs); wave w owns b0 + w, b0 + w + WAVES, ...
+    const int sp = (int)blockIdx.y;
+    const int b0 = sp * a.bps;
+    const int nbs = max(0, min(a.bps, a.nbt - b0));
+    const int nbm = nbs > wave ? (nbs - wave + WAVES - 1) / WAVES : 0;
     const int nmine = nbm * ntl;
 
     int crow[3];
@@ -73,13 +79,13 @@ q4_gemvm_kernel(GemvMArgs a) {
     const uint8_t *xrow = (const uint8_t *)a.X + (int64_t)min(c, a.M - 1) * a.ldx * 2 + 16 * g;
     uint4_t xr[GM_B];
     auto load_x = [&](int m) {
-        const int row0 = (wave + WAVES * m) * GM_B;
+        const int row0 = (b0 + wave + WAVES * m) * GM_B;
 #pragma unroll
         for (int u = 0; u < GM_B; ++u)
             xr[u] = *(const uint4_t *)(xrow + (int64_t)min(row0 + u, a.nb - 1) * (QK * 2));
     };
     auto copy_item = [&](int m, int j, int slot) {
-        const int row0 = (wave + WAVES * m) * GM_B;
+        const int row0 = (b0 + wave + WAVES * m) * GM_B;
         const int rows = min(GM_B, a.nb - row0);
         const uint8_t *wb = a.W + (int64_t)(wg + j * G) * GM_ROW + (int64_t)row0 * grow;
 #pragma unroll
@@ -118,7 +124,7 @@ q4_gemvm_kernel(GemvMArgs a) {
 
     int k = 0, slot = 0;
     for (int m = 0; m < nbm; ++m) {
-        const int rows = min(GM_B, a.nb - (wave + WAVES * m) * GM_B);
+        const int rows = min(GM_B, a.nb - (b0 + wave + WAVES * m) * GM_B);
         half8_t xq[GM_B];
 #pragma unroll
         for (int u = 0; u < GM_B; ++u) {
@@ -189,8 +195,22 @@ q4_gemvm_kernel(GemvMArgs a) {
         float s = 0.f;
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) s += red[((j * WAVES + w) * 16 + rr) * 16 + col];
-        a.Y[(int64_t)rr * a.ldy + (wg + j * G) * 16 + col] = (_Float16)s;
+        const int n = (wg + j * G) * 16 + col;
+        if (a.S == 1) a.Y[(int64_t)rr * a.ldy + n] = (_Float16)s;
+        else a.part[((int64_t)sp * a.M + rr) * (16 * a.ntiles) + n] = s;
     }
+}
+
+// Sums the S fp32 partials of every output in split order (deterministic) and
+// stores fp16; the kernel boundary orders it after the GEMV.
+__global__ void __launch_bounds__(256) q4_gemvm_reduce_kernel(GemvMArgs a) {
+    const int nc = 16 * a.ntiles;
+    const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (v >= (int64_t)a.M * nc) return;
+    const int rr = (int)(v / nc), n = (int)(v % nc);
+    float s = 0.f;
+    for (int sp = 0; sp < a.S; ++sp) s += a.part[((int64_t)sp * a.M + rr) * nc + n];
+    a.Y[(int64_t)rr * a.ldy + n] = (_Float16)s;
 }
 
 static size_t gemvm_lds_bytes(int waves, int tpw) {
@@ -211,7 +231,11 @@ static hipError_t launch_gemvm_t(const GemvMArgs &a, int grid, hipStream_t s) {
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL((q4_gemvm_kernel<WAVES, TPW>), dim3(grid), dim3(WAVES * 64), lds, s, a);
+    hipLaunchKernelGGL((q4_gemvm_kernel<WAVES, TPW>), dim3(grid, a.S), dim3(WAVES * 64), lds, s, a);
+    if (a.S > 1) {
+        const int64_t n = (int64_t)a.M * 16 * a.ntiles;
+        hipLaunchKernelGGL(q4_gemvm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+    }
     return hipGetLastError();
 }
 
@@ -237,22 +261,58 @@ bool gemvm_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M
            N * 18 * 8 < ((int64_t)1 << 31);
 }
 
+// K split: with one tile per 16-wave workgroup every workgroup reads the whole
+// activation block (M x K halves) from L2, and at M >= 8 those loads -- one
+// line per row per instruction -- outnumber the weight copies.  Two tiles per
+// workgroup over half of K each keeps 256 workgroups and halves the activation
+// traffic; the fp32 partials are summed in split order by a second kernel
+// (M=16 K=14336 N=4096: 15.6 us, was 18.7; M=8: 13.4, was 14.3; at M <= 4 and
+// with several tiles per workgroup it does not pay).  MCQ4_GEMVM_SPLIT=1|2|4|8
+// overrides.
+struct GmPlan {
+    int waves, tpw, grid, S, bps;
+};
+static GmPlan gemvm_plan(int64_t M, int64_t K, int64_t N) {
+    const int ntiles = (int)(N / 16), nbt = (int)((K / QK + GM_B - 1) / GM_B);
+    int waves = 16;
+    if (const char *env = getenv("MCQ4_GEMVM_WAVES")) waves = atoi(env) == 8 ? 8 : 16;
+    const int cap = waves == 8 ? 512 : 256;
+    int S = M >= 8 && ntiles <= cap && nbt >= 2 * waves ? 2 : 1;
+    if (const char *env = getenv("MCQ4_GEMVM_SPLIT")) {
+        const int v = atoi(env);
+        S = v == 2 || v == 4 || v == 8 ? v : 1;
+    }
+    S = std::max(1, std::min(S, nbt));
+    const int tpw = S > 1 ? std::min(GM_TPW_MAX, S) : std::min(GM_TPW_MAX, (ntiles + cap - 1) / cap);
+    const int grid = (ntiles + tpw - 1) / tpw;
+    const int bps = (nbt + S - 1) / S;
+    return {waves, tpw, grid, (nbt + bps - 1) / bps, bps};
+}
+
+size_t gemvm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    if (M < 2 || M > 16 || N < 16 || K < QK) return 0;
+    const GmPlan p = gemvm_plan(M, K, N);
+    // Partials follow the workspace's counter area, which other kernels rely on staying zero.
+    return p.S > 1 ? COUNTER_BYTES + (size_t)p.S * M * (N / 16) * 16 * sizeof(float) : 0;
+}
+
 hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
-                        int64_t ldy, int M, int K, int N, int *n_done, hipStream_t s) {
+                        int64_t ldy, int M, int K, int N, void *ws, int *n_done, hipStream_t s) {
     GemvMArgs a;
     a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
     a.M = M; a.nb = K / QK; a.N = N;
     a.ntiles = N / 16;
     a.nbt = (a.nb + GM_B - 1) / GM_B;
     *n_done = a.ntiles * 16;
-    // 16-wave workgroups, one per CU (8-wave ones, two per CU, as an option).
-    int waves = 16;
-    if (const char *env = getenv("MCQ4_GEMVM_WAVES")) waves = atoi(env) == 8 ? 8 : 16;
-    const int cap = waves == 8 ? 512 : 256;
-    const int tpw = std::min(GM_TPW_MAX, (a.ntiles + cap - 1) / cap);
-    const int grid = (a.ntiles + tpw - 1) / tpw;
-    if (waves == 16) return launch_gemvm_w<16>(a, grid, tpw, s);
-    return launch_gemvm_w<8>(a, grid, tpw, s);
+    const GmPlan p = gemvm_plan(M, K, N);
+    a.S = p.S; a.bps = p.bps;
+    a.part = nullptr;
+    if (p.S > 1) {
+        if (!ws) return hipErrorInvalidValue;
+        a.part = (float *)((char *)ws + COUNTER_BYTES);
+    }
+    if (p.waves == 16) return launch_gemvm_w<16>(a, p.grid, p.tpw, s);
+    return launch_gemvm_w<8>(a, p.grid, p.tpw, s);
 }
 
 }  // namespace mcq4

@@ -263,13 +263,18 @@ SkinnyCfg skinny_config(int64_t M, int64_t K, int64_t N) {
     return c;
 }
 
+size_t gemvm_workspace_bytes(int64_t M, int64_t K, int64_t N);
+
+// The larger of this kernel's split-K needs and the small-batch GEMV's.
 size_t skinny_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     const SkinnyCfg c = skinny_config(M, K, N);
-    if (c.S == 1) return 0;
-    const int MT = (int)((M + 15) / 16);
-    const int64_t tiles = (N + 16 * c.NT - 1) / (16 * c.NT);
-    const size_t part = (size_t)tiles * c.S * MT * c.NT * 256 * sizeof(float);
-    return COUNTER_BYTES + part;
+    size_t need = 0;
+    if (c.S > 1) {
+        const int MT = (int)((M + 15) / 16);
+        const int64_t tiles = (N + 16 * c.NT - 1) / (16 * c.NT);
+        need = COUNTER_BYTES + (size_t)tiles * c.S * MT * c.NT * 256 * sizeof(float);
+    }
+    return std::max(need, gemvm_workspace_bytes(M, K, N));
 }
 
 bool decode_lds_supported(const uint8_t *W, int64_t N, int64_t ldx);
@@ -283,7 +288,7 @@ hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int
 bool gemvm_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
                      int64_t N);
 hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
-                        int64_t ldy, int M, int K, int N, int *n_done, hipStream_t s);
+                        int64_t ldy, int M, int K, int N, void *ws, int *n_done, hipStream_t s);
 
 static bool use_decode_lds(const uint8_t *W, int64_t N, int64_t ldx) {
     if (const char *env = getenv("MCQ4_DECODE_PATH"))  // "direct" forces this file's kernel
@@ -299,7 +304,7 @@ hipError_t launch_skinny(const _Float16 *X, int64_t ldx, const uint8_t *W, _Floa
         if (M == 1 && gemv_dma_supported(X, W, K, N))
             e = launch_gemv_dma(X, W, Y, K, N, &n_begin, s);
         else if (gemvm_supported(X, ldx, W, M, K, N))
-            e = launch_gemvm(X, ldx, W, Y, ldy, M, K, N, &n_begin, s);
+            e = launch_gemvm(X, ldx, W, Y, ldy, M, K, N, ws, &n_begin, s);
         else
             e = launch_decode_lds(X, ldx, W, Y, ldy, M, K, N, &n_begin, s);
         if (e != hipSuccess || n_begin == N) return e;

@@ -187,6 +187,8 @@ PATHS = {
     "decode_lds_m1": {"MCQ4_GEMV_PATH": "off"},
     "gemvm": {},
     "gemvm_w8": {"MCQ4_GEMVM_WAVES": "8"},
+    "gemvm_split2": {"MCQ4_GEMVM_SPLIT": "2"},
+    "gemvm_split8": {"MCQ4_GEMVM_SPLIT": "8"},
     "decode_lds": {},
     "decode_lds_small_m": {"MCQ4_GEMV_PATH": "off"},
     "decode_direct": {"MCQ4_DECODE_PATH": "direct"},
@@ -222,6 +224,8 @@ PATH_SHAPES = {
     "gemvm": [(2, 32, 16), (3, 352, 264), (4, 1024, 4104), (5, 11008, 512), (8, 4096, 14336),
               (11, 2048, 1040), (16, 14336, 4096), (16, 352, 8200)],
     "gemvm_w8": [(2, 352, 264), (7, 4096, 1040), (16, 11008, 512)],
+    "gemvm_split2": [(2, 352, 264), (9, 4096, 1040), (16, 14336, 4096), (5, 11008, 512)],
+    "gemvm_split8": [(16, 2048, 1032), (3, 14336, 512), (12, 512, 200)],
     "decode_lds": [(1, 352, 264), (40, 2048, 96), (64, 256, 64), (17, 1024, 520), (33, 4096, 1032)],
     "decode_lds_small_m": [(3, 1024, 520), (16, 4096, 1032)],
     "decode_direct": [(1, 352, 257), (7, 1024, 520), (16, 4096, 1000), (64, 512, 72)],
@@ -257,7 +261,7 @@ PATH_SHAPES = {
 def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM", "MCQ4_GEMV_PATH",
               "MCQ4_GEMV_RING", "MCQ4_GEMVM_WAVES", "MCQ4_GEMM4_SPLIT", "MCQ4_GEMM4_WGM",
-              "MCQ4_GEMV_WAVES", "MCQ4_GEMM6_WGM", "MCQ4_GEMM5_SCHED"):
+              "MCQ4_GEMV_WAVES", "MCQ4_GEMM6_WGM", "MCQ4_GEMM5_SCHED", "MCQ4_GEMVM_SPLIT"):
         monkeypatch.delenv(k, raising=False)
     for k, v in PATHS[path].items():
         monkeypatch.setenv(k, v)
