@@ -30,8 +30,12 @@
 //     row, so element 0 of each result is used.
 //   * Epilogue: the 8 waves' sums in wave order through LDS; with K split over
 //     workgroups, the splits are summed by the last-arriving workgroup of the
-//     tile in split order (agent-scope stores and loads, no fence), as in the
-//     general INT4 GEMV.  Store act(sum) as fp16.
+//     tile in split order.  Default (XL): the grid's x extent is a multiple of
+//     8, so every split of a tile has the same linear id mod 8 and runs on one
+//     XCD; the partials go through that XCD's L2 (plain stores, L1-bypassing
+//     loads) and the 64-bit ticket verifies the placement (a violation writes
+//     NaN rather than a wrong sum).  Otherwise agent-scope stores and loads, as
+//     in the general INT4 GEMV.  Store act(sum) as fp16.
 #include <algorithm>
 #include <atomic>
 #include <stdlib.h>
@@ -61,7 +65,7 @@ struct I4Gemv1Args {
 
 constexpr int I1_SZSLOT = 1024; // scale/zero bytes per group (one 16-byte-per-lane copy)
 
-template <int SZ, int ACT>
+template <int SZ, int ACT, bool XL>
 __global__ void __launch_bounds__(I1_W * 64, 2)
 i4_gemv1_kernel(I4Gemv1Args a) {
     constexpr int ESZ = SZ == DT_F32 ? 4 : 2;
@@ -75,6 +79,7 @@ i4_gemv1_kernel(I4Gemv1Args a) {
     const int G = (int)gridDim.x, G8 = G & ~7;
     int t = (int)blockIdx.x;
     if (t < G8) t = (t & 7) * (G8 >> 3) + (t >> 3);      // consecutive tiles on one XCD
+    if (XL && t >= a.N / I1_TC) return;                  // grid padding to a multiple of 8
     const int sp = (int)blockIdx.y;
     const int N = a.N;
     const int col0 = t * I1_TC;
@@ -233,6 +238,44 @@ i4_gemv1_kernel(I4Gemv1Args a) {
     // Split K: write-through partial stores, a ticket on the tile's counter, and
     // the last workgroup sums every split's partial (L2-bypassing loads) in order.
     float *part = a.part + ((int64_t)t * a.S + sp) * I1_TC;
+    if constexpr (XL) {
+        // Ticket slots: 64-bit, 4096 per linear-id class mod 8 (one XCD each).
+        uint64_t *cnt = (uint64_t *)a.counters + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
+        const uint32_t xcc = xcc_id();
+        if (tid < I1_TC) {
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < I1_W; ++w) sum += red[w * I1_TC + tid];
+            part[tid] = sum;
+        }
+        wait_vmcnt<0>();
+        __syncthreads();
+        uint32_t *last_flag = (uint32_t *)smem;
+        if (tid == 0) {
+            const uint64_t inc = xcd_ticket_inc(xcc);
+            const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u
+                         : xcd_ticket_local(prev + inc, xcc, a.S) ? 1u : 2u;
+        }
+        __syncthreads();
+        const uint32_t lf = *last_flag;
+        if (!lf) return;
+        if (tid < I1_TC) {
+            const float *base = a.part + (int64_t)t * a.S * I1_TC;
+            float sum = 0.f;
+            for (int q0 = 0; q0 < a.S; q0 += 8) {
+                float pv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pv[i] = load_l2_f32(base, (min(q0 + i, a.S - 1) * I1_TC + tid) * 4);
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if (q0 + i < a.S) sum += pv[i];
+            }
+            a.Y[col0 + tid] = lf == 1 ? (_Float16)activate<ACT>(sum) : (_Float16)__builtin_nanf("");
+        }
+        if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     if (tid < I1_TC) {
         float sum = 0.f;
 #pragma unroll
@@ -304,7 +347,14 @@ size_t i4_gemv1_workspace_bytes(int64_t K, int64_t N, int64_t gs) {
     return COUNTER_BYTES + (size_t)(N / I1_TC) * c.S * I1_TC * sizeof(float);
 }
 
-template <int SZ, int ACT>
+// The XCD-local exchange (default; MCQ4_XCD_LOCAL=0 selects the agent-scope
+// one) needs K split and at most 4096 tiles per class of the padded grid.
+static bool use_xcd_local(int ntiles, int S) {
+    const char *env = getenv("MCQ4_XCD_LOCAL");
+    return !(env && env[0] == '0') && S > 1 && (ntiles + 7) / 8 <= 4096;
+}
+
+template <int SZ, int ACT, bool XL>
 static hipError_t launch_i1(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
     const size_t lds = (size_t)I1_W * a.wave_bytes;
     static std::atomic<uint64_t> done{0};
@@ -313,20 +363,27 @@ static hipError_t launch_i1(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)i4_gemv1_kernel<SZ, ACT>,
+        e = hipFuncSetAttribute((const void *)i4_gemv1_kernel<SZ, ACT, XL>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL((i4_gemv1_kernel<SZ, ACT>), dim3(ntiles, a.S), dim3(I1_W * 64), lds, s, a);
+    const int gx = XL ? (ntiles + 7) / 8 * 8 : ntiles;
+    hipLaunchKernelGGL((i4_gemv1_kernel<SZ, ACT, XL>), dim3(gx, a.S), dim3(I1_W * 64), lds, s, a);
     return hipGetLastError();
+}
+
+template <int SZ, int ACT>
+static hipError_t launch_i1_xl(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
+    if (use_xcd_local(ntiles, a.S)) return launch_i1<SZ, ACT, true>(a, ntiles, s);
+    return launch_i1<SZ, ACT, false>(a, ntiles, s);
 }
 
 template <int SZ>
 static hipError_t launch_i1_act(const I4Gemv1Args &a, int ntiles, int act, hipStream_t s) {
-    if (act == ACT_SILU) return launch_i1<SZ, ACT_SILU>(a, ntiles, s);
-    if (act == ACT_GELU) return launch_i1<SZ, ACT_GELU>(a, ntiles, s);
-    return launch_i1<SZ, ACT_NONE>(a, ntiles, s);
+    if (act == ACT_SILU) return launch_i1_xl<SZ, ACT_SILU>(a, ntiles, s);
+    if (act == ACT_GELU) return launch_i1_xl<SZ, ACT_GELU>(a, ntiles, s);
+    return launch_i1_xl<SZ, ACT_NONE>(a, ntiles, s);
 }
 
 hipError_t launch_i4_gemv1(const _Float16 *X, const uint8_t *P, const void *scales, const void *zeros,

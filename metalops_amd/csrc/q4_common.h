@@ -58,6 +58,35 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
 }
 
+// XCD-local split-K exchange.  gfx950 dispatches workgroup i of a grid to XCD
+// (i + c) mod 8, c fixed per device, so workgroups whose linear ids agree mod 8
+// share an XCD and its L2.  Partials exchanged among them can stay in that L2:
+// plain stores (L1 is write-through), then L1-bypassing loads, instead of
+// write-through stores and loads that go to memory.  The arrival ticket stays
+// a device-coherent atomic, and each arrival also adds 1 to its XCD's 5-bit
+// field (bits 8 + 5x), so the last arrival can check that every split ran on
+// its own XCD.
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+    return x & 7;
+}
+__device__ __forceinline__ uint64_t xcd_ticket_inc(uint32_t xcc) {
+    return 1ull + (1ull << (8 + 5 * xcc));
+}
+// True when all `S` arrivals counted in `total` (ticket value after the last
+// one) came from XCD `xcc`.
+__device__ __forceinline__ bool xcd_ticket_local(uint64_t total, uint32_t xcc, int S) {
+    return ((total >> (8 + 5 * xcc)) & 31) == (uint64_t)S;
+}
+// fp32 load at byte offset `off` from the workgroup-uniform `base`, bypassing
+// L1 (sc0) so it is served by the XCD's L2.
+__device__ __forceinline__ float load_l2_f32(const float *base, int off) {
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0x7fffffff, 0x00020000);
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 1));
+}
+
 // Workgroup barrier that waits only for this wave's LDS traffic.  (__syncthreads
 // also waits for all outstanding vector-memory operations, which would drain the
 // async copies that are meant to stay in flight across the barrier; the explicit

@@ -362,7 +362,7 @@ def test_gemv1_paths(mo, dev, monkeypatch, K, N, gs, spw, sz):
     split and unsplit plans, ragged step ranges, group sizes 32..512, N not a
     multiple of 128 (register ring only), all scale dtypes."""
     print(f"gemv1 K={K} N={N} gs={gs} spw={spw} sz={sz}", flush=True)
-    for k in ("MCQ4_I4_SPW1", "MCQ4_I4_GEMV1", "MCQ4_I4_PATH"):
+    for k in ("MCQ4_I4_SPW1", "MCQ4_I4_GEMV1", "MCQ4_I4_PATH", "MCQ4_XCD_LOCAL"):
         monkeypatch.delenv(k, raising=False)
     if spw is not None:
         monkeypatch.setenv("MCQ4_I4_SPW1", str(spw))
@@ -370,7 +370,13 @@ def test_gemv1_paths(mo, dev, monkeypatch, K, N, gs, spw, sz):
     X = torch.randn(1, K, generator=torch.Generator().manual_seed(K)).half().to(dev)
     Yref = _ref(X, packed, s, z, gs)
     for rep in range(2):                       # split-K counters are left at zero
-        _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
+        Y = mo.matmul_int4(X, packed, s, z, gs)
+        _check_rows(Y.float().cpu().numpy(), Yref)
+    # the agent-scope split exchange sums the same partials in the same order
+    monkeypatch.setenv("MCQ4_XCD_LOCAL", "0")
+    Y0 = mo.matmul_int4(X, packed, s, z, gs)
+    assert torch.equal(Y0.view(torch.int16), Y.view(torch.int16))
+    monkeypatch.delenv("MCQ4_XCD_LOCAL")
     # the register-ring GEMV
     monkeypatch.setenv("MCQ4_I4_GEMV1", "0")
     _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
