@@ -73,7 +73,8 @@ struct I4GemvArgs {
     int M, N, nsteps, spg;    // spg = steps per group (group_size / 32)
     int spw, S;               // steps per wave, splits (grid.y)
     float *part;              // [tiles][S][M][TC] when S > 1
-    uint32_t *counters;       // [tiles]
+    uint32_t *counters;       // [tiles]; with xl, 64-bit tickets [8][4096] by blockIdx.x mod 8
+    int xl;                   // XCD-local split exchange (grid.x a multiple of 8)
 };
 
 // Scales and zeros of the lane's NC columns (fp32 slot layout: TC scales then
@@ -147,6 +148,7 @@ i4_gemv_kernel(I4GemvArgs a) {
     const int sp = (int)blockIdx.y;
     const int N = a.N;
     const int col0 = t * TC;
+    if (a.xl && col0 >= N) return;                       // grid padding to a multiple of 8
 
     const int s_begin = (sp * IW + wave) * a.spw;
     const int ns = max(0, min(a.spw, a.nsteps - s_begin));
@@ -338,6 +340,49 @@ i4_gemv_kernel(I4GemvArgs a) {
         }
         return;
     }
+    if (a.xl) {
+        // Every split of this tile runs on this XCD: the partials go through its
+        // L2 (plain stores, L1-bypassing loads); the ticket checks the placement.
+        uint64_t *cnt = (uint64_t *)a.counters + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
+        const uint32_t xcc = xcc_id();
+        for (int v = tid; v < M * TC; v += IW * 64) {
+            const int row = v / TC, cl = v % TC;
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < IW; ++w) sum += red[(w * 16 + row) * TC + cl];
+            part[v] = sum;
+        }
+        wait_vmcnt<0>();
+        __syncthreads();
+        uint32_t *last_flag = (uint32_t *)smem;
+        if (tid == 0) {
+            const uint64_t inc = xcd_ticket_inc(xcc);
+            const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u
+                         : xcd_ticket_local(prev + inc, xcc, a.S) ? 1u : 2u;
+        }
+        __syncthreads();
+        const uint32_t lf = *last_flag;
+        if (!lf) return;
+        const float *base = a.part + (int64_t)t * a.S * M * TC;
+        for (int v = tid; v < M * TC; v += IW * 64) {
+            const int row = v / TC, cl = v % TC;
+            float sum = 0.f;
+            for (int q0 = 0; q0 < a.S; q0 += 8) {
+                float pv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pv[i] = load_l2_f32(base, (min(q0 + i, a.S - 1) * M * TC + v) * 4);
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if (q0 + i < a.S) sum += pv[i];
+            }
+            if (col0 + cl < N)
+                a.Y[(int64_t)row * a.ldy + col0 + cl] =
+                    lf == 1 ? (_Float16)activate<ACT>(sum) : (_Float16)__builtin_nanf("");
+        }
+        if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
     for (int v = tid; v < M * TC; v += IW * 64) {
         const int row = v / TC, cl = v % TC;
         float sum = 0.f;
@@ -489,7 +534,7 @@ static hipError_t launch_one(const I4GemvArgs &a, dim3 grid, hipStream_t s) {
 
 template <int SZ, int D, int NC, int WB, int IW>
 static hipError_t launch_gemv_sz(const I4GemvArgs &a, int ntiles, int act, hipStream_t s) {
-    const dim3 grid(ntiles, a.S);
+    const dim3 grid(a.xl ? (ntiles + 7) / 8 * 8 : ntiles, a.S);
     hipError_t e;
     if (act == ACT_SILU) e = launch_one<SZ, ACT_SILU, D, NC, WB, IW>(a, grid, s);
     else if (act == ACT_GELU) e = launch_one<SZ, ACT_GELU, D, NC, WB, IW>(a, grid, s);
@@ -526,13 +571,16 @@ hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, cons
     a.M = M; a.N = N; a.nsteps = K / ks; a.spg = gs / ks;
     a.spw = c.spw; a.S = c.S;
     a.part = nullptr; a.counters = nullptr;
+    const int ntiles = (N + 16 * c.nc - 1) / (16 * c.nc);
+    a.xl = 0;
     if (c.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.part = (float *)((char *)ws + COUNTER_BYTES);
         const char *red = getenv("MCQ4_I4_RED");                   // experiments
         if (!(red && red[0] == 'k')) a.counters = (uint32_t *)ws;
+        const char *xl = getenv("MCQ4_XCD_LOCAL");
+        a.xl = a.counters && !(xl && xl[0] == '0') && (ntiles + 7) / 8 <= 4096;
     }
-    const int ntiles = (N + 16 * c.nc - 1) / (16 * c.nc);
     if (wb == 8) {
         if (c.nc == 8) return launch_gemv_nc<8, 8, 4>(a, ntiles, sz_dt, act, s);
         return launch_gemv_nc<4, 8, 16>(a, ntiles, sz_dt, act, s);

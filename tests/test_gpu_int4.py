@@ -214,6 +214,35 @@ def test_split_k_repeat_and_interleave(mo, dev):
             _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
 
 
+@pytest.mark.parametrize("wb,M,K,N,gs", [(4, 1, 4096, 4096, 128), (4, 4, 4096, 1040, 64), (4, 16, 14336, 512, 128),
+                                         (4, 9, 2048, 4112, 32), (8, 1, 4096, 4096, 128), (8, 8, 11008, 200, 128)])
+def test_xcd_local_exchange(mo, dev, monkeypatch, wb, M, K, N, gs):
+    """The split-K GEMV's XCD-local exchange (default) and the agent-scope one sum
+    the same partials in the same order: identical bits, and both match the oracle.
+    Tile counts that are not a multiple of 8 exercise the padded grid."""
+    print(f"xcd-local wb={wb} M={M} K={K} N={N} gs={gs}", flush=True)
+    for k in ("MCQ4_I4_SPW1", "MCQ4_I4_PATH", "MCQ4_XCD_LOCAL"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("MCQ4_I4_GEMV1", "0")         # the register-ring GEMV for M == 1 too
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(K + M)).half()
+    if wb == 4:
+        w, packed, s, z = _quant(mo, dev, K, N, gs, seed=K + N)
+        fn = lambda: mo.matmul_int4(X.to(dev), packed, s, z, gs)
+        Yref = _ref(X.to(dev), packed, s, z, gs)
+    else:
+        q, s8, z8 = _int8_weights(K, N, gs, R.F16, K + N)
+        args = [torch.from_numpy(a).to(dev) for a in (q, s8.astype(np.float16), z8.astype(np.float16))]
+        fn = lambda: mo.matmul_int8(X.to(dev), *args, gs)
+        Yref = R.matmul_int8_f32(X.float().numpy(), q, s8, z8, gs)
+    Y = fn()
+    Y2 = fn()
+    monkeypatch.setenv("MCQ4_XCD_LOCAL", "0")
+    Y0 = fn()
+    _check_rows(Y.float().cpu().numpy(), Yref)
+    assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
+    assert torch.equal(Y.view(torch.int16), Y0.view(torch.int16))
+
+
 def _silu(y):
     return y / (1.0 + np.exp(-y))
 
