@@ -19,6 +19,10 @@ struct Gemm4Args {
     int tiles_m, tiles_n;
     int S;               // K splits (grid.z)
     float *partials;     // [tiles][S][BM*256] when S > 1
+    // S == 2 with an XCD-local exchange: grid.x padded to a multiple of 8, the
+    // second split of a tile to finish adds the first's partial and stores Y
+    // (64-bit tickets [8][4096] by blockIdx.x mod 8 at the workspace start).
+    uint64_t *tickets = nullptr;
 };
 
 // Row-tile height and number of K splits of a prefill shape.

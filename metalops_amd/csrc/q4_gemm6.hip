@@ -17,7 +17,9 @@
 //     value) one step ahead, in 12 chunks spread over the step's 16 MFMAs.
 //   * Barrier between the two steps of a stage; stage s+3's copies go out
 //     during the second step, one per two MFMAs.  Plan, split-K partials and
-//     the reduction kernel are q4_gemm5's.
+//     the reduction kernel are q4_gemm5's, except that with two K splits the
+//     second workgroup of a tile to finish adds the first's partial itself,
+//     read from their shared XCD's L2 (see xcd_ticket_inc), and stores Y.
 //
 // MFMA 32x32 output layout: lane l holds D[8*(r/4) + 4*(l/32) + r%4][l%32], r = 0..15.
 #include <algorithm>
@@ -62,9 +64,10 @@ q4_gemm6_kernel(Gemm4Args a) {
     const int wm = wave >> 2, wn = wave & 3;
 
     const int ntiles = a.tiles_m * a.tiles_n;
-    const int bid = blockIdx.x;
+    const int bid = blockIdx.x, gx = gridDim.x;
     int tile_id = bid;
-    if (ntiles % 8 == 0) tile_id = (bid % 8) * (ntiles / 8) + bid / 8;
+    if (gx % 8 == 0) tile_id = (bid % 8) * (gx / 8) + bid / 8;
+    if (tile_id >= ntiles) return;                // grid padding (XCD-local exchange)
     const int tm = tile_id % a.tiles_m;
     const int tn = tile_id / a.tiles_m;
     const int m0 = tm * BM, n0 = tn * G4_BN;
@@ -277,6 +280,43 @@ q4_gemm6_kernel(Gemm4Args a) {
                 part[ml * G4_BN + nl] = acc[i][j][r];
             }
         }
+    if (!a.tickets) return;                       // the reduce kernel sums
+    // Both splits of this tile run on this XCD (same blockIdx.x, grid.x a
+    // multiple of 8): the partials stay in its L2.  The second to arrive adds
+    // the other's partial (p0 + p1 either way: fp32 addition commutes).
+    wait_vmcnt<0>();
+    __syncthreads();
+    uint64_t *cnt = a.tickets + (bid & 7) * 4096 + (bid >> 3);
+    const uint32_t xcc = xcc_id();
+    uint32_t *last_flag = (uint32_t *)smem;
+    if (tid == 0) {
+        const uint64_t inc = xcd_ticket_inc(xcc);
+        const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last_flag = (prev & 0xFF) != 1 ? 0u : xcd_ticket_local(prev + inc, xcc, 2) ? 1u : 2u;
+    }
+    __syncthreads();
+    const uint32_t lf = *last_flag;
+    if (!lf) return;
+    const float *other = a.partials + ((int64_t)tile_id * 2 + (1 - z)) * (BM * G4_BN);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int nl = wn * WN + j * 32 + lrow;
+            float o[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int ml = wm * WM + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
+                o[r] = load_l2_f32(other, (ml * G4_BN + nl) * 4);
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + rsub + (r & 3), n = n0 + nl;
+                const float v = lf == 1 ? acc[i][j][r] + o[r] : __builtin_nanf("");
+                if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (_Float16)v;
+            }
+        }
+    if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Plan of the 4-wave form (two workgroups per CU): 128-row tiles, K split
@@ -321,8 +361,10 @@ static hipError_t launch_g6(Gemm4Args &a, hipStream_t s) {
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL((q4_gemm6_kernel<WGM>), dim3(a.tiles_m * a.tiles_n, 1, a.S), dim3(256 * WGM), lds, s, a);
-    if (a.S > 1) return launch_gemm4_reduce(a, 128 * WGM, s);
+    const int ntiles = a.tiles_m * a.tiles_n;
+    const int gx = a.tickets ? (ntiles + 7) / 8 * 8 : ntiles;
+    hipLaunchKernelGGL((q4_gemm6_kernel<WGM>), dim3(gx, 1, a.S), dim3(256 * WGM), lds, s, a);
+    if (a.S > 1 && !a.tickets) return launch_gemm4_reduce(a, 128 * WGM, s);
     return hipGetLastError();
 }
 
@@ -347,6 +389,11 @@ hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
     if (c.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.partials = (float *)((char *)ws + COUNTER_BYTES);
+        // Two splits: summed in the kernel through the XCD's L2 (MCQ4_XCD_LOCAL=0:
+        // by the reduce kernel).
+        const char *xl = getenv("MCQ4_XCD_LOCAL");
+        if (c.S == 2 && !(xl && xl[0] == '0') && (a.tiles_m * a.tiles_n + 7) / 8 <= 4096)
+            a.tickets = (uint64_t *)ws;
     }
     return wgm == 2 ? launch_g6<2>(a, s) : launch_g6<1>(a, s);
 }

@@ -211,6 +211,9 @@ PATHS = {
     "gemm6_split3": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "3"},
     "gemm6_wgm1": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_WGM": "1"},
     "gemm6_wgm1_split3": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_WGM": "1", "MCQ4_GEMM4_SPLIT": "3"},
+    "gemm6_split2": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "2"},
+    "gemm6_split2_reduce": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "2", "MCQ4_XCD_LOCAL": "0"},
+    "gemm6_wgm2_split2": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_WGM": "2", "MCQ4_GEMM4_SPLIT": "2"},
 }
 PATH_SHAPES = {
     "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
@@ -254,6 +257,9 @@ PATH_SHAPES = {
     "gemm6_wgm1": [(129, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
                    (200, 32, 256), (130, 64, 384), (513, 96, 256), (2048, 11008, 512)],
     "gemm6_wgm1_split3": [(200, 352, 384), (300, 4096, 640)],
+    "gemm6_split2": [(200, 352, 384), (300, 4096, 640), (512, 4096, 1024), (129, 1024, 2304)],
+    "gemm6_split2_reduce": [(300, 4096, 640), (129, 1024, 2304)],
+    "gemm6_wgm2_split2": [(300, 4096, 640), (513, 1024, 2304)],
 }
 
 
@@ -261,7 +267,8 @@ PATH_SHAPES = {
 def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM", "MCQ4_GEMV_PATH",
               "MCQ4_GEMV_RING", "MCQ4_GEMVM_WAVES", "MCQ4_GEMM4_SPLIT", "MCQ4_GEMM4_WGM",
-              "MCQ4_GEMV_WAVES", "MCQ4_GEMM6_WGM", "MCQ4_GEMM5_SCHED", "MCQ4_GEMVM_SPLIT"):
+              "MCQ4_GEMV_WAVES", "MCQ4_GEMM6_WGM", "MCQ4_GEMM5_SCHED", "MCQ4_GEMVM_SPLIT",
+              "MCQ4_XCD_LOCAL"):
         monkeypatch.delenv(k, raising=False)
     for k, v in PATHS[path].items():
         monkeypatch.setenv(k, v)
@@ -271,3 +278,26 @@ def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     blocks = ref.quantize_llama_rule(W.numpy())
     Y = mo.matmul_ggml_q4_0(X.to(dev), torch.from_numpy(blocks).to(dev))
     _check_rows(Y.float().cpu().numpy(), ref.matmul_f32(X.numpy(), blocks))
+
+
+@pytest.mark.parametrize("M,K,N", [(2048, 14336, 4096), (300, 4096, 640), (1000, 2048, 1280)])
+def test_gemm6_split2_exchange_matches_reduce(dev, monkeypatch, M, K, N):
+    """Two K splits: the in-kernel XCD-local sum (default) and the reduction
+    kernel both compute p0 + p1, so the outputs are identical bits."""
+    print(f"gemm6 split2 exchange M={M} K={K} N={N}", flush=True)
+    for k in ("MCQ4_GEMM_PATH", "MCQ4_GEMM6_WGM", "MCQ4_XCD_LOCAL"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("MCQ4_GEMM4_SPLIT", "2")
+    mo = _mo()
+    g = torch.Generator().manual_seed(M + K)
+    blocks = torch.randint(0, 256, (K // 32, N, 18), generator=g, dtype=torch.uint8)
+    blocks[:, :, 0:2] = torch.tensor([0x1f, 0x21], dtype=torch.uint8)   # d = 0.0101 (fp16 0x211f)
+    blocks = blocks.to(dev)
+    X = torch.randn(M, K, generator=g).half().to(dev)
+    Y = mo.matmul_ggml_q4_0(X, blocks)
+    Y2 = mo.matmul_ggml_q4_0(X, blocks)
+    monkeypatch.setenv("MCQ4_XCD_LOCAL", "0")
+    Y0 = mo.matmul_ggml_q4_0(X, blocks)
+    assert torch.isfinite(Y.float()).all()
+    assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
+    assert torch.equal(Y.view(torch.int16), Y0.view(torch.int16))
