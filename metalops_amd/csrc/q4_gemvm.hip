@@ -41,6 +41,10 @@ struct GemvMArgs {
     int M, nb, N, ntiles, nbt;
     int S, bps;          // K splits (grid.y) and batches per split
     float *part;         // [S][M][16 * ntiles] fp32 partials when S > 1 (after the counter area)
+    // S > 1 with the XCD-local exchange: grid.x padded to a multiple of 8 and the
+    // last split of each workgroup sums the partials (64-bit tickets [8][4096]
+    // by blockIdx.x mod 8 at the workspace start); null: the reduction kernel.
+    uint64_t *tickets;
 };
 
 template <int WAVES, int TPW>
@@ -61,6 +65,7 @@ q4_gemvm_kernel(GemvMArgs a) {
     int wg = (int)blockIdx.x;
     if (wg < G8) wg = (wg & 7) * (G8 >> 3) + (wg >> 3);
     const int ntl = min(TPW, (a.ntiles - wg + G - 1) / G);
+    if (ntl <= 0) return;                         // grid padding (XCD-local exchange)
     // This split's batches [b0, b0 + nbs); wave w owns b0 + w, b0 + w + WAVES, ...
     const int sp = (int)blockIdx.y;
     const int b0 = sp * a.bps;
@@ -199,6 +204,43 @@ q4_gemvm_kernel(GemvMArgs a) {
         if (a.S == 1) a.Y[(int64_t)rr * a.ldy + n] = (_Float16)s;
         else a.part[((int64_t)sp * a.M + rr) * (16 * a.ntiles) + n] = s;
     }
+    if (a.S == 1 || !a.tickets) return;
+    // Every split of this workgroup runs on this XCD (same blockIdx.x, grid.x a
+    // multiple of 8): the last to arrive sums the partials, in split order as the
+    // reduction kernel does, from the XCD's L2.
+    wait_vmcnt<0>();
+    __syncthreads();
+    uint64_t *cnt = a.tickets + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
+    const uint32_t xcc = xcc_id();
+    uint32_t *last_flag = (uint32_t *)smem;       // the ring is idle from here
+    if (tid == 0) {
+        const uint64_t inc = xcd_ticket_inc(xcc);
+        const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u : xcd_ticket_local(prev + inc, xcc, a.S) ? 1u : 2u;
+    }
+    __syncthreads();
+    const uint32_t lf = *last_flag;
+    if (!lf) return;
+    const int64_t pstride = (int64_t)a.M * 16 * a.ntiles;         // floats per split
+    for (int v = tid; v < ntl * 256; v += WAVES * 64) {
+        const int j = v >> 8, rr = (v >> 4) & 15, col = v & 15;
+        if (rr >= a.M) continue;
+        float own = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) own += red[((j * WAVES + w) * 16 + rr) * 16 + col];
+        const int n = (wg + j * G) * 16 + col;
+        const float *base = a.part + (int64_t)rr * (16 * a.ntiles) + n;
+        float pv[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            pv[q] = q < a.S && q != sp ? load_l2_f32(a.part, (int)(((int64_t)q * pstride + (base - a.part)) * 4)) : own;
+        float t = 0.f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            if (q < a.S) t += pv[q];
+        a.Y[(int64_t)rr * a.ldy + n] = lf == 1 ? (_Float16)t : (_Float16)__builtin_nanf("");
+    }
+    if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Sums the S fp32 partials of every output in split order (deterministic) and
@@ -231,8 +273,9 @@ static hipError_t launch_gemvm_t(const GemvMArgs &a, int grid, hipStream_t s) {
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL((q4_gemvm_kernel<WAVES, TPW>), dim3(grid, a.S), dim3(WAVES * 64), lds, s, a);
-    if (a.S > 1) {
+    const int gx = a.tickets ? (grid + 7) / 8 * 8 : grid;
+    hipLaunchKernelGGL((q4_gemvm_kernel<WAVES, TPW>), dim3(gx, a.S), dim3(WAVES * 64), lds, s, a);
+    if (a.S > 1 && !a.tickets) {
         const int64_t n = (int64_t)a.M * 16 * a.ntiles;
         hipLaunchKernelGGL(q4_gemvm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
     }
@@ -265,10 +308,11 @@ bool gemvm_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M
 // activation block (M x K halves) from L2, and at M >= 8 those loads -- one
 // line per row per instruction -- outnumber the weight copies.  Two tiles per
 // workgroup over half of K each keeps 256 workgroups and halves the activation
-// traffic; the fp32 partials are summed in split order by a second kernel
-// (M=16 K=14336 N=4096: 15.6 us, was 18.7; M=8: 13.4, was 14.3; at M <= 4 and
-// with several tiles per workgroup it does not pay).  MCQ4_GEMVM_SPLIT=1|2|4|8
-// overrides.
+// traffic; the fp32 partials are summed in split order by the last split of each
+// workgroup (XCD-local exchange) or, with MCQ4_XCD_LOCAL=0, by a second kernel
+// (M=16 K=14336 N=4096: 15.6 us with the second kernel, was 18.7; M=8: 13.4,
+// was 14.3; at M <= 4 and with several tiles per workgroup it does not pay).
+// MCQ4_GEMVM_SPLIT=1|2|4|8 overrides.
 struct GmPlan {
     int waves, tpw, grid, S, bps;
 };
@@ -307,9 +351,12 @@ hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
     const GmPlan p = gemvm_plan(M, K, N);
     a.S = p.S; a.bps = p.bps;
     a.part = nullptr;
+    a.tickets = nullptr;
     if (p.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.part = (float *)((char *)ws + COUNTER_BYTES);
+        const char *xl = getenv("MCQ4_XCD_LOCAL");
+        if (!(xl && xl[0] == '0') && p.S <= 8) a.tickets = (uint64_t *)ws;
     }
     if (p.waves == 16) return launch_gemvm_w<16>(a, p.grid, p.tpw, s);
     return launch_gemvm_w<8>(a, p.grid, p.tpw, s);

@@ -189,6 +189,8 @@ PATHS = {
     "gemvm_w8": {"MCQ4_GEMVM_WAVES": "8"},
     "gemvm_split2": {"MCQ4_GEMVM_SPLIT": "2"},
     "gemvm_split8": {"MCQ4_GEMVM_SPLIT": "8"},
+    "gemvm_split4": {"MCQ4_GEMVM_SPLIT": "4"},
+    "gemvm_split2_reduce": {"MCQ4_GEMVM_SPLIT": "2", "MCQ4_XCD_LOCAL": "0"},
     "decode_lds": {},
     "decode_lds_small_m": {"MCQ4_GEMV_PATH": "off"},
     "decode_direct": {"MCQ4_DECODE_PATH": "direct"},
@@ -229,6 +231,8 @@ PATH_SHAPES = {
     "gemvm_w8": [(2, 352, 264), (7, 4096, 1040), (16, 11008, 512)],
     "gemvm_split2": [(2, 352, 264), (9, 4096, 1040), (16, 14336, 4096), (5, 11008, 512)],
     "gemvm_split8": [(16, 2048, 1032), (3, 14336, 512), (12, 512, 200)],
+    "gemvm_split4": [(16, 4096, 1040), (6, 11008, 264), (13, 352, 8200)],
+    "gemvm_split2_reduce": [(9, 4096, 1040), (16, 14336, 4096)],
     "decode_lds": [(1, 352, 264), (40, 2048, 96), (64, 256, 64), (17, 1024, 520), (33, 4096, 1032)],
     "decode_lds_small_m": [(3, 1024, 520), (16, 4096, 1032)],
     "decode_direct": [(1, 352, 257), (7, 1024, 520), (16, 4096, 1000), (64, 512, 72)],
@@ -280,14 +284,22 @@ def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     _check_rows(Y.float().cpu().numpy(), ref.matmul_f32(X.numpy(), blocks))
 
 
-@pytest.mark.parametrize("M,K,N", [(2048, 14336, 4096), (300, 4096, 640), (1000, 2048, 1280)])
-def test_gemm6_split2_exchange_matches_reduce(dev, monkeypatch, M, K, N):
-    """Two K splits: the in-kernel XCD-local sum (default) and the reduction
-    kernel both compute p0 + p1, so the outputs are identical bits."""
-    print(f"gemm6 split2 exchange M={M} K={K} N={N}", flush=True)
-    for k in ("MCQ4_GEMM_PATH", "MCQ4_GEMM6_WGM", "MCQ4_XCD_LOCAL"):
+@pytest.mark.parametrize("M,K,N,split", [(2048, 14336, 4096, "gemm2"), (300, 4096, 640, "gemm2"),
+                                         (1000, 2048, 1280, "gemm2"), (16, 14336, 4096, "gemvm2"),
+                                         (9, 4096, 1040, "gemvm2"), (12, 11008, 8200, "gemvm4"),
+                                         (16, 2048, 1032, "gemvm8")])
+def test_split_exchange_matches_reduce(dev, monkeypatch, M, K, N, split):
+    """K split over workgroups: the in-kernel XCD-local sum (default) and the
+    reduction kernel add the same partials in the same order (two splits of the
+    GEMM: p0 + p1, which commutes), so the outputs are identical bits."""
+    print(f"split exchange {split} M={M} K={K} N={N}", flush=True)
+    for k in ("MCQ4_GEMM_PATH", "MCQ4_GEMM6_WGM", "MCQ4_XCD_LOCAL", "MCQ4_GEMM4_SPLIT", "MCQ4_GEMVM_SPLIT",
+              "MCQ4_GEMV_PATH", "MCQ4_GEMVM_WAVES"):
         monkeypatch.delenv(k, raising=False)
-    monkeypatch.setenv("MCQ4_GEMM4_SPLIT", "2")
+    if split.startswith("gemm"):
+        monkeypatch.setenv("MCQ4_GEMM4_SPLIT", split[-1])
+    else:
+        monkeypatch.setenv("MCQ4_GEMVM_SPLIT", split[-1])
     mo = _mo()
     g = torch.Generator().manual_seed(M + K)
     blocks = torch.randint(0, 256, (K // 32, N, 18), generator=g, dtype=torch.uint8)
