@@ -41,7 +41,7 @@ FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
 # for a plain 256 MiB device copy (FETCH_SIZE x 2, WRITE_SIZE x 1).  Figures and
 # commands: profiles/gemv_dma_llama7b_m1.md, profiles/gemm6_llama7b_m2048.md.
 DECODE_TRAFFIC_BYTES = 22995538       # average over the five projections
-PREFILL_UP_TRAFFIC_BYTES = 596460441  # 537.5 MB read + 59.0 MB written
+PREFILL_UP_TRAFFIC_BYTES = 597541990  # 538.6 MB read + 58.9 MB written
 
 DECODE_LAYER = [  # (name, K, N) -- Llama-2-7B projections, configs[1]
     ("qkv", 4096, 12288),
