@@ -21,6 +21,11 @@ struct I4GemmArgs {
     int tiles_m, tiles_n;
     int S;               // K splits (grid.z)
     float *partials;     // [tiles][S][BM*256] when S > 1
+    // i4_gemm6 with S == 2 and an XCD-local exchange: grid.x padded to a multiple
+    // of 8, the second split of a tile to finish adds the first's partial and
+    // stores act(sum) (64-bit tickets [8][4096] by blockIdx.x mod 8 at the
+    // workspace start); null: i4_gemm_reduce_kernel.
+    uint64_t *tickets = nullptr;
 };
 
 // Sums the S partial tiles per output tile in split order and stores act(sum) as fp16.

@@ -21,7 +21,9 @@
 //     (the formula of i4_gemm).  The next step's operands are built in chunks
 //     between this step's MFMAs.
 //   * Barrier between the two steps of a stage; stage s+3's copies go out
-//     during the second step, one per two MFMAs.  Split-K partials and their
+//     during the second step, one per two MFMAs.  With two K splits the second
+//     workgroup of a tile to finish sums both partials (XCD-local exchange, see
+//     xcd_ticket_inc).  Otherwise split-K partials and their
 //     reduction (with the fused activation) are i4_gemm's.
 //
 // MFMA 32x32 output layout: lane l holds D[8*(r/4) + 4*(l/32) + r%4][l%32], r = 0..15.
@@ -63,9 +65,10 @@ i4_gemm6_kernel(I4GemmArgs a) {
     const int wn = wave;
 
     const int ntiles = a.tiles_m * a.tiles_n;
-    const int bid = blockIdx.x;
+    const int bid = blockIdx.x, gx = gridDim.x;
     int tile_id = bid;
-    if (ntiles % 8 == 0) tile_id = (bid % 8) * (ntiles / 8) + bid / 8;
+    if (gx % 8 == 0) tile_id = (bid % 8) * (gx / 8) + bid / 8;
+    if (tile_id >= ntiles) return;                // grid padding (XCD-local exchange)
     const int tm = tile_id % a.tiles_m;
     const int tn = tile_id / a.tiles_m;
     const int m0 = tm * BM, n0 = tn * I4G_BN;
@@ -286,6 +289,48 @@ i4_gemm6_kernel(I4GemmArgs a) {
             v.y = acc[i][1][r];
             *(float2 *)(part + ml * I4G_BN + nl) = v;
         }
+    if (!a.tickets) return;                       // the reduction kernel sums
+    // Both splits of this tile run on this XCD (same blockIdx.x, grid.x a
+    // multiple of 8): the second to arrive adds the other's partial from the
+    // XCD's L2 (p0 + p1 either way: fp32 addition commutes).
+    wait_vmcnt<0>();
+    __syncthreads();
+    uint64_t *cnt = a.tickets + (bid & 7) * 4096 + (bid >> 3);
+    const uint32_t xcc = xcc_id();
+    uint32_t *last_flag = (uint32_t *)smem;
+    if (tid == 0) {
+        const uint64_t inc = xcd_ticket_inc(xcc);
+        const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last_flag = (prev & 0xFF) != 1 ? 0u : xcd_ticket_local(prev + inc, xcc, 2) ? 1u : 2u;
+    }
+    __syncthreads();
+    const uint32_t lf = *last_flag;
+    if (!lf) return;
+    const float *other = a.partials + ((int64_t)tile_id * 2 + (1 - z)) * (BM * I4G_BN);
+    _Float16 *Y = (_Float16 *)a.Y;
+    const int n = wcol0 + 2 * lrow;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+        float o[16][2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int ml = i * 32 + 8 * (r >> 2) + rsub + (r & 3);
+            o[r][0] = load_l2_f32(other, (ml * I4G_BN + nl) * 4);
+            o[r][1] = load_l2_f32(other, (ml * I4G_BN + nl + 1) * 4);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int m = m0 + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
+            if (m < a.M && n < N) {
+                half2_t v;
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    v[j] = lf == 1 ? (_Float16)activate<ACT>(acc[i][j][r] + o[r][j]) : (_Float16)__builtin_nanf("");
+                *(half2_t *)(Y + (int64_t)m * a.ldy + n) = v;
+            }
+        }
+    }
+    if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Plan: 128-row tiles, K split (powers of two, at least 16 steps per split)
@@ -332,8 +377,10 @@ static hipError_t launch_j6(const I4GemmArgs &a, hipStream_t s) {
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL((i4_gemm6_kernel<SZ, ACT>), dim3(a.tiles_m * a.tiles_n, 1, a.S), dim3(256), J6_LDS, s, a);
-    if (a.S > 1) return launch_i4_gemm_reduce(a, J6_BM, ACT, s);
+    const int ntiles = a.tiles_m * a.tiles_n;
+    const int gx = a.tickets ? (ntiles + 7) / 8 * 8 : ntiles;
+    hipLaunchKernelGGL((i4_gemm6_kernel<SZ, ACT>), dim3(gx, 1, a.S), dim3(256), J6_LDS, s, a);
+    if (a.S > 1 && !a.tickets) return launch_i4_gemm_reduce(a, J6_BM, ACT, s);
     return hipGetLastError();
 }
 
@@ -358,6 +405,11 @@ hipError_t launch_i4_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *P, con
     if (c.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.partials = (float *)((char *)ws + COUNTER_BYTES);
+        // Two splits: summed in the kernel through the XCD's L2 (MCQ4_XCD_LOCAL=0:
+        // by the reduction kernel).
+        const char *xl = getenv("MCQ4_XCD_LOCAL");
+        if (c.S == 2 && !(xl && xl[0] == '0') && (a.tiles_m * a.tiles_n + 7) / 8 <= 4096)
+            a.tickets = (uint64_t *)ws;
     }
     if (sz_dt == DT_F16) return launch_j6_act<DT_F16>(a, act, s);
     return launch_j6_act<DT_BF16>(a, act, s);

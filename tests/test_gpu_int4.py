@@ -243,6 +243,32 @@ def test_xcd_local_exchange(mo, dev, monkeypatch, wb, M, K, N, gs):
     assert torch.equal(Y.view(torch.int16), Y0.view(torch.int16))
 
 
+@pytest.mark.parametrize("M,K,N,act", [(2048, 14336, 4096, None), (1300, 2048, 5120, None),
+                                       (1024, 2048, 6144, "silu")])
+def test_gemm6_split2_exchange_matches_reduce(mo, dev, monkeypatch, M, K, N, act):
+    """i4_gemm6 with two K splits: the in-kernel XCD-local sum (default) and the
+    reduction kernel both compute act(p0 + p1): identical bits, and the oracle agrees."""
+    print(f"i4_gemm6 split2 exchange M={M} K={K} N={N} act={act}", flush=True)
+    for k in ("MCQ4_I4_GEMM6", "MCQ4_I4_PATH", "MCQ4_XCD_LOCAL"):
+        monkeypatch.delenv(k, raising=False)
+    gs = 128
+    w, packed, s, z = _quant(mo, dev, K, N, gs, seed=M + N)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).half().to(dev)
+    fn = (lambda: mo.matmul_int4_silu(X, packed, s, z, gs)) if act else (lambda: mo.matmul_int4(X, packed, s, z, gs))
+    Y = fn()
+    Y2 = fn()
+    monkeypatch.setenv("MCQ4_XCD_LOCAL", "0")
+    Y0 = fn()
+    assert torch.isfinite(Y.float()).all()
+    assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
+    assert torch.equal(Y.view(torch.int16), Y0.view(torch.int16))
+    if M * K * N <= 2048 * 2048 * 6144:
+        base = _ref(X, packed, s, z, gs)
+        if act:
+            base = _silu(base.astype(np.float64))
+        _check_rows(Y.float().cpu().numpy(), base)
+
+
 def _silu(y):
     return y / (1.0 + np.exp(-y))
 
