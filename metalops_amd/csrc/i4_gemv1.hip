@@ -8,7 +8,8 @@
 // Work decomposition
 //   * Tile = 128 columns (whole 128-byte pieces of each byte row); step = 32 K
 //     (16 byte rows, 2 KiB of the tile).  Workgroup (tile, split sp) = 8 waves;
-//     wave w owns steps [(8 sp + w) spw, +spw).  Two workgroups share a CU.
+//     wave w owns steps [(8 sp + w) spw, +spw).  The plan aims at one workgroup
+//     per CU.
 //   * Per wave, oldest first: one copy per group of the group's scale and zero
 //     rows (128 columns each, one 1 KiB slot), one copy of the range's activations (up to 16
 //     steps), then the steps: two global_load_lds_dwordx4 each (byte rows 0..7
@@ -314,16 +315,24 @@ struct I1Cfg {
     int spw, S, ngr_max;
 };
 
-// Steps per wave: about 4096 waves in flight (16 per CU), 2..16 steps each;
-// MCQ4_I4_SPW1 overrides.  Then the split count and the scale/zero slots a
-// wave's range can touch.
+// Plan: one 8-wave workgroup per CU.  K splits S = the most that keep the
+// grid within 256 workgroups (at least 1, at most 16, and enough that a wave's
+// range fits its 16-step activation slot), then steps per wave from S.
+// Measured on the Llama-2-7B projections, graph replays: QKV 96 tiles x 2 splits
+// 9.6 us (the previous plan's 96 x 6 = 576 workgroups, two rounds of the 512
+// that fit two per CU: 10.6 us; 96 x 3: 12.1 us), gate/up 86 x 2 8.4 us (was
+// 9.8), down 32 x 8 8.6 us (was 32 x 15: 9.7), O 32 x 8 5.8 us (unchanged).
+// Deeper rings (6, 8 steps) were slower on every shape.  MCQ4_I4_SPW1 overrides
+// the steps per wave.
 static I1Cfg i4_gemv1_config(int64_t K, int64_t N, int64_t gs) {
     const int64_t nsteps = K / 32, spg = gs / 32, ntiles = N / I1_TC;
-    int64_t spw = (ntiles * nsteps + 4095) / 4096;
+    int64_t S = std::max<int64_t>(1, std::min<int64_t>(I1_SMAX, 256 / std::max<int64_t>(ntiles, 1)));
+    S = std::max(S, (nsteps + I1_W * 16 - 1) / (I1_W * 16));
+    int64_t spw = (nsteps + I1_W * S - 1) / (I1_W * S);
     if (const char *env = getenv("MCQ4_I4_SPW1")) spw = atoi(env);
     spw = std::max<int64_t>(spw, (nsteps + I1_W * I1_SMAX - 1) / (I1_W * I1_SMAX));
     spw = std::min<int64_t>(std::max<int64_t>(spw, 2), 16);
-    const int64_t S = (nsteps + I1_W * spw - 1) / (I1_W * spw);
+    S = (nsteps + I1_W * spw - 1) / (I1_W * spw);
     const int64_t ngr = spw % spg == 0 ? spw / spg : (spw + spg - 1) / spg + 1;
     return {(int)spw, (int)S, (int)ngr};
 }
