@@ -443,8 +443,12 @@ struct I4GemvCfg {
     int nc, iw, spw, S;
 };
 
-// Tile shape and K split.  Default: 128-column tiles of 4 waves, K split so
-// that about 1024 waves run (2..32 steps each, at most I4V_SMAX splits).  A
+// Tile shape and K split.  Default: 128-column tiles of 4 waves, one workgroup
+// per CU: S = the most K splits that keep the grid within 256 workgroups (2..32
+// steps per wave, at most I4V_SMAX splits).  Graph replays, us: INT4 M=16
+// 4096x14336 15.3 (the previous aim of about 1024 waves gave 336 workgroups:
+// 18.6), M=4 11.7 (13.7); INT8 M=16 4096x14336 21.2 (25.3); 14336x4096 and
+// 4096x4096 were already at 256 workgroups.  A
 // wave's steps must fit its I4V_GMAX scale/zero slots: a range of spw steps
 // touches at most ceil(spw/spg) + 1 groups, or exactly spw/spg when spw is a
 // multiple of spg (every range then starts on a group boundary).
@@ -468,7 +472,9 @@ static I4GemvCfg i4_gemv_config(int64_t K, int64_t N, int64_t gs, int ks) {
     const int64_t ntiles = (N + 16 * nc - 1) / (16 * nc);
     int64_t S;
     if (wide) {
-        int64_t spw = (ntiles * nsteps + 1023) / 1024;
+        S = std::max<int64_t>(1, std::min<int64_t>(I4V_SMAX, 256 / ntiles));
+        S = std::max(S, (nsteps + iw * 32 - 1) / (iw * 32));
+        int64_t spw = (nsteps + iw * S - 1) / (iw * S);
         if (const char *env = getenv("MCQ4_I4_SPW")) spw = atoi(env);
         spw = std::max<int64_t>(spw, (nsteps + iw * I4V_SMAX - 1) / (iw * I4V_SMAX));
         spw = fit(std::min<int64_t>(std::max<int64_t>(spw, 2), 32));
