@@ -216,6 +216,9 @@ PATHS = {
     "gemm6_split2": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "2"},
     "gemm6_split2_reduce": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "2", "MCQ4_XCD_LOCAL": "0"},
     "gemm6_wgm2_split2": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_WGM": "2", "MCQ4_GEMM4_SPLIT": "2"},
+    "gemm6_split4": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "4"},
+    "gemm6_split8": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "8"},
+    "gemm6_split16": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "16"},
 }
 PATH_SHAPES = {
     "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
@@ -264,6 +267,9 @@ PATH_SHAPES = {
     "gemm6_split2": [(200, 352, 384), (300, 4096, 640), (512, 4096, 1024), (129, 1024, 2304)],
     "gemm6_split2_reduce": [(300, 4096, 640), (129, 1024, 2304)],
     "gemm6_wgm2_split2": [(300, 4096, 640), (513, 1024, 2304)],
+    "gemm6_split4": [(200, 2048, 384), (300, 4096, 640), (512, 11008, 1024)],
+    "gemm6_split8": [(129, 4096, 256), (512, 11008, 512), (300, 8192, 768)],
+    "gemm6_split16": [(200, 16384, 256), (130, 8192, 384)],
 }
 
 
@@ -313,3 +319,4 @@ def test_split_exchange_matches_reduce(dev, monkeypatch, M, K, N, split):
     assert torch.isfinite(Y.float()).all()
     assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
     assert torch.equal(Y.view(torch.int16), Y0.view(torch.int16))
+
