@@ -319,14 +319,21 @@ q4_gemm6_kernel(Gemm4Args a) {
     if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Plan of the 4-wave form (two workgroups per CU): 128-row tiles, K split
-// (powers of two, at least 16 steps per split) until about 384 workgroups have
-// work.  MCQ4_GEMM4_SPLIT overrides.
+// Plan of the 4-wave form: 128-row tiles; K split S = the largest power of two
+// (<= 16, at least 16 K blocks per split) that keeps the grid within 256
+// workgroups, one per CU; doubled once more when that stays within 512 (two
+// per CU) and leaves at least 96 blocks per split, which pays on long K.
+// Measured over M = 128..2048 and the Llama shapes (graph replays): M=512
+// 11008x4096 S=4 63.9 us (the previous "until 384 workgroups" plan, S=8:
+// 78.5), M=512 4096x14336 S=1 72.7 (S=2: 81.6), M=2048 4096x4096 S=1 81.2
+// (S=2: 86.4), M=2048 14336x4096 S=2 242.9 (S=1: 252.9).  MCQ4_GEMM4_SPLIT
+// overrides.
 static G4Cfg gemm6_config1(int64_t M, int64_t K, int64_t N) {
     G4Cfg c{128, 1};
     const int64_t t = ((M + 127) / 128) * ((N + G4_BN - 1) / G4_BN);
     const int64_t nb = K / QK;
-    while (t * c.S < 384 && nb / (c.S * 2) >= 16 && c.S < 16) c.S *= 2;
+    while (t * c.S * 2 <= 256 && nb / (c.S * 2) >= 16 && c.S < 16) c.S *= 2;
+    if (t * c.S * 2 <= 512 && nb / (c.S * 2) >= 96 && c.S < 16) c.S *= 2;
     if (const char *env = getenv("MCQ4_GEMM4_SPLIT")) c.S = std::max(1, std::min(16, atoi(env)));
     if (c.S > nb) c.S = 1;
     return c;
