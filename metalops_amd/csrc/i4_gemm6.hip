@@ -333,8 +333,13 @@ i4_gemm6_kernel(I4GemmArgs a) {
     if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Plan: 128-row tiles, K split (powers of two, at least 16 steps per split)
-// until about 384 workgroups have work (two per CU).
+// Plan: 128-row tiles; K split S = the largest power of two (<= 16, at least 16
+// steps per split) that keeps the grid within 256 workgroups, one per CU,
+// doubled once more when that stays within 512 and leaves at least 64 steps per
+// split (q4_gemm6 asks 96; INT4 gains from the extra split down to 64: M=1024
+// 11008x4096 S=4 111 us vs S=2 122, M=512 4096x14336 S=2 80 vs S=1 84).  Against
+// the previous "until 384 workgroups" plan: M=512 4096x4096 35 us (41), M=128
+// 4096x14336 35 (39).  MCQ4_I4_GEMM6_SPLIT overrides.
 struct J6Cfg {
     int S;
 };
@@ -342,7 +347,9 @@ static J6Cfg i4_gemm6_config(int64_t M, int64_t K, int64_t N) {
     const int64_t t = ((M + J6_BM - 1) / J6_BM) * ((N + I4G_BN - 1) / I4G_BN);
     const int64_t ns = K / 32;
     int S = 1;
-    while (t * S < 384 && ns / (S * 2) >= 16 && S < 16) S *= 2;
+    while (t * S * 2 <= 256 && ns / (S * 2) >= 16 && S < 16) S *= 2;
+    if (t * S * 2 <= 512 && ns / (S * 2) >= 64 && S < 16) S *= 2;
+    if (const char *env = getenv("MCQ4_I4_GEMM6_SPLIT")) S = std::max(1, std::min(16, atoi(env)));
     if (S > ns) S = 1;
     return {S};
 }
