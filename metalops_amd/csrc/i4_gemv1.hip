@@ -1,9 +1,11 @@
-// Single-row (M == 1) per-group INT4 GEMV on gfx950 with the weight stream in
+// Decode (M = 1..16) per-group INT4 GEMV on gfx950 with the weight stream in
 // asynchronous global->LDS copies.
 //
-// Y[1][N] = x[K] @ W, W[k][n] = (q - z) * s per (group, column), packed[K/2][N]
+// Y[M][N] = X[M][K] @ W, W[k][n] = (q - z) * s per (group, column), packed[K/2][N]
 // (byte row k/2: even k in the low nibble), fp16 activations, fp32 sums.  The
 // roofline is HBM bandwidth: 0.5 byte per weight plus the group's scale/zero.
+// The description below is the M == 1 form; the MR form (M >= 2) differs only
+// where the kernel's MR comment says.
 //
 // Work decomposition
 //   * Tile = 128 columns (whole 128-byte pieces of each byte row); step = 32 K
@@ -60,15 +62,25 @@ struct I4Gemv1Args {
     int K, N, nsteps, spg, spw, S;
     int ngr_max;          // scale/zero slots per wave
     int wave_bytes;       // LDS bytes per wave
-    float *part;          // [tiles][S][128] when S > 1
+    int M;                // activation rows (1 .. 16)
+    int64_t ldx, ldy;     // row strides of X and Y (elements)
+    float *part;          // [tiles][S][M][128] when S > 1
     uint32_t *counters;   // [tiles]
 };
 
 constexpr int I1_SZSLOT = 1024; // scale/zero bytes per group (one 16-byte-per-lane copy)
+constexpr int I1_XSTEP = 1024;  // MR: a step's activations, 16 rows x 32 halves, after its weights
 
-template <int SZ, int ACT, bool XL>
+// MR (M = 2..16): each ring slot also holds the step's activation block (one
+// more 16-byte-per-lane copy per step: lane -> row min(l/4, M-1), 8 halves
+// 8(l%4)..), lane (c, g) feeds activation row c into the MFMAs, and the four
+// output rows 4g..4g+3 of each column are all live.
+template <int SZ, int ACT, bool XL, bool MR>
 __global__ void __launch_bounds__(I1_W * 64, 2)
 i4_gemv1_kernel(I4Gemv1Args a) {
+    constexpr int NR = MR ? 4 : 1;               // output rows per lane
+    constexpr int NCOPY = MR ? 3 : 2;            // copies per step
+    constexpr int STEPB = I1_STEP + (MR ? I1_XSTEP : 0);   // ring slot bytes
     constexpr int ESZ = SZ == DT_F32 ? 4 : 2;
     constexpr int SLOT = I1_SZSLOT;
     constexpr int PPR = I1_TC * ESZ / 16;        // 16-byte pieces per scale (or zero) row
@@ -87,14 +99,17 @@ i4_gemv1_kernel(I4Gemv1Args a) {
     const int s_begin = (sp * I1_W + wave) * a.spw;
     const int ns = max(0, min(a.spw, a.nsteps - s_begin));
 
-    uint8_t *const wl = smem + wave * a.wave_bytes;      // [ring R x 2 KiB][x 1 KiB][s/z slots]
+    // [ring R x STEPB][x 1 KiB, M == 1 only][s/z slots]
+    uint8_t *const wl = smem + wave * a.wave_bytes;
     uint8_t *const ring = wl;
-    uint8_t *const xs = wl + I1_R * I1_STEP;
-    uint8_t *const szs = xs + I1_XB;
+    uint8_t *const xs = wl + I1_R * STEPB;
+    uint8_t *const szs = xs + (MR ? 0 : I1_XB);
 
-    float acc[8];
+    float acc[8][NR];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < NR; ++i) acc[j][i] = 0.f;
 
     if (ns > 0) {
         // ---- scale/zero rows of the wave's groups, then its activations ----
@@ -113,7 +128,7 @@ i4_gemv1_kernel(I4Gemv1Args a) {
                     (void *)(src + (int64_t)gl * N * ESZ),
                     (__attribute__((address_space(3))) void *)(szs + gl * SLOT), 16, 0, 0);
         }
-        {
+        if constexpr (!MR) {
             // 16 halves-pieces of 8 activations; pieces past K re-read the last one.
             const int e = min(s_begin * 32 + 8 * lane, a.K - 8);
             __builtin_amdgcn_global_load_lds((void *)(a.X + e),
@@ -122,14 +137,18 @@ i4_gemv1_kernel(I4Gemv1Args a) {
 
         // ---- weight steps ----
         const uint8_t *wsrc = a.P + ((int64_t)s_begin * 16 + (lane >> 3)) * N + col0 + 16 * (lane & 7);
+        const _Float16 *xsrc = a.X + (int64_t)min(lane >> 2, a.M - 1) * a.ldx + (int64_t)s_begin * 32 + 8 * (lane & 3);
         auto issue = [&](int k) {                     // step k of the range into slot k % R
             const int kk = min(k, ns - 1);
             const uint8_t *src = wsrc + (int64_t)kk * 16 * N;
-            uint8_t *dst = ring + (k % I1_R) * I1_STEP;
+            uint8_t *dst = ring + (k % I1_R) * STEPB;
             __builtin_amdgcn_global_load_lds((void *)src, (__attribute__((address_space(3))) void *)dst,
                                              16, 0, 0);
             __builtin_amdgcn_global_load_lds((void *)(src + (int64_t)8 * N),
                                              (__attribute__((address_space(3))) void *)(dst + 1024), 16, 0, 0);
+            if constexpr (MR)
+                __builtin_amdgcn_global_load_lds((void *)(xsrc + kk * 32),
+                                                 (__attribute__((address_space(3))) void *)(dst + I1_STEP), 16, 0, 0);
         };
 #pragma unroll
         for (int k = 0; k < I1_R - 1; ++k) issue(k);
@@ -173,8 +192,11 @@ i4_gemv1_kernel(I4Gemv1Args a) {
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float tq = __builtin_fmaf(-zv[j], Sx[0], P[j][0] + Cc[0]);
-                acc[j] = __builtin_fmaf(sv[j], tq, acc[j]);
+#pragma unroll
+                for (int i = 0; i < NR; ++i) {
+                    const float tq = __builtin_fmaf(-zv[j], Sx[i], P[j][i] + Cc[i]);
+                    acc[j][i] = __builtin_fmaf(sv[j], tq, acc[j][i]);
+                }
                 P[j] = zf;
             }
             Cc = zf;
@@ -183,10 +205,10 @@ i4_gemv1_kernel(I4Gemv1Args a) {
 
         for (int k = 0; k < ns; ++k) {
             issue(k + I1_R - 1);
-            wait_vmcnt<(I1_R - 1) * 2>();          // step k (and everything older) landed
-            // x' for this step: elements 8g..8g+7 of the step.
-            const uint4_t xv = *(const __attribute__((address_space(3))) uint4_t *)(
-                lds_ptr(lds_addr(xs + k * 64 + 16 * g)));
+            wait_vmcnt<(I1_R - 1) * NCOPY>();      // step k (and everything older) landed
+            // x' for this step: elements 8g..8g+7 of the step (of row c with MR).
+            const uint4_t xv = *(const __attribute__((address_space(3))) uint4_t *)(lds_ptr(lds_addr(
+                MR ? ring + (k % I1_R) * STEPB + I1_STEP + 64 * c + 16 * g : xs + k * 64 + 16 * g)));
             const uint32_t x02 = __builtin_amdgcn_perm(xv[1], xv[0], 0x05040100u);     // x0, x2
             const uint32_t x13 = __builtin_amdgcn_perm(xv[1], xv[0], 0x07060302u);     // x1, x3
             const uint32_t x46 = __builtin_amdgcn_perm(xv[3], xv[2], 0x05040100u);     // x4, x6
@@ -196,7 +218,7 @@ i4_gemv1_kernel(I4Gemv1Args a) {
             Cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq, negc, Cc, 0, 0, 0);
             Sx = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq, ew, Sx, 0, 0, 0);
             // Byte rows 4g..4g+3, columns 8c..8c+7.
-            const lds_u8 *rs = lds_ptr(lds_addr(ring + (k % I1_R) * I1_STEP + (4 * g) * I1_TC + 8 * c));
+            const lds_u8 *rs = lds_ptr(lds_addr(ring + (k % I1_R) * STEPB + (4 * g) * I1_TC + 8 * c));
             u32x2 r[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) r[i] = *(const __attribute__((address_space(3))) u32x2 *)(rs + i * I1_TC);
@@ -220,35 +242,37 @@ i4_gemv1_kernel(I4Gemv1Args a) {
     }
 
     // ---- ordered sum over the waves ----
+    // Output v = row * 128 + column of the tile, rows < M (row 0 only for M == 1).
+    constexpr int ROWS = MR ? 16 : 1;
+    const int nout = (MR ? a.M : 1) * I1_TC;
     __syncthreads();
-    float *red = (float *)smem;                   // [8 waves][128]
-    if (g == 0) {
+    float *red = (float *)smem;                   // [8 waves][ROWS][128]
 #pragma unroll
-        for (int j = 0; j < 8; ++j) red[wave * I1_TC + 8 * c + j] = acc[j];
+    for (int i = 0; i < NR; ++i) {
+        const int row = MR ? 4 * g + i : 0;
+        if (MR ? row < a.M : g == 0) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) red[(wave * ROWS + row) * I1_TC + 8 * c + j] = acc[j][i];
+        }
     }
     __syncthreads();
-    if (a.S == 1) {
-        if (tid < I1_TC) {
-            float sum = 0.f;
+    auto wave_sum = [&](int v) {
+        float sum = 0.f;
 #pragma unroll
-            for (int w = 0; w < I1_W; ++w) sum += red[w * I1_TC + tid];
-            a.Y[col0 + tid] = (_Float16)activate<ACT>(sum);
-        }
+        for (int w = 0; w < I1_W; ++w) sum += red[w * ROWS * I1_TC + v];
+        return sum;
+    };
+    auto y_at = [&](int v) -> _Float16 & { return a.Y[(int64_t)(v / I1_TC) * a.ldy + col0 + v % I1_TC]; };
+    if (a.S == 1) {
+        for (int v = tid; v < nout; v += I1_W * 64) y_at(v) = (_Float16)activate<ACT>(wave_sum(v));
         return;
     }
-    // Split K: write-through partial stores, a ticket on the tile's counter, and
-    // the last workgroup sums every split's partial (L2-bypassing loads) in order.
-    float *part = a.part + ((int64_t)t * a.S + sp) * I1_TC;
+    float *part = a.part + ((int64_t)t * a.S + sp) * nout;
     if constexpr (XL) {
         // Ticket slots: 64-bit, 4096 per linear-id class mod 8 (one XCD each).
         uint64_t *cnt = (uint64_t *)a.counters + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
         const uint32_t xcc = xcc_id();
-        if (tid < I1_TC) {
-            float sum = 0.f;
-#pragma unroll
-            for (int w = 0; w < I1_W; ++w) sum += red[w * I1_TC + tid];
-            part[tid] = sum;
-        }
+        for (int v = tid; v < nout; v += I1_W * 64) part[v] = wave_sum(v);
         wait_vmcnt<0>();
         __syncthreads();
         uint32_t *last_flag = (uint32_t *)smem;
@@ -261,28 +285,26 @@ i4_gemv1_kernel(I4Gemv1Args a) {
         __syncthreads();
         const uint32_t lf = *last_flag;
         if (!lf) return;
-        if (tid < I1_TC) {
-            const float *base = a.part + (int64_t)t * a.S * I1_TC;
+        const float *base = a.part + (int64_t)t * a.S * nout;
+        for (int v = tid; v < nout; v += I1_W * 64) {
             float sum = 0.f;
             for (int q0 = 0; q0 < a.S; q0 += 8) {
                 float pv[8];
 #pragma unroll
-                for (int i = 0; i < 8; ++i) pv[i] = load_l2_f32(base, (min(q0 + i, a.S - 1) * I1_TC + tid) * 4);
+                for (int i = 0; i < 8; ++i) pv[i] = load_l2_f32(base, (min(q0 + i, a.S - 1) * nout + v) * 4);
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
                     if (q0 + i < a.S) sum += pv[i];
             }
-            a.Y[col0 + tid] = lf == 1 ? (_Float16)activate<ACT>(sum) : (_Float16)__builtin_nanf("");
+            y_at(v) = lf == 1 ? (_Float16)activate<ACT>(sum) : (_Float16)__builtin_nanf("");
         }
         if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    if (tid < I1_TC) {
-        float sum = 0.f;
-#pragma unroll
-        for (int w = 0; w < I1_W; ++w) sum += red[w * I1_TC + tid];
-        __hip_atomic_store(part + tid, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    // Split K: write-through partial stores, a ticket on the tile's counter, and
+    // the last workgroup sums every split's partial (L2-bypassing loads) in order.
+    for (int v = tid; v < nout; v += I1_W * 64)
+        __hip_atomic_store(part + v, wave_sum(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wait_vmcnt<0>();
     __syncthreads();
     uint32_t *last_flag = (uint32_t *)smem;
@@ -293,20 +315,20 @@ i4_gemv1_kernel(I4Gemv1Args a) {
     }
     __syncthreads();
     if (!*last_flag) return;
-    if (tid < I1_TC) {
-        const float *base = a.part + (int64_t)t * a.S * I1_TC + tid;
+    const float *base = a.part + (int64_t)t * a.S * nout;
+    for (int v = tid; v < nout; v += I1_W * 64) {
         float sum = 0.f;
         for (int q0 = 0; q0 < a.S; q0 += 8) {
             float pv[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                pv[i] = __hip_atomic_load(base + (int64_t)min(q0 + i, a.S - 1) * I1_TC, __ATOMIC_RELAXED,
+                pv[i] = __hip_atomic_load(base + (int64_t)min(q0 + i, a.S - 1) * nout + v, __ATOMIC_RELAXED,
                                           __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
             for (int i = 0; i < 8; ++i)
                 if (q0 + i < a.S) sum += pv[i];
         }
-        a.Y[col0 + tid] = (_Float16)activate<ACT>(sum);
+        y_at(v) = (_Float16)activate<ACT>(sum);
     }
     if (tid == 0) __hip_atomic_store(&a.counters[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -337,23 +359,33 @@ static I1Cfg i4_gemv1_config(int64_t K, int64_t N, int64_t gs) {
     return {(int)spw, (int)S, (int)ngr};
 }
 
-// M == 1, 4-bit weights, whole 128-column tiles, group size a multiple of 32,
-// 16-byte aligned operands, and a split count within bounds.
-bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, const void *P,
-                        const void *scales, const void *zeros) {
-    if (const char *env = getenv("MCQ4_I4_GEMV1"))
-        if (env[0] == '0') return false;
-    if (M != 1 || K < 32 || K % 32 || gs % 32 || N % I1_TC || N / I1_TC > COUNTER_SLOTS) return false;
-    if (((uintptr_t)X % 16) || ((uintptr_t)P % 16) || ((uintptr_t)scales % 16) || ((uintptr_t)zeros % 16))
-        return false;
-    const I1Cfg c = i4_gemv1_config(K, N, gs);
-    return c.S <= I1_SMAX && (size_t)I1_W * (I1_R * I1_STEP + I1_XB + c.ngr_max * I1_SZSLOT) <= 160 * 1024;
+static size_t i1_wave_bytes(int64_t M, const I1Cfg &c) {
+    return M > 1 ? (size_t)I1_R * (I1_STEP + I1_XSTEP) + c.ngr_max * I1_SZSLOT
+                 : (size_t)I1_R * I1_STEP + I1_XB + c.ngr_max * I1_SZSLOT;
 }
 
-size_t i4_gemv1_workspace_bytes(int64_t K, int64_t N, int64_t gs) {
+// 1 <= M <= 16, 4-bit weights, whole 128-column tiles, group size a multiple
+// of 32, 16-byte aligned operands (and activation rows), and a split count
+// within bounds.  MCQ4_I4_GEMV1=0 disables it; MCQ4_I4_GEMV1=1 limits it to M == 1.
+bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
+                        const void *P, const void *scales, const void *zeros) {
+    int64_t mmax = 16;
+    if (const char *env = getenv("MCQ4_I4_GEMV1")) {
+        if (env[0] == '0') return false;
+        if (env[0] == '1') mmax = 1;
+    }
+    if (M < 1 || M > mmax || K < 32 || K % 32 || gs % 32 || N % I1_TC || N / I1_TC > COUNTER_SLOTS) return false;
+    if (((uintptr_t)X % 16) || ((uintptr_t)P % 16) || ((uintptr_t)scales % 16) || ((uintptr_t)zeros % 16))
+        return false;
+    if (M > 1 && (ldx % 8 || ldx < K)) return false;
+    const I1Cfg c = i4_gemv1_config(K, N, gs);
+    return c.S <= I1_SMAX && (size_t)I1_W * i1_wave_bytes(M, c) <= 160 * 1024;
+}
+
+size_t i4_gemv1_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs) {
     const I1Cfg c = i4_gemv1_config(K, N, gs);
     if (c.S == 1) return 0;
-    return COUNTER_BYTES + (size_t)(N / I1_TC) * c.S * I1_TC * sizeof(float);
+    return COUNTER_BYTES + (size_t)(N / I1_TC) * c.S * std::max<int64_t>(M, 1) * I1_TC * sizeof(float);
 }
 
 // The XCD-local exchange (default; MCQ4_XCD_LOCAL=0 selects the agent-scope
@@ -363,7 +395,7 @@ static bool use_xcd_local(int ntiles, int S) {
     return !(env && env[0] == '0') && S > 1 && (ntiles + 7) / 8 <= 4096;
 }
 
-template <int SZ, int ACT, bool XL>
+template <int SZ, int ACT, bool XL, bool MR>
 static hipError_t launch_i1(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
     const size_t lds = (size_t)I1_W * a.wave_bytes;
     static std::atomic<uint64_t> done{0};
@@ -372,20 +404,21 @@ static hipError_t launch_i1(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)i4_gemv1_kernel<SZ, ACT, XL>,
+        e = hipFuncSetAttribute((const void *)i4_gemv1_kernel<SZ, ACT, XL, MR>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
     const int gx = XL ? (ntiles + 7) / 8 * 8 : ntiles;
-    hipLaunchKernelGGL((i4_gemv1_kernel<SZ, ACT, XL>), dim3(gx, a.S), dim3(I1_W * 64), lds, s, a);
+    hipLaunchKernelGGL((i4_gemv1_kernel<SZ, ACT, XL, MR>), dim3(gx, a.S), dim3(I1_W * 64), lds, s, a);
     return hipGetLastError();
 }
 
 template <int SZ, int ACT>
 static hipError_t launch_i1_xl(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
-    if (use_xcd_local(ntiles, a.S)) return launch_i1<SZ, ACT, true>(a, ntiles, s);
-    return launch_i1<SZ, ACT, false>(a, ntiles, s);
+    const bool xl = use_xcd_local(ntiles, a.S);
+    if (a.M > 1) return xl ? launch_i1<SZ, ACT, true, true>(a, ntiles, s) : launch_i1<SZ, ACT, false, true>(a, ntiles, s);
+    return xl ? launch_i1<SZ, ACT, true, false>(a, ntiles, s) : launch_i1<SZ, ACT, false, false>(a, ntiles, s);
 }
 
 template <int SZ>
@@ -395,14 +428,16 @@ static hipError_t launch_i1_act(const I4Gemv1Args &a, int ntiles, int act, hipSt
     return launch_i1_xl<SZ, ACT_NONE>(a, ntiles, s);
 }
 
-hipError_t launch_i4_gemv1(const _Float16 *X, const uint8_t *P, const void *scales, const void *zeros,
-                           int sz_dt, _Float16 *Y, int K, int N, int gs, int act, void *ws, hipStream_t s) {
+hipError_t launch_i4_gemv1(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
+                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K, int N, int gs,
+                           int act, void *ws, hipStream_t s) {
     const I1Cfg c = i4_gemv1_config(K, N, gs);
     I4Gemv1Args a;
     a.X = X; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y;
     a.K = K; a.N = N; a.nsteps = K / 32; a.spg = gs / 32; a.spw = c.spw; a.S = c.S;
     a.ngr_max = c.ngr_max;
-    a.wave_bytes = I1_R * I1_STEP + I1_XB + c.ngr_max * I1_SZSLOT;
+    a.M = M; a.ldx = ldx; a.ldy = ldy;
+    a.wave_bytes = (int)i1_wave_bytes(M, c);
     a.part = nullptr; a.counters = nullptr;
     if (c.S > 1) {
         if (!ws) return hipErrorInvalidValue;

@@ -437,6 +437,44 @@ def test_gemv1_paths(mo, dev, monkeypatch, K, N, gs, spw, sz):
     _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
 
 
+GEMV1_MR_CASES = [
+    # (M, K, N, gs, steps per wave or None)
+    (2, 4096, 4096, 128, None), (3, 4096, 14336, 128, None), (4, 14336, 4096, 128, None),
+    (8, 4096, 1024, 32, None), (9, 2048, 512, 64, 3), (16, 4096, 14336, 128, None),
+    (16, 11008, 4096, 128, None), (5, 160, 128, 32, 2), (16, 32, 256, 32, None), (7, 1024, 16384, 128, None),
+]
+
+
+@pytest.mark.parametrize("M,K,N,gs,spw", GEMV1_MR_CASES)
+@pytest.mark.parametrize("sz", [R.F16, R.BF16, R.F32])
+def test_gemv1_multirow(mo, dev, monkeypatch, M, K, N, gs, spw, sz):
+    """The async-copy GEMV with 2..16 activation rows (each ring slot carries the
+    step's activation block) against the oracle, the register-ring GEMV, and the
+    agent-scope split exchange (identical bits)."""
+    print(f"gemv1 multirow M={M} K={K} N={N} gs={gs} spw={spw} sz={sz}", flush=True)
+    for k in ("MCQ4_I4_SPW1", "MCQ4_I4_GEMV1", "MCQ4_I4_PATH", "MCQ4_XCD_LOCAL"):
+        monkeypatch.delenv(k, raising=False)
+    if spw is not None:
+        monkeypatch.setenv("MCQ4_I4_SPW1", str(spw))
+    w, packed, s, z = _quant(mo, dev, K, N, gs, sz, seed=M + K + N + gs)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(M * K)).half().to(dev)
+    Yref = _ref(X, packed, s, z, gs)
+    Y = mo.matmul_int4(X, packed, s, z, gs)
+    _check_rows(Y.float().cpu().numpy(), Yref)
+    Y2 = mo.matmul_int4(X, packed, s, z, gs)                  # counters were left at zero
+    assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
+    monkeypatch.setenv("MCQ4_XCD_LOCAL", "0")
+    assert torch.equal(mo.matmul_int4(X, packed, s, z, gs).view(torch.int16), Y.view(torch.int16))
+    monkeypatch.delenv("MCQ4_XCD_LOCAL")
+    # row-strided activations: a view into a wider buffer
+    Xw = torch.zeros(M, K + 64, dtype=torch.float16, device=dev)
+    Xw[:, :K] = X
+    assert torch.equal(mo.matmul_int4(Xw[:, :K], packed, s, z, gs).view(torch.int16), Y.view(torch.int16))
+    # the register-ring GEMV (async-copy kernel limited to M == 1)
+    monkeypatch.setenv("MCQ4_I4_GEMV1", "1")
+    _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
+
+
 @pytest.mark.parametrize("act", ["silu", "gelu"])
 def test_gemv1_fused_activation(mo, dev, act):
     K, N, gs = 4096, 1024, 128
