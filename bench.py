@@ -35,6 +35,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
+FP16_PEAK_SCLK_MHZ = 2400.0  # the shader clock that peak is quoted at (256 CUs)
 
 # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the same
 # workloads (bench.py --part decode|prefill), each counter scaled by what it reads
@@ -196,6 +197,21 @@ def prefill_bench(mo, torch, dev, iters=30, warmup=10):
         out.append({"name": name, "M": M, "K": K, "N": N, "ms": t * 1e3, "tflops": fl / t / 1e12})
         del w, x
     return out
+
+
+def measure_sclk(torch, dev, iters=20000, reps=3):
+    """Shader clock (MHz) under an MFMA load, from s_memtime against the 100 MHz
+    s_memrealtime (mcq4_measure_sclk): median over the waves of the last of `reps`
+    back-to-back runs, so the clock has settled under the power limit."""
+    from metalops_amd import _lib
+    ticks = torch.zeros(4096, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(reps):
+        _lib.check(_lib.lib.mcq4_measure_sclk(ticks.data_ptr(), iters, stream.cuda_stream), "mcq4_measure_sclk")
+    torch.cuda.synchronize(dev)
+    t = ticks.view(-1, 2).double().cpu()
+    mhz = (100.0 * t[:, 0] / t[:, 1]).median().item()
+    return mhz
 
 
 def make_i4_weights(mo, torch, K, N, seed, dev, outliers=False):
@@ -378,6 +394,8 @@ def main():
     t_launch = t_step / dec["launches_step"]
     pre = prefill_bench(mo, torch, dev)
     pre_up = pre[0]
+    sclk = measure_sclk(torch, dev)
+    peak_sclk = FP16_PEAK_TFLOPS * sclk / FP16_PEAK_SCLK_MHZ
 
     i4_dec = i4_decode_bench(mo, torch, dev, args)
     i4_t = i4_dec["seconds"] / i4_dec["steps"]
@@ -435,6 +453,12 @@ def main():
                 "frac": round(pre_up["tflops"] / FP16_PEAK_TFLOPS, 4),
                 "traffic": PREFILL_UP_TRAFFIC_BYTES,
                 "kernel": "q4_gemm6_kernel<1> (M=2048 K=4096 N=14336)",
+                "sclk_mhz_mfma_load": round(sclk, 1),
+                "sclk_probe": "mcq4_measure_sclk: 512 workgroups of MFMA chains on random fp16 "
+                              "operands, s_memtime vs s_memrealtime; a full MFMA load, so a lower "
+                              "bound on the clock the GEMM itself runs at",
+                "peak_at_sclk": round(peak_sclk, 1),
+                "frac_at_sclk": round(pre_up["tflops"] / peak_sclk, 4),
             },
         },
         "cpu_baseline": cpu,

@@ -204,6 +204,18 @@ int mcq4_fused_rmsnorm_linear_int4(const void *X, int64_t ldx, const void *w_nor
                                    int64_t N, int64_t group_size, void *workspace,
                                    size_t workspace_bytes, void *stream);
 
+/*
+ * Measurement helper; no counterpart in the reference (the benchmark uses it to
+ * restate the fp16 MFMA peak at the measured clock).  Runs 512 workgroups of 4
+ * waves, each `iters` rounds of four v_mfma_f32_32x32x16_f16 chains on fresh
+ * pseudo-random fp16 operands, and writes
+ * per wave w the shader-clock ticks (s_memtime) and 100 MHz real-time ticks
+ * (s_memrealtime) of the loop to ticks[2w] and ticks[2w+1]: ticks is a device
+ * buffer of 4096 uint64 owned by the caller.  sclk = 100 MHz * ticks[2w] /
+ * ticks[2w+1].
+ */
+int mcq4_measure_sclk(uint64_t *ticks, int iters, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
