@@ -507,3 +507,25 @@ def test_gemm6_paths(mo, dev, monkeypatch, M, K, N, gs, sz):
         _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
     monkeypatch.setenv("MCQ4_I4_GEMM6", "0")
     _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), Yref)
+
+
+def _random_decode_shapes(n, seed):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        gs = int(rng.choice([32, 64, 128, 256]))
+        K = int(rng.integers(1, 64)) * gs
+        N = int(rng.integers(1, 40)) * 128
+        M = int(rng.integers(1, 17))
+        out.append((M, K, N, gs))
+    return out
+
+
+@pytest.mark.parametrize("M,K,N,gs", _random_decode_shapes(16, 2024))
+def test_decode_random_shapes(mo, dev, M, K, N, gs):
+    """Seeded random decode shapes (M 1..16, any group size, tile counts that are
+    not multiples of 8) through the default kernels, against the oracle."""
+    print(f"random decode M={M} K={K} N={N} gs={gs}", flush=True)
+    w, packed, s, z = _quant(mo, dev, K, N, gs, seed=M * 7 + K + N)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(K + M)).half().to(dev)
+    _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), _ref(X, packed, s, z, gs))
