@@ -167,10 +167,12 @@ int mcq4_dequantize_q4_0(const uint8_t *blocks, int64_t K, int64_t N, void *out,
 
 size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M <= 0 || K <= 0 || N <= 0 || K % 32) return 0;
-    if (M <= 64) return mcq4::skinny_workspace_bytes(M, K, N);
+    if (M <= 32) return mcq4::skinny_workspace_bytes(M, K, N);
     // The largest of the split-K kernels' needs: an upper bound for any prefill kernel.
-    return std::max({mcq4::gemm_workspace_bytes(M, K, N), mcq4::gemm4_workspace_bytes(M, K, N),
-                     mcq4::gemm5_workspace_bytes(M, K, N), mcq4::gemm6_workspace_bytes(M, K, N)});
+    const size_t pre = std::max({mcq4::gemm_workspace_bytes(M, K, N), mcq4::gemm4_workspace_bytes(M, K, N),
+                                 mcq4::gemm5_workspace_bytes(M, K, N), mcq4::gemm6_workspace_bytes(M, K, N)});
+    // 33..64 rows run either family, depending on the pointers' alignment.
+    return M <= 64 ? std::max(pre, mcq4::skinny_workspace_bytes(M, K, N)) : pre;
 }
 
 int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, int64_t ldy,
@@ -194,7 +196,10 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
     if (need && !aligned(workspace, 16))
         return fail(MCQ4_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
     hipError_t e;
-    if (M <= 64)
+    // 33..64 rows: q4_gemm6 (flat ~31 us for any M <= 128 on 4096x14336) beats the
+    // register-load decode kernel (40-77 us) wherever its alignment rules hold.
+    const bool skinny = M <= 32 || (M <= 64 && !mcq4::gemm4_supported((const _Float16 *)X, ldx, W, K, N));
+    if (skinny)
         e = mcq4::launch_skinny((const _Float16 *)X, ldx, W, (_Float16 *)Y, ldy, (int)M, (int)K,
                                 (int)N, workspace, (hipStream_t)stream);
     else {

@@ -192,6 +192,8 @@ PATHS = {
     "gemvm_split4": {"MCQ4_GEMVM_SPLIT": "4"},
     "gemvm_split2_reduce": {"MCQ4_GEMVM_SPLIT": "2", "MCQ4_XCD_LOCAL": "0"},
     "decode_lds": {},
+    "two_pass_17_32": {},
+    "gemm6_33_64": {},
     "decode_lds_small_m": {"MCQ4_GEMV_PATH": "off"},
     "decode_direct": {"MCQ4_DECODE_PATH": "direct"},
     "gemm_sync": {"MCQ4_GEMM_PATH": "sync"},
@@ -237,6 +239,8 @@ PATH_SHAPES = {
     "gemvm_split4": [(16, 4096, 1040), (6, 11008, 264), (13, 352, 8200)],
     "gemvm_split2_reduce": [(9, 4096, 1040), (16, 14336, 4096)],
     "decode_lds": [(1, 352, 264), (40, 2048, 96), (64, 256, 64), (17, 1024, 520), (33, 4096, 1032)],
+    "two_pass_17_32": [(17, 4096, 1024), (20, 2048, 4096), (32, 14336, 512), (31, 1024, 2048), (18, 352, 272)],
+    "gemm6_33_64": [(33, 4096, 1024), (48, 2048, 768), (64, 11008, 512), (40, 352, 256)],
     "decode_lds_small_m": [(3, 1024, 520), (16, 4096, 1032)],
     "decode_direct": [(1, 352, 257), (7, 1024, 520), (16, 4096, 1000), (64, 512, 72)],
     "gemm_sync": [(65, 352, 70), (200, 1024, 264), (300, 2048, 520)],
