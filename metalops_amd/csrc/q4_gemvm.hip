@@ -47,7 +47,9 @@ struct GemvMArgs {
     uint64_t *tickets;
 };
 
-template <int WAVES, int TPW>
+// RB row blocks of 16 activation rows (M <= 16 RB): each K-block row's B
+// operand is built once and feeds the MFMAs of every row block.
+template <int WAVES, int TPW, int RB>
 __global__ void __launch_bounds__(WAVES * 64)
 q4_gemvm_kernel(GemvMArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -81,13 +83,18 @@ q4_gemvm_kernel(GemvMArgs a) {
         crow[i] = q < GM_WCH ? q / 18 : 0;
         coff[i] = q < GM_WCH ? (uint32_t)(q / 18) * grow + 16u * (uint32_t)(q % 18) : 0u;
     }
-    const uint8_t *xrow = (const uint8_t *)a.X + (int64_t)min(c, a.M - 1) * a.ldx * 2 + 16 * g;
-    uint4_t xr[GM_B];
+    const uint8_t *xrow[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+        xrow[rb] = (const uint8_t *)a.X + (int64_t)min(16 * rb + c, a.M - 1) * a.ldx * 2 + 16 * g;
+    uint4_t xr[RB][GM_B];
     auto load_x = [&](int m) {
         const int row0 = (b0 + wave + WAVES * m) * GM_B;
 #pragma unroll
-        for (int u = 0; u < GM_B; ++u)
-            xr[u] = *(const uint4_t *)(xrow + (int64_t)min(row0 + u, a.nb - 1) * (QK * 2));
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int u = 0; u < GM_B; ++u)
+                xr[rb][u] = *(const uint4_t *)(xrow[rb] + (int64_t)min(row0 + u, a.nb - 1) * (QK * 2));
     };
     auto copy_item = [&](int m, int j, int slot) {
         const int row0 = (b0 + wave + WAVES * m) * GM_B;
@@ -123,24 +130,28 @@ q4_gemvm_kernel(GemvMArgs a) {
     const float4_t z = {0.f, 0.f, 0.f, 0.f};
     const half2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
 
-    float4_t acc[TPW];
+    float4_t acc[RB][TPW];
 #pragma unroll
-    for (int j = 0; j < TPW; ++j) acc[j] = z;
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int j = 0; j < TPW; ++j) acc[rb][j] = z;
 
     int k = 0, slot = 0;
     for (int m = 0; m < nbm; ++m) {
         const int rows = min(GM_B, a.nb - (b0 + wave + WAVES * m) * GM_B);
-        half8_t xq[GM_B];
+        half8_t xq[RB][GM_B];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int u = 0; u < GM_B; ++u) {
-            const uint4_t x = xr[u];
+            const uint4_t x = xr[rb][u];
             const uint32_t h15 = __builtin_amdgcn_perm(x[2], x[0], 0x07060302u);   // x1, x5
             const uint32_t h37 = __builtin_amdgcn_perm(x[3], x[1], 0x07060302u);   // x3, x7
             const uint4_t v = {__builtin_amdgcn_perm(x[2], x[0], 0x05040100u),     // x0, x4
                                bitcast<uint32_t>(bitcast<half2_t>(h15) * s16),
                                __builtin_amdgcn_perm(x[3], x[1], 0x05040100u),     // x2, x6
                                bitcast<uint32_t>(bitcast<half2_t>(h37) * s16)};
-            xq[u] = bitcast<half8_t>(v);
+            xq[rb][u] = bitcast<half8_t>(v);
         }
 #pragma unroll
         for (int j = 0; j < TPW; ++j) {
@@ -151,7 +162,7 @@ q4_gemvm_kernel(GemvMArgs a) {
                 const bool xnext = more && ij == 0;
                 if (more) issue_next();
                 if (!more) wait_vmcnt<0>();
-                else if (xnext) wait_vmcnt<GM_B + 3>();
+                else if (xnext) wait_vmcnt<RB * GM_B + 3>();
                 else wait_vmcnt<3>();
                 const uint32_t base = lds_addr(ring + slot * GM_SLOT);
                 const uint32_t qa = base + qal, da = base + doff;
@@ -165,10 +176,13 @@ q4_gemvm_kernel(GemvMArgs a) {
                                         and_or(w8, mlo, c64), and_or(w8, mhi, c64)};
                     // -S of this row, recomputed per item: keeps 32 VGPRs free so a
                     // 16-wave workgroup fits in 128 VGPRs (the MFMA pipe has room).
-                    const float4_t ns = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], negc, z, 0, 0, 0);
-                    const float4_t blk =
-                        __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], bitcast<half8_t>(bq), ns, 0, 0, 0);
-                    acc[j] += d * blk;
+#pragma unroll
+                    for (int rb = 0; rb < RB; ++rb) {
+                        const float4_t ns = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb][u], negc, z, 0, 0, 0);
+                        const float4_t blk =
+                            __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb][u], bitcast<half8_t>(bq), ns, 0, 0, 0);
+                        acc[rb][j] += d * blk;
+                    }
                 };
                 if (rows == GM_B) {
 #pragma unroll
@@ -185,29 +199,35 @@ q4_gemvm_kernel(GemvMArgs a) {
         }
     }
 
-    // Partials: lane (c, g) holds rows 4g..4g+3 of column c.
+    // Partials: lane (c, g) holds rows 4g..4g+3 of column c (of row block rb).
+    // One row block at a time through the LDS partial area.
 #pragma unroll
-    for (int j = 0; j < TPW; ++j)
-        if (j < ntl) {
-            float *rp = red + ((j * WAVES + wave) * 16 + 4 * g) * 16 + c;
+    for (int rb = 0; rb < RB; ++rb) {
+        if (rb > 0) __syncthreads();              // the previous block's sums are read
 #pragma unroll
-            for (int i = 0; i < 4; ++i) rp[16 * i] = nbm > 0 ? acc[j][i] : 0.f;
+        for (int j = 0; j < TPW; ++j)
+            if (j < ntl) {
+                float *rp = red + ((j * WAVES + wave) * 16 + 4 * g) * 16 + c;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) rp[16 * i] = nbm > 0 ? acc[rb][j][i] : 0.f;
+            }
+        __syncthreads();
+        for (int v = tid; v < ntl * 256; v += WAVES * 64) {
+            const int j = v >> 8, rr = 16 * rb + ((v >> 4) & 15), col = v & 15;
+            if (rr >= a.M) continue;
+            float s = 0.f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) s += red[((j * WAVES + w) * 16 + (rr & 15)) * 16 + col];
+            const int n = (wg + j * G) * 16 + col;
+            if (a.S == 1) a.Y[(int64_t)rr * a.ldy + n] = (_Float16)s;
+            else a.part[((int64_t)sp * a.M + rr) * (16 * a.ntiles) + n] = s;
         }
-    __syncthreads();
-    for (int v = tid; v < ntl * 256; v += WAVES * 64) {
-        const int j = v >> 8, rr = (v >> 4) & 15, col = v & 15;
-        if (rr >= a.M) continue;
-        float s = 0.f;
-#pragma unroll
-        for (int w = 0; w < WAVES; ++w) s += red[((j * WAVES + w) * 16 + rr) * 16 + col];
-        const int n = (wg + j * G) * 16 + col;
-        if (a.S == 1) a.Y[(int64_t)rr * a.ldy + n] = (_Float16)s;
-        else a.part[((int64_t)sp * a.M + rr) * (16 * a.ntiles) + n] = s;
     }
     if (a.S == 1 || !a.tickets) return;
     // Every split of this workgroup runs on this XCD (same blockIdx.x, grid.x a
     // multiple of 8): the last to arrive sums the partials, in split order as the
-    // reduction kernel does, from the XCD's L2.
+    // reduction kernel does, from the XCD's L2 (its own too with RB > 1: the LDS
+    // area holds only the last row block's wave sums).
     wait_vmcnt<0>();
     __syncthreads();
     uint64_t *cnt = a.tickets + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
@@ -222,18 +242,21 @@ q4_gemvm_kernel(GemvMArgs a) {
     const uint32_t lf = *last_flag;
     if (!lf) return;
     const int64_t pstride = (int64_t)a.M * 16 * a.ntiles;         // floats per split
-    for (int v = tid; v < ntl * 256; v += WAVES * 64) {
-        const int j = v >> 8, rr = (v >> 4) & 15, col = v & 15;
-        if (rr >= a.M) continue;
+    for (int v = tid; v < TPW * 256 * RB; v += WAVES * 64) {   // v = (rb, j, row, col)
+        const int j = (v >> 8) % TPW, rr = 16 * (v / (256 * TPW)) + ((v >> 4) & 15), col = v & 15;
+        if (j >= ntl || rr >= a.M) continue;
         float own = 0.f;
+        if (RB == 1) {
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) own += red[((j * WAVES + w) * 16 + rr) * 16 + col];
+            for (int w = 0; w < WAVES; ++w) own += red[((j * WAVES + w) * 16 + rr) * 16 + col];
+        }
         const int n = (wg + j * G) * 16 + col;
         const float *base = a.part + (int64_t)rr * (16 * a.ntiles) + n;
         float pv[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q)
-            pv[q] = q < a.S && q != sp ? load_l2_f32(a.part, (int)(((int64_t)q * pstride + (base - a.part)) * 4)) : own;
+            pv[q] = q < a.S && (RB > 1 || q != sp)
+                        ? load_l2_f32(a.part, (int)(((int64_t)q * pstride + (base - a.part)) * 4)) : own;
         float t = 0.f;
 #pragma unroll
         for (int q = 0; q < 8; ++q)
@@ -259,7 +282,7 @@ static size_t gemvm_lds_bytes(int waves, int tpw) {
     return (size_t)waves * 2 * GM_SLOT + (size_t)tpw * waves * 256 * sizeof(float);
 }
 
-template <int WAVES, int TPW>
+template <int WAVES, int TPW, int RB>
 static hipError_t launch_gemvm_t(const GemvMArgs &a, int grid, hipStream_t s) {
     const size_t lds = gemvm_lds_bytes(WAVES, TPW);
     static std::atomic<uint64_t> done{0};
@@ -268,13 +291,13 @@ static hipError_t launch_gemvm_t(const GemvMArgs &a, int grid, hipStream_t s) {
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)q4_gemvm_kernel<WAVES, TPW>,
+        e = hipFuncSetAttribute((const void *)q4_gemvm_kernel<WAVES, TPW, RB>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
     const int gx = a.tickets ? (grid + 7) / 8 * 8 : grid;
-    hipLaunchKernelGGL((q4_gemvm_kernel<WAVES, TPW>), dim3(gx, a.S), dim3(WAVES * 64), lds, s, a);
+    hipLaunchKernelGGL((q4_gemvm_kernel<WAVES, TPW, RB>), dim3(gx, a.S), dim3(WAVES * 64), lds, s, a);
     if (a.S > 1 && !a.tickets) {
         const int64_t n = (int64_t)a.M * 16 * a.ntiles;
         hipLaunchKernelGGL(q4_gemvm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
@@ -282,24 +305,24 @@ static hipError_t launch_gemvm_t(const GemvMArgs &a, int grid, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int WAVES>
+template <int WAVES, int RB>
 static hipError_t launch_gemvm_w(const GemvMArgs &a, int grid, int tpw, hipStream_t s) {
     switch (tpw) {
-        case 1: return launch_gemvm_t<WAVES, 1>(a, grid, s);
-        case 2: return launch_gemvm_t<WAVES, 2>(a, grid, s);
-        case 3: return launch_gemvm_t<WAVES, 3>(a, grid, s);
-        default: return launch_gemvm_t<WAVES, 4>(a, grid, s);
+        case 1: return launch_gemvm_t<WAVES, 1, RB>(a, grid, s);
+        case 2: return launch_gemvm_t<WAVES, 2, RB>(a, grid, s);
+        case 3: return launch_gemvm_t<WAVES, 3, RB>(a, grid, s);
+        default: return launch_gemvm_t<WAVES, 4, RB>(a, grid, s);
     }
 }
 
-// 2 <= M <= 16, 16-byte aligned weights and activation rows, N % 8 == 0, at
-// least one 16-column tile and at most 4 tiles per workgroup on a
-// 512-workgroup grid (N <= 32768).
+// 2 <= M <= 32 (two row blocks above 16), 16-byte aligned weights and
+// activation rows, N % 8 == 0, at least one 16-column tile and at most 4 tiles
+// per workgroup on a 512-workgroup grid (N <= 32768).
 bool gemvm_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
                      int64_t N) {
     if (const char *env = getenv("MCQ4_GEMV_PATH"))
         if (env[0] == 'o') return false;
-    return M >= 2 && M <= 16 && N % 8 == 0 && N >= 16 && N / 16 <= 512 * GM_TPW_MAX &&
+    return M >= 2 && M <= 32 && N % 8 == 0 && N >= 16 && N / 16 <= 512 * GM_TPW_MAX &&
            ((uintptr_t)W % 16) == 0 && ((uintptr_t)X % 16) == 0 && ldx % 8 == 0 && K >= QK &&
            N * 18 * 8 < ((int64_t)1 << 31);
 }
@@ -320,7 +343,9 @@ static GmPlan gemvm_plan(int64_t M, int64_t K, int64_t N) {
     const int ntiles = (int)(N / 16), nbt = (int)((K / QK + GM_B - 1) / GM_B);
     int waves = 16;
     if (const char *env = getenv("MCQ4_GEMVM_WAVES")) waves = atoi(env) == 8 ? 8 : 16;
-    const int cap = waves == 8 ? 512 : 256;
+    // Two row blocks: 8-wave workgroups, one per CU (their registers fill the SIMDs).
+    if (M > 16) waves = 8;
+    const int cap = waves == 8 && M <= 16 ? 512 : 256;
     int S = M >= 8 && ntiles <= cap && nbt >= 2 * waves ? 2 : 1;
     if (const char *env = getenv("MCQ4_GEMVM_SPLIT")) {
         const int v = atoi(env);
@@ -334,7 +359,7 @@ static GmPlan gemvm_plan(int64_t M, int64_t K, int64_t N) {
 }
 
 size_t gemvm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
-    if (M < 2 || M > 16 || N < 16 || K < QK) return 0;
+    if (M < 2 || M > 32 || N < 16 || K < QK) return 0;
     const GmPlan p = gemvm_plan(M, K, N);
     // Partials follow the workspace's counter area, which other kernels rely on staying zero.
     return p.S > 1 ? COUNTER_BYTES + (size_t)p.S * M * (N / 16) * 16 * sizeof(float) : 0;
@@ -358,8 +383,9 @@ hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
         const char *xl = getenv("MCQ4_XCD_LOCAL");
         if (!(xl && xl[0] == '0') && p.S <= 8) a.tickets = (uint64_t *)ws;
     }
-    if (p.waves == 16) return launch_gemvm_w<16>(a, p.grid, p.tpw, s);
-    return launch_gemvm_w<8>(a, p.grid, p.tpw, s);
+    if (M > 16) return launch_gemvm_w<8, 2>(a, p.grid, p.tpw, s);
+    if (p.waves == 16) return launch_gemvm_w<16, 1>(a, p.grid, p.tpw, s);
+    return launch_gemvm_w<8, 1>(a, p.grid, p.tpw, s);
 }
 
 }  // namespace mcq4

@@ -274,10 +274,7 @@ size_t skinny_workspace_bytes(int64_t M, int64_t K, int64_t N) {
         const int64_t tiles = (N + 16 * c.NT - 1) / (16 * c.NT);
         need = COUNTER_BYTES + (size_t)tiles * c.S * MT * c.NT * 256 * sizeof(float);
     }
-    need = std::max(need, gemvm_workspace_bytes(M, K, N));
-    if (M > 16 && M <= 32)                        // the two-pass form (launch_skinny)
-        need = std::max({need, gemvm_workspace_bytes(16, K, N), gemvm_workspace_bytes(M - 16, K, N)});
-    return need;
+    return std::max(need, gemvm_workspace_bytes(M, K, N));
 }
 
 bool decode_lds_supported(const uint8_t *W, int64_t N, int64_t ldx);
@@ -302,19 +299,6 @@ static bool use_decode_lds(const uint8_t *W, int64_t N, int64_t ldx) {
 hipError_t launch_skinny(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                          int64_t ldy, int M, int K, int N, void *ws, hipStream_t s) {
     int n_begin = 0;
-    // 17..32 rows: two passes of the small-batch GEMV (rows 0..15, then the rest,
-    // which re-reads the weights) beat the register-load kernel: 4096x14336 M=32
-    // 25.6 us vs 33.7, 14336x4096 vs 47.7; M=17 22.6 us vs 27.5.  Needs whole
-    // 16-column tiles so both passes cover every column.
-    const _Float16 *X1 = X + 16 * ldx;
-    if (M > 16 && M <= 32 && N % 16 == 0 && use_decode_lds(W, N, ldx) &&
-        gemvm_supported(X, ldx, W, 16, K, N) &&
-        (M - 16 == 1 ? gemv_dma_supported(X1, W, K, N) : gemvm_supported(X1, ldx, W, M - 16, K, N))) {
-        hipError_t e = launch_gemvm(X, ldx, W, Y, ldy, 16, K, N, ws, &n_begin, s);
-        if (e != hipSuccess) return e;
-        if (M - 16 == 1) return launch_gemv_dma(X1, W, Y + 16 * ldy, K, N, &n_begin, s);
-        return launch_gemvm(X1, ldx, W, Y + 16 * ldy, ldy, M - 16, K, N, ws, &n_begin, s);
-    }
     if (use_decode_lds(W, N, ldx) && skinny_config(M, K, N).S == 1) {
         hipError_t e;
         if (M == 1 && gemv_dma_supported(X, W, K, N))

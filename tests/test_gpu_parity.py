@@ -192,7 +192,9 @@ PATHS = {
     "gemvm_split4": {"MCQ4_GEMVM_SPLIT": "4"},
     "gemvm_split2_reduce": {"MCQ4_GEMVM_SPLIT": "2", "MCQ4_XCD_LOCAL": "0"},
     "decode_lds": {},
-    "two_pass_17_32": {},
+    "gemvm_rb2": {},
+    "gemvm_rb2_split2": {"MCQ4_GEMVM_SPLIT": "2"},
+    "gemvm_rb2_split4_reduce": {"MCQ4_GEMVM_SPLIT": "4", "MCQ4_XCD_LOCAL": "0"},
     "gemm6_33_64": {},
     "decode_lds_small_m": {"MCQ4_GEMV_PATH": "off"},
     "decode_direct": {"MCQ4_DECODE_PATH": "direct"},
@@ -239,7 +241,10 @@ PATH_SHAPES = {
     "gemvm_split4": [(16, 4096, 1040), (6, 11008, 264), (13, 352, 8200)],
     "gemvm_split2_reduce": [(9, 4096, 1040), (16, 14336, 4096)],
     "decode_lds": [(1, 352, 264), (40, 2048, 96), (64, 256, 64), (17, 1024, 520), (33, 4096, 1032)],
-    "two_pass_17_32": [(17, 4096, 1024), (20, 2048, 4096), (32, 14336, 512), (31, 1024, 2048), (18, 352, 272)],
+    "gemvm_rb2": [(17, 4096, 1024), (20, 2048, 4096), (32, 14336, 512), (31, 1024, 2048), (18, 352, 272),
+                  (24, 4096, 1032), (29, 11008, 4096)],
+    "gemvm_rb2_split2": [(32, 14336, 4096), (21, 4096, 1040), (17, 2048, 264)],
+    "gemvm_rb2_split4_reduce": [(32, 4096, 1024), (25, 11008, 512)],
     "gemm6_33_64": [(33, 4096, 1024), (48, 2048, 768), (64, 11008, 512), (40, 352, 256)],
     "decode_lds_small_m": [(3, 1024, 520), (16, 4096, 1032)],
     "decode_direct": [(1, 352, 257), (7, 1024, 520), (16, 4096, 1000), (64, 512, 72)],
