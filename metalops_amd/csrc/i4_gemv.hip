@@ -512,7 +512,7 @@ size_t i4_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs, int 
     const I4GemvCfg c = i4_gemv_config(K, N, gs, wb == 4 ? 32 : 16);
     const int64_t tc = 16 * c.nc;
     size_t need = c.S == 1 ? 0 : COUNTER_BYTES + (size_t)((N + tc - 1) / tc) * c.S * M * tc * sizeof(float);
-    if (M <= 16 && wb == 4 && K % 32 == 0 && gs % 32 == 0 && N % 128 == 0)
+    if (M <= 32 && wb == 4 && K % 32 == 0 && gs % 32 == 0 && N % 128 == 0)
         need = std::max(need, i4_gemv1_workspace_bytes(M, K, N, gs));
     return need;
 }

@@ -71,16 +71,21 @@ struct I4Gemv1Args {
 constexpr int I1_SZSLOT = 1024; // scale/zero bytes per group (one 16-byte-per-lane copy)
 constexpr int I1_XSTEP = 1024;  // MR: a step's activations, 16 rows x 32 halves, after its weights
 
-// MR (M = 2..16): each ring slot also holds the step's activation block (one
-// more 16-byte-per-lane copy per step: lane -> row min(l/4, M-1), 8 halves
-// 8(l%4)..), lane (c, g) feeds activation row c into the MFMAs, and the four
-// output rows 4g..4g+3 of each column are all live.
-template <int SZ, int ACT, bool XL, bool MR>
-__global__ void __launch_bounds__(I1_W * 64, 2)
+// RB = 0: M == 1.  RB = 1, 2 (the MR forms, M = 2..16 and 17..32): each ring
+// slot also holds the step's activation blocks of 16 rows (one more
+// 16-byte-per-lane copy per block and step: lane -> row min(16 rb + l/4, M-1),
+// 8 halves 8(l%4)..), lane (c, g) feeds activation row 16 rb + c into block rb's
+// MFMAs (the B operand is built once for all blocks), and the four output rows
+// 4g..4g+3 of each column are all live.  RB = 2 runs one workgroup per CU (its
+// registers fill the SIMDs).
+template <int SZ, int ACT, bool XL, int RB>
+__global__ void __launch_bounds__(I1_W * 64, RB == 2 ? 1 : 2)
 i4_gemv1_kernel(I4Gemv1Args a) {
-    constexpr int NR = MR ? 4 : 1;               // output rows per lane
-    constexpr int NCOPY = MR ? 3 : 2;            // copies per step
-    constexpr int STEPB = I1_STEP + (MR ? I1_XSTEP : 0);   // ring slot bytes
+    constexpr bool MR = RB > 0;
+    constexpr int NB = MR ? RB : 1;              // row blocks
+    constexpr int NR = MR ? 4 : 1;               // output rows per lane and block
+    constexpr int NCOPY = 2 + (MR ? RB : 0);     // copies per step
+    constexpr int STEPB = I1_STEP + (MR ? RB * I1_XSTEP : 0);   // ring slot bytes
     constexpr int ESZ = SZ == DT_F32 ? 4 : 2;
     constexpr int SLOT = I1_SZSLOT;
     constexpr int PPR = I1_TC * ESZ / 16;        // 16-byte pieces per scale (or zero) row
@@ -105,11 +110,13 @@ i4_gemv1_kernel(I4Gemv1Args a) {
     uint8_t *const xs = wl + I1_R * STEPB;
     uint8_t *const szs = xs + (MR ? 0 : I1_XB);
 
-    float acc[8][NR];
+    float acc[NB][8][NR];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int rb = 0; rb < NB; ++rb)
 #pragma unroll
-        for (int i = 0; i < NR; ++i) acc[j][i] = 0.f;
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int i = 0; i < NR; ++i) acc[rb][j][i] = 0.f;
 
     if (ns > 0) {
         // ---- scale/zero rows of the wave's groups, then its activations ----
@@ -137,7 +144,11 @@ i4_gemv1_kernel(I4Gemv1Args a) {
 
         // ---- weight steps ----
         const uint8_t *wsrc = a.P + ((int64_t)s_begin * 16 + (lane >> 3)) * N + col0 + 16 * (lane & 7);
-        const _Float16 *xsrc = a.X + (int64_t)min(lane >> 2, a.M - 1) * a.ldx + (int64_t)s_begin * 32 + 8 * (lane & 3);
+        const _Float16 *xsrc[NB];
+#pragma unroll
+        for (int rb = 0; rb < NB; ++rb)
+            xsrc[rb] = a.X + (int64_t)min(16 * rb + (lane >> 2), a.M - 1) * a.ldx + (int64_t)s_begin * 32 +
+                       8 * (lane & 3);
         auto issue = [&](int k) {                     // step k of the range into slot k % R
             const int kk = min(k, ns - 1);
             const uint8_t *src = wsrc + (int64_t)kk * 16 * N;
@@ -146,9 +157,13 @@ i4_gemv1_kernel(I4Gemv1Args a) {
                                              16, 0, 0);
             __builtin_amdgcn_global_load_lds((void *)(src + (int64_t)8 * N),
                                              (__attribute__((address_space(3))) void *)(dst + 1024), 16, 0, 0);
-            if constexpr (MR)
-                __builtin_amdgcn_global_load_lds((void *)(xsrc + kk * 32),
-                                                 (__attribute__((address_space(3))) void *)(dst + I1_STEP), 16, 0, 0);
+            if constexpr (MR) {
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb)
+                    __builtin_amdgcn_global_load_lds((void *)(xsrc[rb] + kk * 32),
+                                                     (__attribute__((address_space(3))) void *)(dst + I1_STEP + I1_XSTEP * rb),
+                                                     16, 0, 0);
+            }
         };
 #pragma unroll
         for (int k = 0; k < I1_R - 1; ++k) issue(k);
@@ -159,9 +174,14 @@ i4_gemv1_kernel(I4Gemv1Args a) {
         const half8_t ew = bitcast<half8_t>(uint4_t{0x3C003C00u, 0x4C004C00u, 0x3C003C00u, 0x4C004C00u});
         const half2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
         const float4_t zf = {0.f, 0.f, 0.f, 0.f};
-        float4_t P[8], Cc = zf, Sx = zf;
+        float4_t P[NB][8], Cc[NB], Sx[NB];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) P[j] = zf;
+        for (int rb = 0; rb < NB; ++rb) {
+            Cc[rb] = zf;
+            Sx[rb] = zf;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) P[rb][j] = zf;
+        }
 
         auto flush = [&](int gl) {
             const lds_u8 *sl = lds_ptr(lds_addr(szs + gl * SLOT));
@@ -191,32 +211,40 @@ i4_gemv1_kernel(I4Gemv1Args a) {
                 }
             }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int rb = 0; rb < NB; ++rb) {
 #pragma unroll
-                for (int i = 0; i < NR; ++i) {
-                    const float tq = __builtin_fmaf(-zv[j], Sx[i], P[j][i] + Cc[i]);
-                    acc[j][i] = __builtin_fmaf(sv[j], tq, acc[j][i]);
+                for (int j = 0; j < 8; ++j) {
+#pragma unroll
+                    for (int i = 0; i < NR; ++i) {
+                        const float tq = __builtin_fmaf(-zv[j], Sx[rb][i], P[rb][j][i] + Cc[rb][i]);
+                        acc[rb][j][i] = __builtin_fmaf(sv[j], tq, acc[rb][j][i]);
+                    }
+                    P[rb][j] = zf;
                 }
-                P[j] = zf;
+                Cc[rb] = zf;
+                Sx[rb] = zf;
             }
-            Cc = zf;
-            Sx = zf;
         };
 
         for (int k = 0; k < ns; ++k) {
             issue(k + I1_R - 1);
             wait_vmcnt<(I1_R - 1) * NCOPY>();      // step k (and everything older) landed
-            // x' for this step: elements 8g..8g+7 of the step (of row c with MR).
-            const uint4_t xv = *(const __attribute__((address_space(3))) uint4_t *)(lds_ptr(lds_addr(
-                MR ? ring + (k % I1_R) * STEPB + I1_STEP + 64 * c + 16 * g : xs + k * 64 + 16 * g)));
-            const uint32_t x02 = __builtin_amdgcn_perm(xv[1], xv[0], 0x05040100u);     // x0, x2
-            const uint32_t x13 = __builtin_amdgcn_perm(xv[1], xv[0], 0x07060302u);     // x1, x3
-            const uint32_t x46 = __builtin_amdgcn_perm(xv[3], xv[2], 0x05040100u);     // x4, x6
-            const uint32_t x57 = __builtin_amdgcn_perm(xv[3], xv[2], 0x07060302u);     // x5, x7
-            const half8_t xq = bitcast<half8_t>(uint4_t{x02, bitcast<uint32_t>(bitcast<half2_t>(x13) * s16),
-                                                        x46, bitcast<uint32_t>(bitcast<half2_t>(x57) * s16)});
-            Cc = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq, negc, Cc, 0, 0, 0);
-            Sx = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq, ew, Sx, 0, 0, 0);
+            // x' for this step: elements 8g..8g+7 of the step (of row 16 rb + c with MR).
+            half8_t xq[NB];
+#pragma unroll
+            for (int rb = 0; rb < NB; ++rb) {
+                const uint4_t xv = *(const __attribute__((address_space(3))) uint4_t *)(lds_ptr(lds_addr(
+                    MR ? ring + (k % I1_R) * STEPB + I1_STEP + I1_XSTEP * rb + 64 * c + 16 * g
+                       : xs + k * 64 + 16 * g)));
+                const uint32_t x02 = __builtin_amdgcn_perm(xv[1], xv[0], 0x05040100u);     // x0, x2
+                const uint32_t x13 = __builtin_amdgcn_perm(xv[1], xv[0], 0x07060302u);     // x1, x3
+                const uint32_t x46 = __builtin_amdgcn_perm(xv[3], xv[2], 0x05040100u);     // x4, x6
+                const uint32_t x57 = __builtin_amdgcn_perm(xv[3], xv[2], 0x07060302u);     // x5, x7
+                xq[rb] = bitcast<half8_t>(uint4_t{x02, bitcast<uint32_t>(bitcast<half2_t>(x13) * s16),
+                                                  x46, bitcast<uint32_t>(bitcast<half2_t>(x57) * s16)});
+                Cc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb], negc, Cc[rb], 0, 0, 0);
+                Sx[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb], ew, Sx[rb], 0, 0, 0);
+            }
             // Byte rows 4g..4g+3, columns 8c..8c+7.
             const lds_u8 *rs = lds_ptr(lds_addr(ring + (k % I1_R) * STEPB + (4 * g) * I1_TC + 8 * c));
             u32x2 r[4];
@@ -232,7 +260,9 @@ i4_gemv1_kernel(I4Gemv1Args a) {
                 const uint32_t p23 = __builtin_amdgcn_perm(r[3][h], r[2][h], sel);
                 const uint4_t bq = {and_or(p01, mlo, c64), and_or(p01, mhi, c64),
                                     and_or(p23, mlo, c64), and_or(p23, mhi, c64)};
-                P[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq, bitcast<half8_t>(bq), P[j], 0, 0, 0);
+#pragma unroll
+                for (int rb = 0; rb < NB; ++rb)
+                    P[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb], bitcast<half8_t>(bq), P[rb][j], 0, 0, 0);
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");     // slot reads done before its refill
             const int sg = s_begin + k;
@@ -241,41 +271,52 @@ i4_gemv1_kernel(I4Gemv1Args a) {
         wait_vmcnt<0>();
     }
 
-    // ---- ordered sum over the waves ----
+    // ---- ordered sum over the waves, one row block at a time ----
     // Output v = row * 128 + column of the tile, rows < M (row 0 only for M == 1).
     constexpr int ROWS = MR ? 16 : 1;
     const int nout = (MR ? a.M : 1) * I1_TC;
-    __syncthreads();
     float *red = (float *)smem;                   // [8 waves][ROWS][128]
+    auto y_at = [&](int v) -> _Float16 & { return a.Y[(int64_t)(v / I1_TC) * a.ldy + col0 + v % I1_TC]; };
+    float *part = a.part + ((int64_t)t * a.S + sp) * nout;
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-        const int row = MR ? 4 * g + i : 0;
-        if (MR ? row < a.M : g == 0) {
+    for (int rb = 0; rb < NB; ++rb) {
+        __syncthreads();                          // ring reads (or the previous block's sums) done
 #pragma unroll
-            for (int j = 0; j < 8; ++j) red[(wave * ROWS + row) * I1_TC + 8 * c + j] = acc[j][i];
+        for (int i = 0; i < NR; ++i) {
+            const int row = MR ? 4 * g + i : 0;
+            if (MR ? 16 * rb + row < a.M : g == 0) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) red[(wave * ROWS + row) * I1_TC + 8 * c + j] = acc[rb][j][i];
+            }
+        }
+        __syncthreads();
+        const int nv = (MR ? min(16, a.M - 16 * rb) : 1) * I1_TC;
+        for (int v = tid; v < nv; v += I1_W * 64) {
+            float sum = 0.f;
+#pragma unroll
+            for (int w = 0; w < I1_W; ++w) sum += red[w * ROWS * I1_TC + v];
+            const int vo = 16 * rb * I1_TC + v;
+            if (a.S == 1) y_at(vo) = (_Float16)activate<ACT>(sum);
+            else if (XL) part[vo] = sum;          // stays in the XCD's L2
+            else __hip_atomic_store(part + vo, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+    if (a.S == 1) return;
+    // Split K: once this workgroup's partial is stored, one lane takes a ticket;
+    // the workgroup that draws the last sums every split's partial in split
+    // order.  XL: the partials were plain stores into this XCD's L2 (every split
+    // of the tile runs here, which the 64-bit ticket verifies; a violation
+    // writes NaN) and are read back through the L2.  Otherwise they went out
+    // write-through (agent-scope atomic stores) and come back with L2-bypassing
+    // loads.
+    wait_vmcnt<0>();
     __syncthreads();
-    auto wave_sum = [&](int v) {
-        float sum = 0.f;
-#pragma unroll
-        for (int w = 0; w < I1_W; ++w) sum += red[w * ROWS * I1_TC + v];
-        return sum;
-    };
-    auto y_at = [&](int v) -> _Float16 & { return a.Y[(int64_t)(v / I1_TC) * a.ldy + col0 + v % I1_TC]; };
-    if (a.S == 1) {
-        for (int v = tid; v < nout; v += I1_W * 64) y_at(v) = (_Float16)activate<ACT>(wave_sum(v));
-        return;
-    }
-    float *part = a.part + ((int64_t)t * a.S + sp) * nout;
+    uint32_t *last_flag = (uint32_t *)smem;
+    const float *base = a.part + (int64_t)t * a.S * nout;
     if constexpr (XL) {
         // Ticket slots: 64-bit, 4096 per linear-id class mod 8 (one XCD each).
         uint64_t *cnt = (uint64_t *)a.counters + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
         const uint32_t xcc = xcc_id();
-        for (int v = tid; v < nout; v += I1_W * 64) part[v] = wave_sum(v);
-        wait_vmcnt<0>();
-        __syncthreads();
-        uint32_t *last_flag = (uint32_t *)smem;
         if (tid == 0) {
             const uint64_t inc = xcd_ticket_inc(xcc);
             const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -285,7 +326,6 @@ i4_gemv1_kernel(I4Gemv1Args a) {
         __syncthreads();
         const uint32_t lf = *last_flag;
         if (!lf) return;
-        const float *base = a.part + (int64_t)t * a.S * nout;
         for (int v = tid; v < nout; v += I1_W * 64) {
             float sum = 0.f;
             for (int q0 = 0; q0 < a.S; q0 += 8) {
@@ -301,13 +341,6 @@ i4_gemv1_kernel(I4Gemv1Args a) {
         if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
-    // Split K: write-through partial stores, a ticket on the tile's counter, and
-    // the last workgroup sums every split's partial (L2-bypassing loads) in order.
-    for (int v = tid; v < nout; v += I1_W * 64)
-        __hip_atomic_store(part + v, wave_sum(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    wait_vmcnt<0>();
-    __syncthreads();
-    uint32_t *last_flag = (uint32_t *)smem;
     if (tid == 0) {
         const uint32_t prev =
             __hip_atomic_fetch_add(&a.counters[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -315,7 +348,6 @@ i4_gemv1_kernel(I4Gemv1Args a) {
     }
     __syncthreads();
     if (!*last_flag) return;
-    const float *base = a.part + (int64_t)t * a.S * nout;
     for (int v = tid; v < nout; v += I1_W * 64) {
         float sum = 0.f;
         for (int q0 = 0; q0 < a.S; q0 += 8) {
@@ -360,16 +392,17 @@ static I1Cfg i4_gemv1_config(int64_t K, int64_t N, int64_t gs) {
 }
 
 static size_t i1_wave_bytes(int64_t M, const I1Cfg &c) {
-    return M > 1 ? (size_t)I1_R * (I1_STEP + I1_XSTEP) + c.ngr_max * I1_SZSLOT
+    const int rb = M > 16 ? 2 : 1;                // activation blocks per ring slot
+    return M > 1 ? (size_t)I1_R * (I1_STEP + rb * I1_XSTEP) + c.ngr_max * I1_SZSLOT
                  : (size_t)I1_R * I1_STEP + I1_XB + c.ngr_max * I1_SZSLOT;
 }
 
-// 1 <= M <= 16, 4-bit weights, whole 128-column tiles, group size a multiple
+// 1 <= M <= 32, 4-bit weights, whole 128-column tiles, group size a multiple
 // of 32, 16-byte aligned operands (and activation rows), and a split count
 // within bounds.  MCQ4_I4_GEMV1=0 disables it; MCQ4_I4_GEMV1=1 limits it to M == 1.
 bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
                         const void *P, const void *scales, const void *zeros) {
-    int64_t mmax = 16;
+    int64_t mmax = 32;
     if (const char *env = getenv("MCQ4_I4_GEMV1")) {
         if (env[0] == '0') return false;
         if (env[0] == '1') mmax = 1;
@@ -395,7 +428,7 @@ static bool use_xcd_local(int ntiles, int S) {
     return !(env && env[0] == '0') && S > 1 && (ntiles + 7) / 8 <= 4096;
 }
 
-template <int SZ, int ACT, bool XL, bool MR>
+template <int SZ, int ACT, bool XL, int RB>
 static hipError_t launch_i1(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
     const size_t lds = (size_t)I1_W * a.wave_bytes;
     static std::atomic<uint64_t> done{0};
@@ -404,21 +437,22 @@ static hipError_t launch_i1(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)i4_gemv1_kernel<SZ, ACT, XL, MR>,
+        e = hipFuncSetAttribute((const void *)i4_gemv1_kernel<SZ, ACT, XL, RB>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
     const int gx = XL ? (ntiles + 7) / 8 * 8 : ntiles;
-    hipLaunchKernelGGL((i4_gemv1_kernel<SZ, ACT, XL, MR>), dim3(gx, a.S), dim3(I1_W * 64), lds, s, a);
+    hipLaunchKernelGGL((i4_gemv1_kernel<SZ, ACT, XL, RB>), dim3(gx, a.S), dim3(I1_W * 64), lds, s, a);
     return hipGetLastError();
 }
 
 template <int SZ, int ACT>
 static hipError_t launch_i1_xl(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
     const bool xl = use_xcd_local(ntiles, a.S);
-    if (a.M > 1) return xl ? launch_i1<SZ, ACT, true, true>(a, ntiles, s) : launch_i1<SZ, ACT, false, true>(a, ntiles, s);
-    return xl ? launch_i1<SZ, ACT, true, false>(a, ntiles, s) : launch_i1<SZ, ACT, false, false>(a, ntiles, s);
+    if (a.M > 16) return xl ? launch_i1<SZ, ACT, true, 2>(a, ntiles, s) : launch_i1<SZ, ACT, false, 2>(a, ntiles, s);
+    if (a.M > 1) return xl ? launch_i1<SZ, ACT, true, 1>(a, ntiles, s) : launch_i1<SZ, ACT, false, 1>(a, ntiles, s);
+    return xl ? launch_i1<SZ, ACT, true, 0>(a, ntiles, s) : launch_i1<SZ, ACT, false, 0>(a, ntiles, s);
 }
 
 template <int SZ>

@@ -31,6 +31,8 @@ hipError_t launch_i4_generic(const void *X, int x_dt, int64_t ldx, const uint8_t
 bool i4_gemv_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
                        const void *P, const void *scales, const void *zeros, int wb);
 size_t i4_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs, int wb);
+bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
+                        const void *P, const void *scales, const void *zeros);
 hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K,
                           int N, int gs, int act, void *ws, hipStream_t s, int wb);
@@ -75,7 +77,8 @@ int check_kng(int64_t K, int64_t N, int64_t gs) {
 }
 
 // Matmul kernel choice: the MFMA kernels for fp16 activations in the shapes
-// they take (GEMV for M <= 16, GEMM above), the general kernel otherwise.
+// they take (GEMV for M <= 16, and for M <= 32 where the async-copy INT4 GEMV
+// takes the shape; GEMM above), the general kernel otherwise.
 // MCQ4_I4_PATH=generic forces the general kernel (tests, comparisons).
 enum class I4Path { Generic, Gemv, Gemm };
 I4Path i4_path(const void *X, int x_dt, int64_t ldx, const uint8_t *P, const void *s,
@@ -86,6 +89,7 @@ I4Path i4_path(const void *X, int x_dt, int64_t ldx, const uint8_t *P, const voi
     if (x_dt != MCQ4_DTYPE_F16) return I4Path::Generic;
     if (M <= 16) return mcq4::i4_gemv_supported(M, K, N, gs, X, ldx, P, s, z, wb) ? I4Path::Gemv
                                                                                   : I4Path::Generic;
+    if (M <= 32 && wb == 4 && mcq4::i4_gemv1_supported(M, K, N, gs, X, ldx, P, s, z)) return I4Path::Gemv;
     return mcq4::i4_gemm_supported(K, N, gs, X, ldx, P, s, z, Y, ldy) ? I4Path::Gemm
                                                                      : I4Path::Generic;
 }
@@ -97,6 +101,9 @@ size_t ws_bytes(int64_t M, int64_t K, int64_t N, int64_t gs, int x_dt, int wb = 
         return 0;
     if (M <= 16) return mcq4::i4_gemv_workspace_bytes(M, K, N, gs, wb);
     if (K % 32 || gs % 32) return 0;
+    // 17..32 rows take the GEMV or the GEMM depending on alignment: cover both.
+    if (M <= 32 && wb == 4)
+        return std::max(mcq4::i4_gemv_workspace_bytes(M, K, N, gs, wb), mcq4::i4_gemm_workspace_bytes(M, K, N));
     return mcq4::i4_gemm_workspace_bytes(M, K, N);
 }
 

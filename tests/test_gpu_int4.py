@@ -442,6 +442,9 @@ GEMV1_MR_CASES = [
     (2, 4096, 4096, 128, None), (3, 4096, 14336, 128, None), (4, 14336, 4096, 128, None),
     (8, 4096, 1024, 32, None), (9, 2048, 512, 64, 3), (16, 4096, 14336, 128, None),
     (16, 11008, 4096, 128, None), (5, 160, 128, 32, 2), (16, 32, 256, 32, None), (7, 1024, 16384, 128, None),
+    # two 16-row activation blocks (M = 17..32)
+    (17, 4096, 4096, 128, None), (24, 14336, 4096, 128, None), (32, 4096, 14336, 128, None),
+    (20, 2048, 512, 64, 3), (31, 1024, 16384, 128, None), (32, 160, 128, 32, 2), (29, 11008, 1024, 256, None),
 ]
 
 
