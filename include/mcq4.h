@@ -132,7 +132,8 @@ size_t mcq4_matmul_int4_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t
  * native/core_mps.mm:5612-5776): Y[M][ldy] = X[M][ldx] @ dequant(W) with
  * fp32 accumulation; X and Y in x_dtype (F16, BF16 or F32).  fp16 activations
  * with group_size % 32 == 0, K % 32 == 0 and N % 8 == 0 run the MFMA kernels
- * (decode GEMV for M <= 16, prefill GEMM above); every other case runs a
+ * (decode GEMV for M <= 16, and for M <= 32 with N % 128 == 0 and 16-byte
+ * aligned operands; prefill GEMM above); every other case runs a
  * general fp32 kernel.  X needs x_dtype alignment (16 bytes and ldx % 8 == 0
  * for the MFMA kernels; the general kernel is used otherwise), Y x_dtype
  * alignment; ldx >= K, ldy >= N.

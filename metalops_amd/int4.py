@@ -246,7 +246,8 @@ def matmul_int4(
     """``Y = X @ dequant(W_packed, scales, zeros)`` for ``X`` ``[M, K]`` or ``[B, M, K]``.
 
     fp32 accumulation; the result has ``X``'s dtype.  fp16 activations run the
-    MFMA kernels (decode GEMV for M <= 16 rows, prefill GEMM above); fp32 and
+    MFMA kernels (decode GEMV for M <= 16 rows, and up to 32 rows when N is a
+    multiple of 128; prefill GEMM above); fp32 and
     bf16 activations run the general fp32 kernel with the weight rounded to
     ``X``'s dtype first, as the reference builds ``W`` in ``X.dtype``
     (quantization.py:220-239).
