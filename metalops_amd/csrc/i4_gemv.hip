@@ -502,17 +502,17 @@ bool i4_gemv_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *
 
 size_t i4_gemv1_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs);
 bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
-                        const void *P, const void *scales, const void *zeros);
+                        const void *P, const void *scales, const void *zeros, int wb);
 hipError_t launch_i4_gemv1(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
                            const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K, int N, int gs,
-                           int act, void *ws, hipStream_t s);
+                           int act, void *ws, hipStream_t s, int wb);
 
 // Covers both decode kernels (i4_gemv1 when it applies, this one otherwise).
 size_t i4_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs, int wb) {
     const I4GemvCfg c = i4_gemv_config(K, N, gs, wb == 4 ? 32 : 16);
     const int64_t tc = 16 * c.nc;
     size_t need = c.S == 1 ? 0 : COUNTER_BYTES + (size_t)((N + tc - 1) / tc) * c.S * M * tc * sizeof(float);
-    if (M <= 32 && wb == 4 && K % 32 == 0 && gs % 32 == 0 && N % 128 == 0)
+    if (M <= (wb == 4 ? 32 : 16) && K % 32 == 0 && gs % 32 == 0 && N % 128 == 0)
         need = std::max(need, i4_gemv1_workspace_bytes(M, K, N, gs));
     return need;
 }
@@ -569,9 +569,9 @@ hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, cons
                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K,
                           int N, int gs, int act, void *ws, hipStream_t s, int wb) {
     const int ks = wb == 4 ? 32 : 16;
-    // 4-bit: the async-copy GEMV (i4_gemv1.hip) when its shape rules hold.
-    if (wb == 4 && ldx >= K && i4_gemv1_supported(M, K, N, gs, X, ldx, P, scales, zeros))
-        return launch_i4_gemv1(X, ldx, P, scales, zeros, sz_dt, Y, ldy, M, K, N, gs, act, ws, s);
+    // The async-copy GEMV (i4_gemv1.hip) when its shape rules hold.
+    if (ldx >= K && i4_gemv1_supported(M, K, N, gs, X, ldx, P, scales, zeros, wb))
+        return launch_i4_gemv1(X, ldx, P, scales, zeros, sz_dt, Y, ldy, M, K, N, gs, act, ws, s, wb);
     const I4GemvCfg c = i4_gemv_config(K, N, gs, ks);
     I4GemvArgs a;
     a.X = X; a.ldx = ldx; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y; a.ldy = ldy;

@@ -39,6 +39,12 @@
 //     loads) and the 64-bit ticket verifies the placement (a violation writes
 //     NaN rather than a wrong sum).  Otherwise agent-scope stores and loads, as
 //     in the general INT4 GEMV.  Store act(sum) as fp16.
+//
+// Int8 weights (WB = 8, W int8 [K][N], M <= 16): a step is 32 byte rows (4 KiB,
+// four copies), lane (c, g) reads byte rows 8g..8g+7, the K order is natural,
+// x' = x, and the B pair of rows 2p, 2p+1 is one v_perm_b32 and one xor with
+// 0x64806480: fp16 1152 + q exactly (q + 128 in the low byte).  C uses -1152
+// and S ones.
 #include <algorithm>
 #include <atomic>
 #include <stdlib.h>
@@ -49,7 +55,7 @@ namespace mcq4 {
 
 constexpr int I1_W = 8;          // waves per workgroup
 constexpr int I1_TC = 128;       // tile columns
-constexpr int I1_STEP = 2048;    // bytes per step and tile (16 byte rows x 128)
+constexpr int I1_STEP = 2048;    // 4-bit weight bytes per step and tile (16 byte rows x 128)
 constexpr int I1_R = 3;          // ring slots (steps) per wave
 constexpr int I1_XB = 1024;      // activation bytes per wave (16 steps)
 constexpr int I1_SMAX = 16;      // K splits at most
@@ -78,14 +84,17 @@ constexpr int I1_XSTEP = 1024;  // MR: a step's activations, 16 rows x 32 halves
 // MFMAs (the B operand is built once for all blocks), and the four output rows
 // 4g..4g+3 of each column are all live.  RB = 2 runs one workgroup per CU (its
 // registers fill the SIMDs).
-template <int SZ, int ACT, bool XL, int RB>
+template <int SZ, int ACT, bool XL, int RB, int WB>
 __global__ void __launch_bounds__(I1_W * 64, RB == 2 ? 1 : 2)
 i4_gemv1_kernel(I4Gemv1Args a) {
+    static_assert(WB == 4 || (WB == 8 && RB < 2), "int8 form covers M <= 16");
     constexpr bool MR = RB > 0;
     constexpr int NB = MR ? RB : 1;              // row blocks
     constexpr int NR = MR ? 4 : 1;               // output rows per lane and block
-    constexpr int NCOPY = 2 + (MR ? RB : 0);     // copies per step
-    constexpr int STEPB = I1_STEP + (MR ? RB * I1_XSTEP : 0);   // ring slot bytes
+    constexpr int WROWS = WB == 4 ? 16 : 32;     // weight byte rows per step
+    constexpr int STEPW = WROWS * I1_TC;         // weight bytes per step
+    constexpr int NCOPY = WROWS / 8 + (MR ? RB : 0);     // copies per step
+    constexpr int STEPB = STEPW + (MR ? RB * I1_XSTEP : 0);   // ring slot bytes
     constexpr int ESZ = SZ == DT_F32 ? 4 : 2;
     constexpr int SLOT = I1_SZSLOT;
     constexpr int PPR = I1_TC * ESZ / 16;        // 16-byte pieces per scale (or zero) row
@@ -143,7 +152,7 @@ i4_gemv1_kernel(I4Gemv1Args a) {
         }
 
         // ---- weight steps ----
-        const uint8_t *wsrc = a.P + ((int64_t)s_begin * 16 + (lane >> 3)) * N + col0 + 16 * (lane & 7);
+        const uint8_t *wsrc = a.P + ((int64_t)s_begin * WROWS + (lane >> 3)) * N + col0 + 16 * (lane & 7);
         const _Float16 *xsrc[NB];
 #pragma unroll
         for (int rb = 0; rb < NB; ++rb)
@@ -151,17 +160,17 @@ i4_gemv1_kernel(I4Gemv1Args a) {
                        8 * (lane & 3);
         auto issue = [&](int k) {                     // step k of the range into slot k % R
             const int kk = min(k, ns - 1);
-            const uint8_t *src = wsrc + (int64_t)kk * 16 * N;
+            const uint8_t *src = wsrc + (int64_t)kk * WROWS * N;
             uint8_t *dst = ring + (k % I1_R) * STEPB;
-            __builtin_amdgcn_global_load_lds((void *)src, (__attribute__((address_space(3))) void *)dst,
-                                             16, 0, 0);
-            __builtin_amdgcn_global_load_lds((void *)(src + (int64_t)8 * N),
-                                             (__attribute__((address_space(3))) void *)(dst + 1024), 16, 0, 0);
+#pragma unroll
+            for (int q = 0; q < WROWS / 8; ++q)           // byte rows 8q..8q+7
+                __builtin_amdgcn_global_load_lds((void *)(src + (int64_t)8 * q * N),
+                                                 (__attribute__((address_space(3))) void *)(dst + 1024 * q), 16, 0, 0);
             if constexpr (MR) {
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb)
                     __builtin_amdgcn_global_load_lds((void *)(xsrc[rb] + kk * 32),
-                                                     (__attribute__((address_space(3))) void *)(dst + I1_STEP + I1_XSTEP * rb),
+                                                     (__attribute__((address_space(3))) void *)(dst + STEPW + I1_XSTEP * rb),
                                                      16, 0, 0);
             }
         };
@@ -170,8 +179,10 @@ i4_gemv1_kernel(I4Gemv1Args a) {
 
         const uint32_t c64 = opaque_vgpr(0x64006400u);
         const uint32_t mlo = opaque_sgpr(0x000F000Fu), mhi = opaque_sgpr(0x00F000F0u);
-        const half8_t negc = bitcast<half8_t>(uint4_t{0xE400E400u, 0xE400E400u, 0xE400E400u, 0xE400E400u});
-        const half8_t ew = bitcast<half8_t>(uint4_t{0x3C003C00u, 0x4C004C00u, 0x3C003C00u, 0x4C004C00u});
+        constexpr uint32_t NEGC = WB == 4 ? 0xE400E400u : 0xE480E480u;     // -1024 / -1152
+        constexpr uint32_t EW1 = WB == 4 ? 0x4C004C00u : 0x3C003C00u;      // 16 / 1
+        const half8_t negc = bitcast<half8_t>(uint4_t{NEGC, NEGC, NEGC, NEGC});
+        const half8_t ew = bitcast<half8_t>(uint4_t{0x3C003C00u, EW1, 0x3C003C00u, EW1});
         const half2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
         const float4_t zf = {0.f, 0.f, 0.f, 0.f};
         float4_t P[NB][8], Cc[NB], Sx[NB];
@@ -234,8 +245,14 @@ i4_gemv1_kernel(I4Gemv1Args a) {
 #pragma unroll
             for (int rb = 0; rb < NB; ++rb) {
                 const uint4_t xv = *(const __attribute__((address_space(3))) uint4_t *)(lds_ptr(lds_addr(
-                    MR ? ring + (k % I1_R) * STEPB + I1_STEP + I1_XSTEP * rb + 64 * c + 16 * g
+                    MR ? ring + (k % I1_R) * STEPB + STEPW + I1_XSTEP * rb + 64 * c + 16 * g
                        : xs + k * 64 + 16 * g)));
+                if constexpr (WB == 8) {
+                    xq[rb] = bitcast<half8_t>(xv);
+                    Cc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb], negc, Cc[rb], 0, 0, 0);
+                    Sx[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb], ew, Sx[rb], 0, 0, 0);
+                    continue;
+                }
                 const uint32_t x02 = __builtin_amdgcn_perm(xv[1], xv[0], 0x05040100u);     // x0, x2
                 const uint32_t x13 = __builtin_amdgcn_perm(xv[1], xv[0], 0x07060302u);     // x1, x3
                 const uint32_t x46 = __builtin_amdgcn_perm(xv[3], xv[2], 0x05040100u);     // x4, x6
@@ -245,21 +262,29 @@ i4_gemv1_kernel(I4Gemv1Args a) {
                 Cc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb], negc, Cc[rb], 0, 0, 0);
                 Sx[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb], ew, Sx[rb], 0, 0, 0);
             }
-            // Byte rows 4g..4g+3, columns 8c..8c+7.
-            const lds_u8 *rs = lds_ptr(lds_addr(ring + (k % I1_R) * STEPB + (4 * g) * I1_TC + 8 * c));
-            u32x2 r[4];
+            // Byte rows (WROWS/4) g .. +WROWS/4-1, columns 8c..8c+7.
+            constexpr int LR = WROWS / 4;
+            const lds_u8 *rs = lds_ptr(lds_addr(ring + (k % I1_R) * STEPB + (LR * g) * I1_TC + 8 * c));
+            u32x2 r[LR];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) r[i] = *(const __attribute__((address_space(3))) u32x2 *)(rs + i * I1_TC);
+            for (int i = 0; i < LR; ++i) r[i] = *(const __attribute__((address_space(3))) u32x2 *)(rs + i * I1_TC);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int h = j >> 2, b = j & 3;
                 // bytes 0 and 2 <- byte b of the first and second row of the pair
                 // (v_perm_b32 selector values 0-3 pick bytes of the second operand, 4-7 of the first)
                 const uint32_t sel = (uint32_t)b | (uint32_t)(4 + b) << 16 | 0x0C000C00u;
-                const uint32_t p01 = __builtin_amdgcn_perm(r[1][h], r[0][h], sel);
-                const uint32_t p23 = __builtin_amdgcn_perm(r[3][h], r[2][h], sel);
-                const uint4_t bq = {and_or(p01, mlo, c64), and_or(p01, mhi, c64),
-                                    and_or(p23, mlo, c64), and_or(p23, mhi, c64)};
+                uint4_t bq;
+                if constexpr (WB == 4) {
+                    const uint32_t p01 = __builtin_amdgcn_perm(r[1][h], r[0][h], sel);
+                    const uint32_t p23 = __builtin_amdgcn_perm(r[3][h], r[2][h], sel);
+                    bq = uint4_t{and_or(p01, mlo, c64), and_or(p01, mhi, c64),
+                                 and_or(p23, mlo, c64), and_or(p23, mhi, c64)};
+                } else {
+#pragma unroll
+                    for (int p = 0; p < 4; ++p)
+                        bq[p] = __builtin_amdgcn_perm(r[2 * p + 1][h], r[2 * p][h], sel) ^ 0x64806480u;
+                }
 #pragma unroll
                 for (int rb = 0; rb < NB; ++rb)
                     P[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb], bitcast<half8_t>(bq), P[rb][j], 0, 0, 0);
@@ -391,28 +416,39 @@ static I1Cfg i4_gemv1_config(int64_t K, int64_t N, int64_t gs) {
     return {(int)spw, (int)S, (int)ngr};
 }
 
-static size_t i1_wave_bytes(int64_t M, const I1Cfg &c) {
+static size_t i1_wave_bytes(int64_t M, const I1Cfg &c, int wb) {
     const int rb = M > 16 ? 2 : 1;                // activation blocks per ring slot
-    return M > 1 ? (size_t)I1_R * (I1_STEP + rb * I1_XSTEP) + c.ngr_max * I1_SZSLOT
-                 : (size_t)I1_R * I1_STEP + I1_XB + c.ngr_max * I1_SZSLOT;
+    const size_t stepw = (size_t)I1_STEP * (wb / 4);
+    return M > 1 ? (size_t)I1_R * (stepw + rb * I1_XSTEP) + c.ngr_max * I1_SZSLOT
+                 : (size_t)I1_R * stepw + I1_XB + c.ngr_max * I1_SZSLOT;
 }
 
-// 1 <= M <= 32, 4-bit weights, whole 128-column tiles, group size a multiple
+// 1 <= M <= 32 with 4-bit weights (wb = 4), M <= 16 with int8 (wb = 8), whole 128-column tiles, group size a multiple
 // of 32, 16-byte aligned operands (and activation rows), and a split count
-// within bounds.  MCQ4_I4_GEMV1=0 disables it; MCQ4_I4_GEMV1=1 limits it to M == 1.
+// within bounds.  MCQ4_I4_GEMV1=0 disables it; =1 limits it to M == 1; =4 to 4-bit
+// weights; =8 lifts the int8 size rule below.
 bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
-                        const void *P, const void *scales, const void *zeros) {
-    int64_t mmax = 32;
+                        const void *P, const void *scales, const void *zeros, int wb) {
+    int64_t mmax = wb == 4 ? 32 : 16;
+    // Int8 weights at M <= 4 on matrices above 32 Mi weights stay on the
+    // register-ring GEMV, measured faster there (graph replays, M = 1:
+    // 14336x4096 14.7 against 16.0 us, 4096x14336 16.7 against 17.0; M = 4
+    // 4096x14336 17.3 against 18.0); this kernel wins below (4096x4096 7.5
+    // against 8.8 us) and from M = 8 (M = 16 4096x14336 20.5 against 22.4).
+    bool i8_size_rule = wb == 8;
     if (const char *env = getenv("MCQ4_I4_GEMV1")) {
         if (env[0] == '0') return false;
         if (env[0] == '1') mmax = 1;
+        if (env[0] == '4' && wb != 4) return false;     // 4-bit only
+        if (env[0] == '8') i8_size_rule = false;        // int8 at every size
     }
+    if (i8_size_rule && M <= 4 && K * N > ((int64_t)1 << 25)) return false;
     if (M < 1 || M > mmax || K < 32 || K % 32 || gs % 32 || N % I1_TC || N / I1_TC > COUNTER_SLOTS) return false;
     if (((uintptr_t)X % 16) || ((uintptr_t)P % 16) || ((uintptr_t)scales % 16) || ((uintptr_t)zeros % 16))
         return false;
     if (M > 1 && (ldx % 8 || ldx < K)) return false;
     const I1Cfg c = i4_gemv1_config(K, N, gs);
-    return c.S <= I1_SMAX && (size_t)I1_W * i1_wave_bytes(M, c) <= 160 * 1024;
+    return c.S <= I1_SMAX && (size_t)I1_W * i1_wave_bytes(M, c, wb) <= 160 * 1024;
 }
 
 size_t i4_gemv1_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs) {
@@ -428,7 +464,7 @@ static bool use_xcd_local(int ntiles, int S) {
     return !(env && env[0] == '0') && S > 1 && (ntiles + 7) / 8 <= 4096;
 }
 
-template <int SZ, int ACT, bool XL, int RB>
+template <int SZ, int ACT, bool XL, int RB, int WB>
 static hipError_t launch_i1(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
     const size_t lds = (size_t)I1_W * a.wave_bytes;
     static std::atomic<uint64_t> done{0};
@@ -437,41 +473,52 @@ static hipError_t launch_i1(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)i4_gemv1_kernel<SZ, ACT, XL, RB>,
+        e = hipFuncSetAttribute((const void *)i4_gemv1_kernel<SZ, ACT, XL, RB, WB>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
     const int gx = XL ? (ntiles + 7) / 8 * 8 : ntiles;
-    hipLaunchKernelGGL((i4_gemv1_kernel<SZ, ACT, XL, RB>), dim3(gx, a.S), dim3(I1_W * 64), lds, s, a);
+    hipLaunchKernelGGL((i4_gemv1_kernel<SZ, ACT, XL, RB, WB>), dim3(gx, a.S), dim3(I1_W * 64), lds, s, a);
     return hipGetLastError();
 }
 
-template <int SZ, int ACT>
+template <int SZ, int ACT, int WB>
 static hipError_t launch_i1_xl(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
     const bool xl = use_xcd_local(ntiles, a.S);
-    if (a.M > 16) return xl ? launch_i1<SZ, ACT, true, 2>(a, ntiles, s) : launch_i1<SZ, ACT, false, 2>(a, ntiles, s);
-    if (a.M > 1) return xl ? launch_i1<SZ, ACT, true, 1>(a, ntiles, s) : launch_i1<SZ, ACT, false, 1>(a, ntiles, s);
-    return xl ? launch_i1<SZ, ACT, true, 0>(a, ntiles, s) : launch_i1<SZ, ACT, false, 0>(a, ntiles, s);
+    if constexpr (WB == 4) {
+        if (a.M > 16)
+            return xl ? launch_i1<SZ, ACT, true, 2, WB>(a, ntiles, s) : launch_i1<SZ, ACT, false, 2, WB>(a, ntiles, s);
+    } else {
+        if (a.M > 16) return hipErrorInvalidValue;
+    }
+    if (a.M > 1) return xl ? launch_i1<SZ, ACT, true, 1, WB>(a, ntiles, s) : launch_i1<SZ, ACT, false, 1, WB>(a, ntiles, s);
+    return xl ? launch_i1<SZ, ACT, true, 0, WB>(a, ntiles, s) : launch_i1<SZ, ACT, false, 0, WB>(a, ntiles, s);
+}
+
+template <int SZ, int WB>
+static hipError_t launch_i1_act(const I4Gemv1Args &a, int ntiles, int act, hipStream_t s) {
+    if (act == ACT_SILU) return launch_i1_xl<SZ, ACT_SILU, WB>(a, ntiles, s);
+    if (act == ACT_GELU) return launch_i1_xl<SZ, ACT_GELU, WB>(a, ntiles, s);
+    return launch_i1_xl<SZ, ACT_NONE, WB>(a, ntiles, s);
 }
 
 template <int SZ>
-static hipError_t launch_i1_act(const I4Gemv1Args &a, int ntiles, int act, hipStream_t s) {
-    if (act == ACT_SILU) return launch_i1_xl<SZ, ACT_SILU>(a, ntiles, s);
-    if (act == ACT_GELU) return launch_i1_xl<SZ, ACT_GELU>(a, ntiles, s);
-    return launch_i1_xl<SZ, ACT_NONE>(a, ntiles, s);
+static hipError_t launch_i1_wb(const I4Gemv1Args &a, int ntiles, int act, int wb, hipStream_t s) {
+    return wb == 8 ? launch_i1_act<SZ, 8>(a, ntiles, act, s) : launch_i1_act<SZ, 4>(a, ntiles, act, s);
 }
 
 hipError_t launch_i4_gemv1(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
                            const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K, int N, int gs,
-                           int act, void *ws, hipStream_t s) {
+                           int act, void *ws, hipStream_t s, int wb) {
+    if (wb != 4 && (wb != 8 || M > 16)) return hipErrorInvalidValue;
     const I1Cfg c = i4_gemv1_config(K, N, gs);
     I4Gemv1Args a;
     a.X = X; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y;
     a.K = K; a.N = N; a.nsteps = K / 32; a.spg = gs / 32; a.spw = c.spw; a.S = c.S;
     a.ngr_max = c.ngr_max;
     a.M = M; a.ldx = ldx; a.ldy = ldy;
-    a.wave_bytes = (int)i1_wave_bytes(M, c);
+    a.wave_bytes = (int)i1_wave_bytes(M, c, wb);
     a.part = nullptr; a.counters = nullptr;
     if (c.S > 1) {
         if (!ws) return hipErrorInvalidValue;
@@ -480,9 +527,9 @@ hipError_t launch_i4_gemv1(const _Float16 *X, int64_t ldx, const uint8_t *P, con
     }
     if ((size_t)I1_W * a.wave_bytes > 160 * 1024) return hipErrorInvalidValue;
     const int ntiles = N / I1_TC;
-    if (sz_dt == DT_F32) return launch_i1_act<DT_F32>(a, ntiles, act, s);
-    if (sz_dt == DT_F16) return launch_i1_act<DT_F16>(a, ntiles, act, s);
-    return launch_i1_act<DT_BF16>(a, ntiles, act, s);
+    if (sz_dt == DT_F32) return launch_i1_wb<DT_F32>(a, ntiles, act, wb, s);
+    if (sz_dt == DT_F16) return launch_i1_wb<DT_F16>(a, ntiles, act, wb, s);
+    return launch_i1_wb<DT_BF16>(a, ntiles, act, wb, s);
 }
 
 }  // namespace mcq4

@@ -32,7 +32,7 @@ bool i4_gemv_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *
                        const void *P, const void *scales, const void *zeros, int wb);
 size_t i4_gemv_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs, int wb);
 bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
-                        const void *P, const void *scales, const void *zeros);
+                        const void *P, const void *scales, const void *zeros, int wb);
 hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K,
                           int N, int gs, int act, void *ws, hipStream_t s, int wb);
@@ -89,7 +89,7 @@ I4Path i4_path(const void *X, int x_dt, int64_t ldx, const uint8_t *P, const voi
     if (x_dt != MCQ4_DTYPE_F16) return I4Path::Generic;
     if (M <= 16) return mcq4::i4_gemv_supported(M, K, N, gs, X, ldx, P, s, z, wb) ? I4Path::Gemv
                                                                                   : I4Path::Generic;
-    if (M <= 32 && wb == 4 && mcq4::i4_gemv1_supported(M, K, N, gs, X, ldx, P, s, z)) return I4Path::Gemv;
+    if (M <= 32 && wb == 4 && mcq4::i4_gemv1_supported(M, K, N, gs, X, ldx, P, s, z, wb)) return I4Path::Gemv;
     return mcq4::i4_gemm_supported(K, N, gs, X, ldx, P, s, z, Y, ldy) ? I4Path::Gemm
                                                                      : I4Path::Generic;
 }

@@ -388,6 +388,47 @@ def test_matmul_int8_fp16(mo, dev, M, K, N, gs, sz):
     _check_rows(Y.float().cpu().numpy(), R.matmul_int8_f32(X.float().numpy(), q, s, z, gs))
 
 
+GEMV1_I8_CASES = [
+    # (M, K, N, gs, steps per wave or None): int8 weights on the async-copy GEMV
+    (1, 4096, 4096, 128, None), (1, 4096, 14336, 128, None), (1, 14336, 4096, 128, None),
+    (1, 4096, 32000, 128, None), (1, 160, 128, 32, 2), (1, 2048, 384, 64, 3),
+    (2, 4096, 4096, 128, None), (5, 11008, 4096, 128, None), (8, 4096, 1024, 32, None),
+    (16, 4096, 14336, 128, None), (16, 14336, 4096, 128, None), (11, 1024, 16384, 256, None),
+]
+
+
+@pytest.mark.parametrize("M,K,N,gs,spw", GEMV1_I8_CASES)
+@pytest.mark.parametrize("sz", [R.F16, R.BF16, R.F32])
+def test_gemv1_int8(mo, dev, monkeypatch, M, K, N, gs, spw, sz):
+    """Int8 weights on the async-copy GEMV against the oracle, repeat calls and
+    the agent-scope split exchange (identical bits), strided activations, and
+    the register-ring int8 GEMV."""
+    print(f"gemv1 int8 M={M} K={K} N={N} gs={gs} spw={spw} sz={sz}", flush=True)
+    for k in ("MCQ4_I4_SPW1", "MCQ4_I4_GEMV1", "MCQ4_I4_PATH", "MCQ4_XCD_LOCAL"):
+        monkeypatch.delenv(k, raising=False)
+    if spw is not None:
+        monkeypatch.setenv("MCQ4_I4_SPW1", str(spw))
+    monkeypatch.setenv("MCQ4_I4_GEMV1", "8")            # every size, not only where it is the default
+    q, s, z = _int8_weights(K, N, gs, sz, M + K + N + gs)
+    args = [torch.from_numpy(q).to(dev), torch.from_numpy(s).to(TDT[sz]).to(dev),
+            torch.from_numpy(z).to(TDT[sz]).to(dev)]
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(M * K + 1)).half().to(dev)
+    Yref = R.matmul_int8_f32(X.float().cpu().numpy(), q, s, z, gs)
+    Y = mo.matmul_int8(X, *args, gs)
+    _check_rows(Y.float().cpu().numpy(), Yref)
+    assert torch.equal(mo.matmul_int8(X, *args, gs).view(torch.int16), Y.view(torch.int16))
+    monkeypatch.setenv("MCQ4_XCD_LOCAL", "0")
+    assert torch.equal(mo.matmul_int8(X, *args, gs).view(torch.int16), Y.view(torch.int16))
+    monkeypatch.delenv("MCQ4_XCD_LOCAL")
+    Xw = torch.zeros(M, K + 64, dtype=torch.float16, device=dev)
+    Xw[:, :K] = X
+    assert torch.equal(mo.matmul_int8(Xw[:, :K], *args, gs).view(torch.int16), Y.view(torch.int16))
+    monkeypatch.delenv("MCQ4_I4_GEMV1")                 # default routing
+    _check_rows(mo.matmul_int8(X, *args, gs).float().cpu().numpy(), Yref)
+    monkeypatch.setenv("MCQ4_I4_GEMV1", "4")            # async-copy GEMV for 4-bit weights only
+    _check_rows(mo.matmul_int8(X, *args, gs).float().cpu().numpy(), Yref)
+
+
 @pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
 def test_matmul_int8_other_dtypes(mo, dev, xdt):
     M, K, N, gs = 6, 512, 136, 64
