@@ -1,5 +1,5 @@
-// Decode (M = 1..16) per-group INT4 GEMV on gfx950 with the weight stream in
-// asynchronous global->LDS copies.
+// Decode per-group INT4 (M = 1..32) and INT8 (M = 1..16) GEMV on gfx950 with
+// the weight stream in asynchronous global->LDS copies.
 //
 // Y[M][N] = X[M][K] @ W, W[k][n] = (q - z) * s per (group, column), packed[K/2][N]
 // (byte row k/2: even k in the low nibble), fp16 activations, fp32 sums.  The
