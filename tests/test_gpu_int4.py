@@ -573,3 +573,19 @@ def test_decode_random_shapes(mo, dev, M, K, N, gs):
     w, packed, s, z = _quant(mo, dev, K, N, gs, seed=M * 7 + K + N)
     X = torch.randn(M, K, generator=torch.Generator().manual_seed(K + M)).half().to(dev)
     _check_rows(mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy(), _ref(X, packed, s, z, gs))
+
+
+@pytest.mark.parametrize("M,K,N,gs", _random_decode_shapes(12, 2025))
+def test_decode_random_shapes_int8(mo, dev, monkeypatch, M, K, N, gs):
+    """Seeded random int8 decode shapes on the async-copy GEMV (its size rule
+    lifted) and on the default routing, against the oracle."""
+    print(f"random int8 decode M={M} K={K} N={N} gs={gs}", flush=True)
+    monkeypatch.delenv("MCQ4_I4_SPW1", raising=False)
+    q, s, z = _int8_weights(K, N, gs, R.F16, M * 5 + K + N)
+    args = [torch.from_numpy(q).to(dev), torch.from_numpy(s).half().to(dev), torch.from_numpy(z).half().to(dev)]
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(K * 3 + M)).half().to(dev)
+    Yref = R.matmul_int8_f32(X.float().cpu().numpy(), q, s, z, gs)
+    monkeypatch.setenv("MCQ4_I4_GEMV1", "8")
+    _check_rows(mo.matmul_int8(X, *args, gs).float().cpu().numpy(), Yref)
+    monkeypatch.delenv("MCQ4_I4_GEMV1")
+    _check_rows(mo.matmul_int8(X, *args, gs).float().cpu().numpy(), Yref)
