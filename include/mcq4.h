@@ -53,6 +53,17 @@ int mcq4_quantize_q4_0(const float *W, int64_t ldw, int64_t K, int64_t N,
                        uint8_t *blocks, void *stream);
 
 /*
+ * quantize_ggml_q4_0 (quantization.py:307-371) for a weight of any float dtype
+ * (w_dtype MCQ4_DTYPE_F32 / F16 / BF16).  The reference runs every step as a
+ * torch op in the weight's own dtype (quantization.py:335-347): amax, amax/7,
+ * the zero test, x/d, +8 and the rounding are each rounded to w_dtype here as
+ * there; d is then stored as fp16 (:352).  W: [K][ldw] in w_dtype, aligned to
+ * its element size.  For MCQ4_DTYPE_F32 this is mcq4_quantize_q4_0.
+ */
+int mcq4_quantize_q4_0_typed(const void *W, int w_dtype, int64_t ldw, int64_t K, int64_t N,
+                             uint8_t *blocks, void *stream);
+
+/*
  * llama.cpp quantize_row_q4_0_ref scale/rounding rule, emitted in the same
  * [K/32][N][18] layout and nibble order.  No counterpart in the reference: it
  * generates the benchmark configurations (signed scales, q = 0 reachable).
@@ -89,6 +100,26 @@ size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N);
 int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y,
                          int64_t ldy, int64_t M, int64_t K, int64_t N,
                          void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * matmul_ggml_q4_0 for activations of any float dtype (quantization.py:422-454).
+ * x_dtype MCQ4_DTYPE_F16 is mcq4_matmul_q4_0_f16 (the fp16 MFMA kernels, the
+ * semantics of the reference's GPU binding, core_mps.mm:5917-5975).
+ * MCQ4_DTYPE_BF16 / F32 follow the reference's path for those dtypes
+ * (quantization.py:452-454): W dequantized to x_dtype (one rounding of the
+ * exact product), Y = X @ W with fp32 accumulation, Y in x_dtype.  X and Y
+ * aligned to x_dtype; no workspace is needed for them (may be NULL).
+ */
+int mcq4_matmul_q4_0(const void *X, int x_dtype, int64_t ldx, const uint8_t *W, void *Y,
+                     int64_t ldy, int64_t M, int64_t K, int64_t N, void *workspace,
+                     size_t workspace_bytes, void *stream);
+
+/*
+ * Re-reads the library's MCQ4_* test and experiment switches from the
+ * environment (they are read once, at the first launch, and never per call).
+ * No counterpart in the reference.
+ */
+int mcq4_reload_options(void);
 
 /* ---------------------------------------------------------------------------
  * Per-group INT4 (metalcore quantization.py:26-239, Int4Linear :457-613).

@@ -28,10 +28,13 @@ SIGNATURES = {
     "mcq4_status_string": (ctypes.c_char_p, [_int]),
     "mcq4_last_error": (ctypes.c_char_p, []),
     "mcq4_quantize_q4_0": (_int, [_p, _i64, _i64, _i64, _p, _p]),
+    "mcq4_quantize_q4_0_typed": (_int, [_p, _int, _i64, _i64, _i64, _p, _p]),
     "mcq4_quantize_q4_0_llama": (_int, [_p, _i64, _i64, _i64, _p, _p]),
     "mcq4_dequantize_q4_0": (_int, [_p, _i64, _i64, _p, _i64, _int, _p]),
     "mcq4_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "mcq4_matmul_q4_0_f16": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
+    "mcq4_matmul_q4_0": (_int, [_p, _int, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
+    "mcq4_reload_options": (_int, []),
     "mcq4_quantize_int4": (_int, [_p, _int, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "mcq4_dequantize_int4": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _p, _i64, _int, _p]),
     "mcq4_matmul_int4_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _int]),
@@ -78,6 +81,14 @@ lib = _load()
 
 def status_string(status: int) -> str:
     return lib.mcq4_status_string(status).decode()
+
+
+def reload_options() -> None:
+    """Re-read the library's MCQ4_* test switches from the environment.
+
+    The library reads them once, at its first launch, and again only here.
+    """
+    check(lib.mcq4_reload_options(), "mcq4_reload_options")
 
 
 def check(status: int, func: str) -> None:

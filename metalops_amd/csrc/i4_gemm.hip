@@ -423,8 +423,6 @@ static I4GCfg i4_gemm_config(int64_t M, int64_t K, int64_t N) {
     const int64_t t = ((M + c.bm - 1) / c.bm) * tn;
     const int64_t ns = K / 32;
     while (t * c.S < 192 && ns / (c.S * 2) >= 16 && c.S < 16) c.S *= 2;
-    if (const char *env = getenv("MCQ4_I4_GEMM_BM")) c.bm = atoi(env) == 128 ? 128 : 256;
-    if (const char *env = getenv("MCQ4_I4_GEMM_SPLIT")) c.S = std::max(1, std::min(16, atoi(env)));
     if (c.S > ns) c.S = 1;
     return c;
 }

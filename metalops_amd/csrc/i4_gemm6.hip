@@ -349,7 +349,6 @@ static J6Cfg i4_gemm6_config(int64_t M, int64_t K, int64_t N) {
     int S = 1;
     while (t * S * 2 <= 256 && ns / (S * 2) >= 16 && S < 16) S *= 2;
     if (t * S * 2 <= 512 && ns / (S * 2) >= 64 && S < 16) S *= 2;
-    if (const char *env = getenv("MCQ4_I4_GEMM6_SPLIT")) S = std::max(1, std::min(16, atoi(env)));
     if (S > ns) S = 1;
     return {S};
 }
@@ -358,8 +357,7 @@ static J6Cfg i4_gemm6_config(int64_t M, int64_t K, int64_t N) {
 // K % 32, group % 32, 16-byte aligned operands) and 4-byte aligned Y rows.
 // MCQ4_I4_GEMM6=0 disables it.
 bool i4_gemm6_supported(int wb, int sz_dt, int64_t K, int64_t N, int64_t gs, const void *Y, int64_t ldy) {
-    if (const char *env = getenv("MCQ4_I4_GEMM6"))
-        if (env[0] == '0') return false;
+    if (opt_is("MCQ4_I4_GEMM6", '0')) return false;
     return wb == 4 && (sz_dt == DT_F16 || sz_dt == DT_BF16) && N % 128 == 0 && K % 32 == 0 && gs % 32 == 0 &&
            ((uintptr_t)Y % 4) == 0 && ldy % 2 == 0;
 }
@@ -414,8 +412,7 @@ hipError_t launch_i4_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *P, con
         a.partials = (float *)((char *)ws + COUNTER_BYTES);
         // Two splits: summed in the kernel through the XCD's L2 (MCQ4_XCD_LOCAL=0:
         // by the reduction kernel).
-        const char *xl = getenv("MCQ4_XCD_LOCAL");
-        if (c.S == 2 && !(xl && xl[0] == '0') && (a.tiles_m * a.tiles_n + 7) / 8 <= 4096)
+        if (c.S == 2 && !opt_is("MCQ4_XCD_LOCAL", '0') && (a.tiles_m * a.tiles_n + 7) / 8 <= 4096)
             a.tickets = (uint64_t *)ws;
     }
     if (sz_dt == DT_F16) return launch_j6_act<DT_F16>(a, act, s);

@@ -329,17 +329,6 @@ i4_gemv_kernel(I4GemvArgs a) {
     // keeps the cross-XCD exchange to the partials themselves instead of the
     // full-L2 write-back and invalidate that an agent-scope fence costs.
     float *part = a.part + ((int64_t)t * a.S + sp) * M * TC;
-    if (!a.counters) {
-        // Reduction kernel mode: plain stores; the next kernel on the stream sums.
-        for (int v = tid; v < M * TC; v += IW * 64) {
-            const int row = v / TC, cl = v % TC;
-            float sum = 0.f;
-#pragma unroll
-            for (int w = 0; w < IW; ++w) sum += red[(w * 16 + row) * TC + cl];
-            part[v] = sum;
-        }
-        return;
-    }
     if (a.xl) {
         // Every split of this tile runs on this XCD: the partials go through its
         // L2 (plain stores, L1-bypassing loads); the ticket checks the placement.
@@ -421,24 +410,6 @@ i4_gemv_kernel(I4GemvArgs a) {
     if (tid == 0) __hip_atomic_store(&a.counters[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Reduction-kernel mode: sums the S partials of every output in split order
-// and stores act(sum) as fp16 (the kernel boundary orders it after the GEMV).
-template <int ACT>
-__global__ void __launch_bounds__(256) i4_gemv_reduce_kernel(I4GemvArgs a, int tc) {
-    const int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t per_tile = (int64_t)a.M * tc;
-    const int64_t ntiles = (a.N + tc - 1) / tc;
-    if (v >= ntiles * per_tile) return;
-    const int64_t t = v / per_tile;
-    const int e = (int)(v % per_tile);
-    const int row = e / tc, cl = e % tc;
-    if (t * tc + cl >= a.N) return;
-    const float *p = a.part + t * a.S * per_tile + e;
-    float sum = 0.f;
-    for (int q = 0; q < a.S; ++q) sum += p[(int64_t)q * per_tile];
-    a.Y[(int64_t)row * a.ldy + t * tc + cl] = (_Float16)activate<ACT>(sum);
-}
-
 struct I4GemvCfg {
     int nc, iw, spw, S;
 };
@@ -452,11 +423,9 @@ struct I4GemvCfg {
 // wave's steps must fit its I4V_GMAX scale/zero slots: a range of spw steps
 // touches at most ceil(spw/spg) + 1 groups, or exactly spw/spg when spw is a
 // multiple of spg (every range then starts on a group boundary).
-// Experiments: MCQ4_I4_MODE=narrow selects 64-column tiles of 16 waves with
-// the whole K in one workgroup where the slots allow (64-byte row pieces read
-// at about half the bandwidth of 128-byte pieces on MI355X, so it is slower);
-// MCQ4_I4_SPW / MCQ4_I4_SPLIT force the steps per wave / split count;
-// MCQ4_I4_RED=kernel sums splits in a second kernel instead of the ticket.
+// (64-column tiles of 16 waves with the whole K in one workgroup were measured
+// slower: 64-byte row pieces read at about half the bandwidth of 128-byte
+// pieces on MI355X.)
 static I4GemvCfg i4_gemv_config(int64_t K, int64_t N, int64_t gs, int ks) {
     const int64_t nsteps = K / ks, spg = gs / ks;
     const int64_t loose = (I4V_GMAX - 1) * spg;          // any alignment
@@ -464,27 +433,17 @@ static I4GemvCfg i4_gemv_config(int64_t K, int64_t N, int64_t gs, int ks) {
         if (w <= loose) return w;
         return std::min<int64_t>((w + spg - 1) / spg * spg, I4V_GMAX * spg);
     };
-    const char *mode = getenv("MCQ4_I4_MODE");
-    const bool narrow = mode && mode[0] == 'n';
-    const bool wide = !narrow;
-    const int nc = narrow ? 4 : 8;
-    const int64_t iw = narrow ? 16 : 4;
+    const int nc = 8;
+    const int64_t iw = 4;
     const int64_t ntiles = (N + 16 * nc - 1) / (16 * nc);
-    int64_t S;
-    if (wide) {
-        S = std::max<int64_t>(1, std::min<int64_t>(I4V_SMAX, 256 / ntiles));
-        S = std::max(S, (nsteps + iw * 32 - 1) / (iw * 32));
+    int64_t S = std::max<int64_t>(1, std::min<int64_t>(I4V_SMAX, 256 / ntiles));
+    S = std::max(S, (nsteps + iw * 32 - 1) / (iw * 32));
+    {
         int64_t spw = (nsteps + iw * S - 1) / (iw * S);
-        if (const char *env = getenv("MCQ4_I4_SPW")) spw = atoi(env);
         spw = std::max<int64_t>(spw, (nsteps + iw * I4V_SMAX - 1) / (iw * I4V_SMAX));
         spw = fit(std::min<int64_t>(std::max<int64_t>(spw, 2), 32));
         S = (nsteps + iw * spw - 1) / (iw * spw);
-    } else {
-        S = 1;
-        while ((nsteps + iw * S - 1) / (iw * S) > fit((nsteps + iw * S - 1) / (iw * S)) && S < I4V_SMAX)
-            S *= 2;
     }
-    if (const char *env = getenv("MCQ4_I4_SPLIT")) S = std::max(1, std::min(I4V_SMAX, atoi(env)));
     int64_t spw = fit((nsteps + iw * S - 1) / (iw * S));
     S = (nsteps + iw * spw - 1) / (iw * spw);
     return {nc, (int)iw, (int)spw, (int)S};
@@ -547,14 +506,6 @@ static hipError_t launch_gemv_sz(const I4GemvArgs &a, int ntiles, int act, hipSt
     else if (act == ACT_GELU) e = launch_one<SZ, ACT_GELU, D, NC, WB, IW>(a, grid, s);
     else e = launch_one<SZ, ACT_NONE, D, NC, WB, IW>(a, grid, s);
     if (e != hipSuccess) return e;
-    if (a.S > 1 && !a.counters) {
-        constexpr int tc = I4vShape<NC, IW>::TC;
-        const int64_t n = (int64_t)ntiles * a.M * tc;
-        const dim3 rg((unsigned)((n + 255) / 256));
-        if (act == ACT_SILU) hipLaunchKernelGGL((i4_gemv_reduce_kernel<ACT_SILU>), rg, dim3(256), 0, s, a, tc);
-        else if (act == ACT_GELU) hipLaunchKernelGGL((i4_gemv_reduce_kernel<ACT_GELU>), rg, dim3(256), 0, s, a, tc);
-        else hipLaunchKernelGGL((i4_gemv_reduce_kernel<ACT_NONE>), rg, dim3(256), 0, s, a, tc);
-    }
     return hipGetLastError();
 }
 
@@ -583,17 +534,11 @@ hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, cons
     if (c.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.part = (float *)((char *)ws + COUNTER_BYTES);
-        const char *red = getenv("MCQ4_I4_RED");                   // experiments
-        if (!(red && red[0] == 'k')) a.counters = (uint32_t *)ws;
-        const char *xl = getenv("MCQ4_XCD_LOCAL");
-        a.xl = a.counters && !(xl && xl[0] == '0') && (ntiles + 7) / 8 <= 4096;
+        a.counters = (uint32_t *)ws;
+        a.xl = !opt_is("MCQ4_XCD_LOCAL", '0') && (ntiles + 7) / 8 <= 4096;
     }
-    if (wb == 8) {
-        if (c.nc == 8) return launch_gemv_nc<8, 8, 4>(a, ntiles, sz_dt, act, s);
-        return launch_gemv_nc<4, 8, 16>(a, ntiles, sz_dt, act, s);
-    }
-    if (c.nc == 8) return launch_gemv_nc<8, 4, 4>(a, ntiles, sz_dt, act, s);
-    return launch_gemv_nc<4, 4, 16>(a, ntiles, sz_dt, act, s);
+    if (wb == 8) return launch_gemv_nc<8, 8, 4>(a, ntiles, sz_dt, act, s);
+    return launch_gemv_nc<8, 4, 4>(a, ntiles, sz_dt, act, s);
 }
 
 }  // namespace mcq4

@@ -408,7 +408,7 @@ static I1Cfg i4_gemv1_config(int64_t K, int64_t N, int64_t gs) {
     int64_t S = std::max<int64_t>(1, std::min<int64_t>(I1_SMAX, 256 / std::max<int64_t>(ntiles, 1)));
     S = std::max(S, (nsteps + I1_W * 16 - 1) / (I1_W * 16));
     int64_t spw = (nsteps + I1_W * S - 1) / (I1_W * S);
-    if (const char *env = getenv("MCQ4_I4_SPW1")) spw = atoi(env);
+    if (const char *env = opt("MCQ4_I4_SPW1")) spw = atoi(env);
     spw = std::max<int64_t>(spw, (nsteps + I1_W * I1_SMAX - 1) / (I1_W * I1_SMAX));
     spw = std::min<int64_t>(std::max<int64_t>(spw, 2), 16);
     S = (nsteps + I1_W * spw - 1) / (I1_W * spw);
@@ -436,7 +436,7 @@ bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void 
     // 4096x14336 17.3 against 18.0); this kernel wins below (4096x4096 7.5
     // against 8.8 us) and from M = 8 (M = 16 4096x14336 20.5 against 22.4).
     bool i8_size_rule = wb == 8;
-    if (const char *env = getenv("MCQ4_I4_GEMV1")) {
+    if (const char *env = opt("MCQ4_I4_GEMV1")) {
         if (env[0] == '0') return false;
         if (env[0] == '1') mmax = 1;
         if (env[0] == '4' && wb != 4) return false;     // 4-bit only
@@ -460,8 +460,7 @@ size_t i4_gemv1_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs) {
 // The XCD-local exchange (default; MCQ4_XCD_LOCAL=0 selects the agent-scope
 // one) needs K split and at most 4096 tiles per class of the padded grid.
 static bool use_xcd_local(int ntiles, int S) {
-    const char *env = getenv("MCQ4_XCD_LOCAL");
-    return !(env && env[0] == '0') && S > 1 && (ntiles + 7) / 8 <= 4096;
+    return !opt_is("MCQ4_XCD_LOCAL", '0') && S > 1 && (ntiles + 7) / 8 <= 4096;
 }
 
 template <int SZ, int ACT, bool XL, int RB, int WB>

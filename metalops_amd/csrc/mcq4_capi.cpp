@@ -13,7 +13,7 @@
 #include <stdio.h>
 
 #include "../../include/mcq4.h"
-#include "q4_gemm4.h"
+#include "q4_prefill.h"
 
 namespace mcq4 {
 hipError_t launch_quantize(bool llama_rule, const float *W, int64_t ldw, int nb, int N,
@@ -29,19 +29,10 @@ hipError_t launch_gemm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float1
 bool gemm2_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
 hipError_t launch_gemm2(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, hipStream_t s);
-hipError_t launch_gemm3(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
-                        int64_t ldy, int M, int K, int N, hipStream_t s);
-bool gemm4_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
-size_t gemm4_workspace_bytes(int64_t M, int64_t K, int64_t N);
-bool gemm5_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
-size_t gemm5_workspace_bytes(int64_t M, int64_t K, int64_t N);
-hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
-                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
-size_t gemm6_workspace_bytes(int64_t M, int64_t K, int64_t N);
-hipError_t launch_gemm5(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
-                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
-hipError_t launch_gemm4(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
-                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
+hipError_t launch_quantize_typed(int w_dtype, const void *W, int64_t ldw, int nb, int N,
+                                 uint8_t *out, hipStream_t s);
+hipError_t launch_q4_xact(const void *X, int x_dt, int64_t ldx, const uint8_t *W, void *Y,
+                          int64_t ldy, int64_t M, int64_t K, int64_t N, hipStream_t s);
 }  // namespace mcq4
 
 namespace {
@@ -67,24 +58,21 @@ constexpr int64_t kMaxDim = (int64_t)1 << 30;  // keeps 32-bit lane offsets safe
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
 // Prefill kernel choice (M > 64).  Default, when N % 128 == 0 and the pointers
-// are 16-byte aligned: the LDS-staged GEMM with two waves per SIMD (q4_gemm6).  Otherwise the
-// async-copy GEMM (q4_gemm2) when its alignment needs hold and the output has
-// at least 128 tiles of 128x256; otherwise the register-staged split-K kernel.
-// MCQ4_GEMM_PATH=sync|async|3|4|5|6 forces one kernel (tests, experiments).
-enum class Prefill { Sync, Async2, Async3, Free4, Staged5, Staged6 };
+// are 16-byte aligned: the LDS-staged GEMM with two waves per SIMD (q4_gemm6).
+// Otherwise the async-copy GEMM (q4_gemm2) when its alignment needs hold and
+// the output has at least 128 tiles of 128x256; otherwise the register-staged
+// split-K kernel.  MCQ4_GEMM_PATH=sync|async|6 forces one kernel (tests).
+enum class Prefill { Sync, Async2, Staged6 };
 Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
                        int64_t N) {
     const bool ok2 = mcq4::gemm2_supported(X, ldx, W, K, N);
-    const bool ok4 = mcq4::gemm4_supported(X, ldx, W, K, N);
-    if (const char *env = getenv("MCQ4_GEMM_PATH")) {
+    const bool ok6 = mcq4::gemm6_supported(X, ldx, W, K, N);
+    if (const char *env = mcq4::opt("MCQ4_GEMM_PATH")) {
         if (env[0] == 's') return Prefill::Sync;
         if (env[0] == 'a' && ok2) return Prefill::Async2;
-        if (env[0] == '3' && ok2) return Prefill::Async3;
-        if (env[0] == '4' && ok4) return Prefill::Free4;
-        if (env[0] == '5' && ok4) return Prefill::Staged5;
-        if (env[0] == '6' && ok4) return Prefill::Staged6;
+        if (env[0] == '6' && ok6) return Prefill::Staged6;
     }
-    if (ok4) return Prefill::Staged6;
+    if (ok6) return Prefill::Staged6;
     if (ok2 && ((M + 127) / 128) * ((N + 255) / 256) >= 128) return Prefill::Async2;
     return Prefill::Sync;
 }
@@ -144,6 +132,22 @@ int mcq4_quantize_q4_0(const float *W, int64_t ldw, int64_t K, int64_t N, uint8_
     return quantize_common(false, W, ldw, K, N, blocks, stream);
 }
 
+int mcq4_quantize_q4_0_typed(const void *W, int w_dtype, int64_t ldw, int64_t K, int64_t N,
+                             uint8_t *blocks, void *stream) {
+    g_err[0] = 0;
+    if (!W || !blocks) return fail(MCQ4_ERR_INVALID_ARG, "null pointer");
+    if (w_dtype != MCQ4_DTYPE_F32 && w_dtype != MCQ4_DTYPE_F16 && w_dtype != MCQ4_DTYPE_BF16)
+        return fail(MCQ4_ERR_INVALID_ARG, "w_dtype must be MCQ4_DTYPE_F32, F16 or BF16");
+    if (int st = check_kn(K, N)) return st;
+    if (ldw < N) return fail(MCQ4_ERR_SHAPE, "ldw (%lld) < N (%lld)", (long long)ldw, (long long)N);
+    if (!aligned(W, w_dtype == MCQ4_DTYPE_F32 ? 4 : 2))
+        return fail(MCQ4_ERR_ALIGNMENT, "W is misaligned for its dtype");
+    if (!aligned(blocks, 2)) return fail(MCQ4_ERR_ALIGNMENT, "blocks must be 2-byte aligned");
+    return hip_status(mcq4::launch_quantize_typed(w_dtype, W, ldw, (int)(K / 32), (int)N, blocks,
+                                                  (hipStream_t)stream),
+                      "quantize launch");
+}
+
 int mcq4_quantize_q4_0_llama(const float *W, int64_t ldw, int64_t K, int64_t N,
                              uint8_t *blocks, void *stream) {
     return quantize_common(true, W, ldw, K, N, blocks, stream);
@@ -169,8 +173,7 @@ size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M <= 0 || K <= 0 || N <= 0 || K % 32) return 0;
     if (M <= 32) return mcq4::skinny_workspace_bytes(M, K, N);
     // The largest of the split-K kernels' needs: an upper bound for any prefill kernel.
-    const size_t pre = std::max({mcq4::gemm_workspace_bytes(M, K, N), mcq4::gemm4_workspace_bytes(M, K, N),
-                                 mcq4::gemm5_workspace_bytes(M, K, N), mcq4::gemm6_workspace_bytes(M, K, N)});
+    const size_t pre = std::max(mcq4::gemm_workspace_bytes(M, K, N), mcq4::gemm6_workspace_bytes(M, K, N));
     // 33..64 rows run either family, depending on the pointers' alignment.
     return M <= 64 ? std::max(pre, mcq4::skinny_workspace_bytes(M, K, N)) : pre;
 }
@@ -198,7 +201,7 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
     hipError_t e;
     // 33..64 rows: q4_gemm6 (flat ~31 us for any M <= 128 on 4096x14336) beats the
     // register-load decode kernel (40-77 us) wherever its alignment rules hold.
-    const bool skinny = M <= 32 || (M <= 64 && !mcq4::gemm4_supported((const _Float16 *)X, ldx, W, K, N));
+    const bool skinny = M <= 32 || (M <= 64 && !mcq4::gemm6_supported((const _Float16 *)X, ldx, W, K, N));
     if (skinny)
         e = mcq4::launch_skinny((const _Float16 *)X, ldx, W, (_Float16 *)Y, ldy, (int)M, (int)K,
                                 (int)N, workspace, (hipStream_t)stream);
@@ -208,14 +211,34 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
         hipStream_t st = (hipStream_t)stream;
         switch (prefill_kernel(x, ldx, W, M, K, N)) {
             case Prefill::Staged6: e = mcq4::launch_gemm6(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
-            case Prefill::Staged5: e = mcq4::launch_gemm5(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
-            case Prefill::Free4: e = mcq4::launch_gemm4(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
-            case Prefill::Async3: e = mcq4::launch_gemm3(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;
             case Prefill::Async2: e = mcq4::launch_gemm2(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;
             default: e = mcq4::launch_gemm(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
         }
     }
     return hip_status(e, "matmul launch");
+}
+
+int mcq4_matmul_q4_0(const void *X, int x_dtype, int64_t ldx, const uint8_t *W, void *Y,
+                     int64_t ldy, int64_t M, int64_t K, int64_t N, void *workspace,
+                     size_t workspace_bytes, void *stream) {
+    if (x_dtype == MCQ4_DTYPE_F16)
+        return mcq4_matmul_q4_0_f16(X, ldx, W, Y, ldy, M, K, N, workspace, workspace_bytes, stream);
+    g_err[0] = 0;
+    if (x_dtype != MCQ4_DTYPE_F32 && x_dtype != MCQ4_DTYPE_BF16)
+        return fail(MCQ4_ERR_INVALID_ARG, "x_dtype must be MCQ4_DTYPE_F32, F16 or BF16");
+    if (!X || !W || !Y) return fail(MCQ4_ERR_INVALID_ARG, "null pointer");
+    if (M <= 0) return fail(MCQ4_ERR_SHAPE, "M (%lld) must be positive", (long long)M);
+    if (int st = check_kn(K, N)) return st;
+    if (M > ((int64_t)65535 * 8)) return fail(MCQ4_ERR_SHAPE, "M (%lld) too large", (long long)M);
+    if (ldx < K) return fail(MCQ4_ERR_SHAPE, "ldx (%lld) < K (%lld)", (long long)ldx, (long long)K);
+    if (ldy < N) return fail(MCQ4_ERR_SHAPE, "ldy (%lld) < N (%lld)", (long long)ldy, (long long)N);
+    const uintptr_t al = x_dtype == MCQ4_DTYPE_F32 ? 4 : 2;
+    if (!aligned(X, al) || !aligned(Y, al))
+        return fail(MCQ4_ERR_ALIGNMENT, "X and Y must be aligned to their dtype");
+    if (!aligned(W, 2)) return fail(MCQ4_ERR_ALIGNMENT, "W must be 2-byte aligned");
+    (void)workspace; (void)workspace_bytes;
+    return hip_status(mcq4::launch_q4_xact(X, x_dtype, ldx, W, Y, ldy, M, K, N, (hipStream_t)stream),
+                      "matmul launch");
 }
 
 }  // extern "C"

@@ -16,6 +16,7 @@
 #include <stdlib.h>
 
 #include "../../include/mcq4.h"
+#include "mcq4_options.h"
 
 namespace mcq4 {
 hipError_t launch_i4_quantize(const void *W, int w_dt, int64_t ldw, int64_t K, int64_t N,
@@ -84,8 +85,7 @@ enum class I4Path { Generic, Gemv, Gemm };
 I4Path i4_path(const void *X, int x_dt, int64_t ldx, const uint8_t *P, const void *s,
                const void *z, const void *Y, int64_t ldy, int64_t M, int64_t K, int64_t N,
                int64_t gs, int wb) {
-    if (const char *env = getenv("MCQ4_I4_PATH"))
-        if (env[0] == 'g') return I4Path::Generic;
+    if (mcq4::opt_is("MCQ4_I4_PATH", 'g')) return I4Path::Generic;
     if (x_dt != MCQ4_DTYPE_F16) return I4Path::Generic;
     if (M <= 16) return mcq4::i4_gemv_supported(M, K, N, gs, X, ldx, P, s, z, wb) ? I4Path::Gemv
                                                                                   : I4Path::Generic;

@@ -1,0 +1,14 @@
+// Test and experiment switches of the library, read from the environment once
+// (at the first launch) and again only on mcq4_reload_options(), never per
+// call.  opt(name) returns the value of a known MCQ4_* variable as it was at
+// the last (re)load, or nullptr when it was unset.
+#pragma once
+
+namespace mcq4 {
+const char *opt(const char *name);
+// True when the named switch is set and its value starts with `c`.
+inline bool opt_is(const char *name, char c) {
+    const char *v = opt(name);
+    return v && v[0] == c;
+}
+}  // namespace mcq4

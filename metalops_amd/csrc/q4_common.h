@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "mcq4_options.h"
+
 namespace mcq4 {
 
 constexpr int QK = 32;       // weights per block

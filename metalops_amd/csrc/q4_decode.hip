@@ -319,12 +319,6 @@ static DecodeCfg decode_config(int64_t M, int64_t K, int64_t N) {
     DecodeCfg c{1, 16, 16, 256};                  // one resident 16-wave workgroup per CU
     if (M > 4 && N >= 8192) c = DecodeCfg{2, 16, 16, 0};
     if (M <= 16 && N / 16 >= 4096) c = DecodeCfg{2, 8, 1, 0};     // lm_head-sized N
-    if (const char *env = getenv("MCQ4_DECODE_CFG")) {  // "NT,WAVES,KS,GRIDCAP" (tuning aid)
-        int nt, w, ks, cap;
-        if (sscanf(env, "%d,%d,%d,%d", &nt, &w, &ks, &cap) == 4 && (nt == 1 || nt == 2) &&
-            (w == 4 || w == 8 || w == 16) && (ks == 1 || ks == 4 || ks == w) && cap >= 0)
-            c = DecodeCfg{nt, w, ks, cap};
-    }
     return c;
 }
 

@@ -242,13 +242,6 @@ static GemmCfg gemm_config(int64_t M, int64_t K, int64_t N) {
     int64_t S = 1;
     while (t * S < 192 && nb / (S * 2) >= 32) S *= 2;
     c.S = (int)S;
-    if (const char *env = getenv("MCQ4_GEMM_CFG")) {  // "BM,BN,S" (tuning aid)
-        int bm, bn, s;
-        if (sscanf(env, "%d,%d,%d", &bm, &bn, &s) == 3 && (bm == 128 || bm == 256) &&
-            (bn == 128 || bn == 256) && s >= 1 && s <= 16) {
-            c.BM = bm; c.BN = bn; c.S = s;
-        }
-    }
     if (((M + c.BM - 1) / c.BM) * ((N + c.BN - 1) / c.BN) > COUNTER_SLOTS) c.S = 1;
     return c;
 }

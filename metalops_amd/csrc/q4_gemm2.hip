@@ -299,7 +299,7 @@ hipError_t launch_gemm2(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
     a.tiles_n = (N + G2_BN - 1) / G2_BN;
     int bm = 256;
     if (((int64_t)(M + 255) / 256) * a.tiles_n < 192) bm = 128;
-    if (const char *env = getenv("MCQ4_GEMM2_BM")) bm = atoi(env) == 128 ? 128 : 256;
+    if (const char *env = opt("MCQ4_GEMM2_BM")) bm = atoi(env) == 128 ? 128 : 256;
     a.tiles_m = (M + bm - 1) / bm;
     if (bm == 256) return launch_g2<256>(a, s);
     return launch_g2<128>(a, s);

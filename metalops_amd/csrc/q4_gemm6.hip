@@ -1,13 +1,12 @@
-// Prefill-shaped q4_0 matmul (M > 64) on gfx950: the LDS-staged GEMM of
-// q4_gemm5 with two waves per SIMD.
+// Prefill-shaped q4_0 matmul (M > 64) on gfx950: LDS-staged activations,
+// per-wave dequantized weights, two waves per SIMD.
 //
 //   * Wave tile 128 x 64 of v_mfma_f32_32x32x16_f16 (128 fp32 accumulators), so
 //     two waves share each SIMD and one wave's LDS, copy and barrier stalls are
-//     covered by the other's MFMAs.  Default form (WGM = 1): WG = 4 waves along
-//     N, WG tile 128 x 256, two workgroups per CU, each barrier among 4 waves.
-//     WGM = 2: WG = 8 waves in a 2 (M) x 4 (N) grid, WG tile 256 x 256.
-//   * Activations: as q4_gemm5 (one BM x 128-byte stage per slot, 3 slots,
-//     swizzled chunk positions 8r + (c ^ (r & 7))); each wave copies 32 rows.
+//     covered by the other's MFMAs.  WG = 4 waves along N, WG tile 128 x 256,
+//     two workgroups per CU, each barrier among 4 waves.
+//   * Activations: one 128 x 128-byte stage per slot, 3 slots, swizzled chunk
+//     positions 8r + (c ^ (r & 7)); each wave copies 32 rows.
 //     A operands are reloaded in place: operand (ks, i) of the next step is
 //     read right after the last MFMA of this step that uses it.
 //   * Weights: each wave copies the raw bytes of its 64 columns (1152 bytes per
@@ -16,17 +15,18 @@
 //     unpack to 1024 + q, minus 1032, times d: the reference's fp16 dequant
 //     value) one step ahead, in 12 chunks spread over the step's 16 MFMAs.
 //   * Barrier between the two steps of a stage; stage s+3's copies go out
-//     during the second step, one per two MFMAs.  Plan, split-K partials and
-//     the reduction kernel are q4_gemm5's, except that with two K splits the
-//     second workgroup of a tile to finish adds the first's partial itself,
-//     read from their shared XCD's L2 (see xcd_ticket_inc), and stores Y.
+//     during the second step, one per two MFMAs.
+//   * Split K (grid.z): fp32 partial tiles in the caller's workspace, summed in
+//     split order by q4_gemm6_reduce_kernel; with two splits the second
+//     workgroup of a tile to finish adds the first's partial itself, read from
+//     their shared XCD's L2 (see xcd_ticket_inc), and stores Y.
 //
 // MFMA 32x32 output layout: lane l holds D[8*(r/4) + 4*(l/32) + r%4][l%32], r = 0..15.
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
 
-#include "q4_gemm4.h"
+#include "q4_prefill.h"
 
 namespace mcq4 {
 
@@ -36,20 +36,15 @@ constexpr int G6_WN = 64;                      // columns per wave
 constexpr int G6_RAW_W = 18 * G6_WN;           // raw weight bytes per wave and step (1152)
 constexpr int G6_RAW_SLOT = 1280;              // 1024 + 256 (remainder copy); covers the read overhang
 constexpr int G6_RAW_N = 2 * G6_NS;            // raw ring slots per wave (steps)
-// WGM rows of four waves: WG tile (128 WGM) x 256, 4 WGM waves.  WGM = 2 runs
-// one 8-wave workgroup per CU; WGM = 1 two 4-wave workgroups per CU.
-template <int WGM>
-constexpr size_t g6_lds_bytes() {
-    return (size_t)G6_NS * (128 * WGM) * G6_ROWB + (size_t)(4 * WGM) * G6_RAW_N * G6_RAW_SLOT;
-}
-static_assert(g6_lds_bytes<2>() <= 160 * 1024 && 2 * g6_lds_bytes<1>() <= 160 * 1024, "LDS budget");
+constexpr int WGM = 1;                         // rows of four waves per workgroup
+constexpr size_t G6_LDS = (size_t)G6_NS * (128 * WGM) * G6_ROWB + (size_t)(4 * WGM) * G6_RAW_N * G6_RAW_SLOT;
+static_assert(2 * G6_LDS <= 160 * 1024, "LDS budget: two workgroups per CU");
 static_assert(G6_RAW_SLOT >= 1024 + 64 * 4 && G6_RAW_SLOT >= G6_RAW_W + 16, "raw slot covers the remainder copy and the read overhang");
 
-template <int WGM>
-__global__ void __launch_bounds__(256 * WGM, 2 / WGM)
-q4_gemm6_kernel(Gemm4Args a) {
+__global__ void __launch_bounds__(256, 2)
+q4_gemm6_kernel(Gemm6Args a) {
     constexpr int BM = 128 * WGM, NWAVES = 4 * WGM;
-    constexpr int WM = BM / WGM, WN = G6_WN;   // 128 x 64 wave tiles in both forms
+    constexpr int WM = BM / WGM, WN = G6_WN;   // 128 x 64 wave tiles
     constexpr int TM = WM / 32, TN = WN / 32;    // 4 x 2
     constexpr int A_SLOT = BM * G6_ROWB;
     constexpr int A_LD = BM * 8 / (64 * NWAVES);     // A copies per wave and stage (4)
@@ -70,7 +65,7 @@ q4_gemm6_kernel(Gemm4Args a) {
     if (tile_id >= ntiles) return;                // grid padding (XCD-local exchange)
     const int tm = tile_id % a.tiles_m;
     const int tn = tile_id / a.tiles_m;
-    const int m0 = tm * BM, n0 = tn * G4_BN;
+    const int m0 = tm * BM, n0 = tn * G6_BN;
     const int z = (int)blockIdx.z;
     const int k_lo = (int)((int64_t)a.nb * z / a.S);
     const int nk = (int)((int64_t)a.nb * (z + 1) / a.S) - k_lo;
@@ -268,7 +263,7 @@ q4_gemm6_kernel(Gemm4Args a) {
             }
         return;
     }
-    float *part = a.partials + ((int64_t)tile_id * a.S + z) * (BM * G4_BN);
+    float *part = a.partials + ((int64_t)tile_id * a.S + z) * (BM * G6_BN);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -277,7 +272,7 @@ q4_gemm6_kernel(Gemm4Args a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int ml = wm * WM + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
-                part[ml * G4_BN + nl] = acc[i][j][r];
+                part[ml * G6_BN + nl] = acc[i][j][r];
             }
         }
     if (!a.tickets) return;                       // the reduce kernel sums
@@ -297,7 +292,7 @@ q4_gemm6_kernel(Gemm4Args a) {
     __syncthreads();
     const uint32_t lf = *last_flag;
     if (!lf) return;
-    const float *other = a.partials + ((int64_t)tile_id * 2 + (1 - z)) * (BM * G4_BN);
+    const float *other = a.partials + ((int64_t)tile_id * 2 + (1 - z)) * (BM * G6_BN);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -307,7 +302,7 @@ q4_gemm6_kernel(Gemm4Args a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int ml = wm * WM + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
-                o[r] = load_l2_f32(other, (ml * G4_BN + nl) * 4);
+                o[r] = load_l2_f32(other, (ml * G6_BN + nl) * 4);
             }
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
@@ -319,90 +314,94 @@ q4_gemm6_kernel(Gemm4Args a) {
     if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Plan of the 4-wave form: 128-row tiles; K split S = the largest power of two
-// (<= 16, at least 16 K blocks per split) that keeps the grid within 256
-// workgroups, one per CU; doubled once more when that stays within 512 (two
-// per CU) and leaves at least 96 blocks per split, which pays on long K.
-// Measured over M = 128..2048 and the Llama shapes (graph replays): M=512
-// 11008x4096 S=4 63.9 us (the previous "until 384 workgroups" plan, S=8:
-// 78.5), M=512 4096x14336 S=1 72.7 (S=2: 81.6), M=2048 4096x4096 S=1 81.2
-// (S=2: 86.4), M=2048 14336x4096 S=2 242.9 (S=1: 252.9).  MCQ4_GEMM4_SPLIT
-// overrides.
-static G4Cfg gemm6_config1(int64_t M, int64_t K, int64_t N) {
-    G4Cfg c{128, 1};
-    const int64_t t = ((M + 127) / 128) * ((N + G4_BN - 1) / G4_BN);
-    const int64_t nb = K / QK;
-    while (t * c.S * 2 <= 256 && nb / (c.S * 2) >= 16 && c.S < 16) c.S *= 2;
-    if (t * c.S * 2 <= 512 && nb / (c.S * 2) >= 96 && c.S < 16) c.S *= 2;
-    if (const char *env = getenv("MCQ4_GEMM4_SPLIT")) c.S = std::max(1, std::min(16, atoi(env)));
-    if (c.S > nb) c.S = 1;
-    return c;
+// Sums the S fp32 partial tiles of every output tile in split order
+// (deterministic) and stores fp16; four consecutive columns per thread.
+__global__ void __launch_bounds__(256)
+q4_gemm6_reduce_kernel(Gemm6Args a) {
+    constexpr int TILE = G6_BM * G6_BN;
+    const int64_t v4 = (int64_t)blockIdx.x * 256 + threadIdx.x;     // float4 index
+    const int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n;
+    if (v4 >= ntiles * (TILE / 4)) return;
+    const int64_t tile = v4 / (TILE / 4);
+    const int e = (int)(v4 % (TILE / 4)) * 4;
+    const int tm = (int)(tile % a.tiles_m), tn = (int)(tile / a.tiles_m);
+    const float4_t *p = (const float4_t *)(a.partials + tile * a.S * TILE + e);
+    float4_t sum = p[0];
+    for (int sp = 1; sp < a.S; ++sp) sum += p[(int64_t)sp * (TILE / 4)];
+    const int m = tm * G6_BM + e / G6_BN, n = tn * G6_BN + e % G6_BN;
+    if (m >= a.M) return;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        if (n + c < a.N) a.Y[(int64_t)m * a.ldy + n + c] = (_Float16)sum[c];
 }
 
-// Workgroup rows: MCQ4_GEMM6_WGM=1|2 (default 1: two 4-wave workgroups per CU
-// match or beat one 8-wave workgroup on every shape measured -- M=128
-// K=N=4096: 23 vs 31 us; M=512 K=11008 N=4096: 64 vs 70 us; M=2048: equal).
-static int gemm6_wgm() {
-    if (const char *env = getenv("MCQ4_GEMM6_WGM")) return atoi(env) == 2 ? 2 : 1;
-    return 1;
+// Plan: 128-row tiles; K split S = the largest power of two (<= 16, at least
+// 16 K blocks per split) that keeps the grid within 256 workgroups, one per
+// CU; doubled once more when that stays within 512 (two per CU) and leaves at
+// least 96 blocks per split, which pays on long K.  Measured over M =
+// 128..2048 and the Llama shapes (graph replays): M=512 11008x4096 S=4 63.9 us
+// (the previous "until 384 workgroups" plan, S=8: 78.5), M=512 4096x14336 S=1
+// 72.7 (S=2: 81.6), M=2048 4096x4096 S=1 81.2 (S=2: 86.4), M=2048 14336x4096
+// S=2 242.9 (S=1: 252.9).  MCQ4_GEMM6_SPLIT overrides (tests).
+static int gemm6_splits(int64_t M, int64_t K, int64_t N) {
+    int S = 1;
+    const int64_t t = ((M + G6_BM - 1) / G6_BM) * ((N + G6_BN - 1) / G6_BN);
+    const int64_t nb = K / QK;
+    while (t * S * 2 <= 256 && nb / (S * 2) >= 16 && S < 16) S *= 2;
+    if (t * S * 2 <= 512 && nb / (S * 2) >= 96 && S < 16) S *= 2;
+    if (const char *env = opt("MCQ4_GEMM6_SPLIT")) S = std::max(1, std::min(16, atoi(env)));
+    if (S > nb) S = 1;
+    return S;
+}
+
+bool gemm6_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N) {
+    return N % 128 == 0 && ((uintptr_t)W % 16) == 0 && ((uintptr_t)X % 16) == 0 && ldx % 8 == 0 &&
+           K >= QK;
 }
 
 size_t gemm6_workspace_bytes(int64_t M, int64_t K, int64_t N) {
-    const G4Cfg c = gemm6_config1(M, K, N);
-    if (c.S == 1) return 0;
-    const int64_t t = ((M + 127) / 128) * ((N + G4_BN - 1) / G4_BN);
-    return COUNTER_BYTES + (size_t)t * c.S * 128 * G4_BN * sizeof(float);
+    const int S = gemm6_splits(M, K, N);
+    if (S == 1) return 0;
+    const int64_t t = ((M + G6_BM - 1) / G6_BM) * ((N + G6_BN - 1) / G6_BN);
+    return COUNTER_BYTES + (size_t)t * S * G6_BM * G6_BN * sizeof(float);
 }
 
-template <int WGM>
-static hipError_t launch_g6(Gemm4Args &a, hipStream_t s) {
-    constexpr size_t lds = g6_lds_bytes<WGM>();
+hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s) {
+    Gemm6Args a;
+    a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
+    a.M = M; a.nb = K / QK; a.N = N;
+    a.tiles_n = (N + G6_BN - 1) / G6_BN;
+    a.tiles_m = (M + G6_BM - 1) / G6_BM;
+    a.S = gemm6_splits(M, K, N);
+    a.partials = nullptr;
+    if (a.S > 1) {
+        if (!ws) return hipErrorInvalidValue;
+        a.partials = (float *)((char *)ws + COUNTER_BYTES);
+        // Two splits: summed in the kernel through the XCD's L2 (MCQ4_XCD_LOCAL=0:
+        // by the reduction kernel).
+        if (a.S == 2 && !opt_is("MCQ4_XCD_LOCAL", '0') && (a.tiles_m * a.tiles_n + 7) / 8 <= 4096)
+            a.tickets = (uint64_t *)ws;
+    }
     static std::atomic<uint64_t> done{0};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)q4_gemm6_kernel<WGM>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds);
+        e = hipFuncSetAttribute((const void *)q4_gemm6_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)G6_LDS);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
     const int ntiles = a.tiles_m * a.tiles_n;
     const int gx = a.tickets ? (ntiles + 7) / 8 * 8 : ntiles;
-    hipLaunchKernelGGL((q4_gemm6_kernel<WGM>), dim3(gx, 1, a.S), dim3(256 * WGM), lds, s, a);
-    if (a.S > 1 && !a.tickets) return launch_gemm4_reduce(a, 128 * WGM, s);
+    hipLaunchKernelGGL(q4_gemm6_kernel, dim3(gx, 1, a.S), dim3(256), G6_LDS, s, a);
+    if (a.S > 1 && !a.tickets) {
+        const int64_t n4 = (int64_t)ntiles * (G6_BM * G6_BN / 4);
+        hipLaunchKernelGGL(q4_gemm6_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, a);
+    }
     return hipGetLastError();
-}
-
-// Same requirements as q4_gemm5 (N % 128 == 0, 16-byte aligned W and X rows).
-// WGM = 2 uses q4_gemm5's plan (256-row tiles); WGM = 1 its own.  The
-// workspace bound covers both (gemm5_workspace_bytes, gemm6_workspace_bytes).
-hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
-                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s) {
-    int wgm = gemm6_wgm();
-    G4Cfg c = wgm == 2 ? gemm5_config(M, K, N) : gemm6_config1(M, K, N);
-    if (c.bm != 128 * wgm) {                     // the 8-wave form needs 256-row tiles
-        wgm = 1;
-        c = gemm6_config1(M, K, N);
-    }
-    Gemm4Args a;
-    a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
-    a.M = M; a.nb = K / QK; a.N = N;
-    a.tiles_n = (N + G4_BN - 1) / G4_BN;
-    a.tiles_m = (M + c.bm - 1) / c.bm;
-    a.S = c.S;
-    a.partials = nullptr;
-    if (c.S > 1) {
-        if (!ws) return hipErrorInvalidValue;
-        a.partials = (float *)((char *)ws + COUNTER_BYTES);
-        // Two splits: summed in the kernel through the XCD's L2 (MCQ4_XCD_LOCAL=0:
-        // by the reduce kernel).
-        const char *xl = getenv("MCQ4_XCD_LOCAL");
-        if (c.S == 2 && !(xl && xl[0] == '0') && (a.tiles_m * a.tiles_n + 7) / 8 <= 4096)
-            a.tickets = (uint64_t *)ws;
-    }
-    return wgm == 2 ? launch_g6<2>(a, s) : launch_g6<1>(a, s);
 }
 
 }  // namespace mcq4

@@ -52,6 +52,7 @@ constexpr int GV_LOADS = 3;                  // copies per item (chunks 0..143 o
 constexpr int GV_SLOT = GV_WCH * 16 + 64;    // 2304 strip bytes + read overhang
 constexpr int GV_TPW_MAX = 4;                // tiles per workgroup
 constexpr int GV_XB_MAX = 4;                 // batches per wave (K <= 16*4*8*32 = 16384)
+constexpr int GV_RING = 2;                   // items in flight per wave (1 and 3 measured slower)
 constexpr int GV_NT = 2;                     // cache policy of the weight copies: non-temporal
 
 struct GemvArgs {
@@ -272,21 +273,11 @@ static hipError_t launch_gemv_r(const GemvArgs &a, int grid, int tpw, hipStream_
     }
 }
 
-template <int NW>
-static hipError_t launch_gemv_nw(const GemvArgs &a, int grid, int tpw, int ring, hipStream_t s) {
-    switch (ring) {
-        case 3: return launch_gemv_r<3, NW>(a, grid, tpw, s);
-        case 2: return launch_gemv_r<2, NW>(a, grid, tpw, s);
-        default: return launch_gemv_r<1, NW>(a, grid, tpw, s);
-    }
-}
-
 // True when the M == 1 kernel applies: 16-byte aligned weights and
 // activations, 18*N a multiple of 16 (N % 8 == 0), at least one whole 16-column
 // tile and at most GV_XB_MAX batches per wave (K <= 16384).
 bool gemv_dma_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t N) {
-    if (const char *env = getenv("MCQ4_GEMV_PATH"))
-        if (env[0] == 'o') return false;        // "off": use the batched decode kernel
+    if (opt_is("MCQ4_GEMV_PATH", 'o')) return false;   // "off": use the batched decode kernel
     return N % 8 == 0 && N >= 16 && ((uintptr_t)W % 16) == 0 &&
            ((uintptr_t)X % 16) == 0 && K >= QK && K <= GV_WAVES * GV_XB_MAX * GV_B * QK &&
            N * 18 * 8 < ((int64_t)1 << 31);
@@ -305,18 +296,15 @@ hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int
     // One 16-wave workgroup per CU and up to GV_TPW_MAX tiles each.  Larger N
     // (lm_head: more than 1024 tiles) runs 8-wave workgroups of GV_TPW_MAX tiles,
     // two per CU, backfilled as they finish (measured 56 vs 66 us at N = 128256;
-    // 16 waves stay faster on the layer shapes).  MCQ4_GEMV_WAVES=8|16 forces one.
-    int nw = a.ntiles > 256 * GV_TPW_MAX ? 8 : 16;
-    if (const char *env = getenv("MCQ4_GEMV_WAVES")) nw = atoi(env) == 8 ? 8 : 16;
+    // 16 waves stay faster on the layer shapes).
+    const int nw = a.ntiles > 256 * GV_TPW_MAX ? 8 : 16;
     const int per_round = nw == 16 ? 256 : 512;
     int grid = std::min(a.ntiles, per_round);
     if (a.ntiles > per_round * GV_TPW_MAX) grid = (a.ntiles + GV_TPW_MAX - 1) / GV_TPW_MAX;
     const int tpw = (a.ntiles + grid - 1) / grid;
     a.xw = ((a.nbt + nw - 1) / nw) * GV_B * 64;                   // my batches' activations
-    int ring = 2;
-    if (const char *env = getenv("MCQ4_GEMV_RING")) ring = std::max(1, std::min(3, atoi(env)));
-    if (nw == 8) return launch_gemv_nw<8>(a, grid, tpw, ring, s);
-    return launch_gemv_nw<16>(a, grid, tpw, ring, s);
+    if (nw == 8) return launch_gemv_r<GV_RING, 8>(a, grid, tpw, s);
+    return launch_gemv_r<GV_RING, 16>(a, grid, tpw, s);
 }
 
 }  // namespace mcq4

@@ -320,8 +320,7 @@ static hipError_t launch_gemvm_w(const GemvMArgs &a, int grid, int tpw, hipStrea
 // per workgroup on a 512-workgroup grid (N <= 32768).
 bool gemvm_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
                      int64_t N) {
-    if (const char *env = getenv("MCQ4_GEMV_PATH"))
-        if (env[0] == 'o') return false;
+    if (opt_is("MCQ4_GEMV_PATH", 'o')) return false;
     return M >= 2 && M <= 32 && N % 8 == 0 && N >= 16 && N / 16 <= 512 * GM_TPW_MAX &&
            ((uintptr_t)W % 16) == 0 && ((uintptr_t)X % 16) == 0 && ldx % 8 == 0 && K >= QK &&
            N * 18 * 8 < ((int64_t)1 << 31);
@@ -342,12 +341,11 @@ struct GmPlan {
 static GmPlan gemvm_plan(int64_t M, int64_t K, int64_t N) {
     const int ntiles = (int)(N / 16), nbt = (int)((K / QK + GM_B - 1) / GM_B);
     int waves = 16;
-    if (const char *env = getenv("MCQ4_GEMVM_WAVES")) waves = atoi(env) == 8 ? 8 : 16;
     // Two row blocks: 8-wave workgroups, one per CU (their registers fill the SIMDs).
     if (M > 16) waves = 8;
     const int cap = waves == 8 && M <= 16 ? 512 : 256;
     int S = M >= 8 && ntiles <= cap && nbt >= 2 * waves ? 2 : 1;
-    if (const char *env = getenv("MCQ4_GEMVM_SPLIT")) {
+    if (const char *env = opt("MCQ4_GEMVM_SPLIT")) {
         const int v = atoi(env);
         S = v == 2 || v == 4 || v == 8 ? v : 1;
     }
@@ -380,8 +378,7 @@ hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
     if (p.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.part = (float *)((char *)ws + COUNTER_BYTES);
-        const char *xl = getenv("MCQ4_XCD_LOCAL");
-        if (!(xl && xl[0] == '0') && p.S <= 8) a.tickets = (uint64_t *)ws;
+        if (!opt_is("MCQ4_XCD_LOCAL", '0') && p.S <= 8) a.tickets = (uint64_t *)ws;
     }
     if (M > 16) return launch_gemvm_w<8, 2>(a, p.grid, p.tpw, s);
     if (p.waves == 16) return launch_gemvm_w<16, 1>(a, p.grid, p.tpw, s);

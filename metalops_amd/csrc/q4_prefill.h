@@ -1,0 +1,38 @@
+// Shared plan and arguments of the LDS-staged q4_0 prefill GEMM (q4_gemm6):
+// output tiles of 128 x 256, optional split-K over grid.z with fp32 partial
+// tiles in the caller's workspace.
+#pragma once
+
+#include "q4_common.h"
+
+namespace mcq4 {
+
+constexpr int G6_BM = 128;   // output tile rows
+constexpr int G6_BN = 256;   // output tile columns
+
+struct Gemm6Args {
+    const _Float16 *X;
+    int64_t ldx;
+    const uint8_t *W;
+    _Float16 *Y;
+    int64_t ldy;
+    int M, nb, N;
+    int tiles_m, tiles_n;
+    int S;               // K splits (grid.z)
+    float *partials;     // [tiles][S][128*256] when S > 1
+    // S == 2 with an XCD-local exchange: grid.x padded to a multiple of 8, the
+    // second split of a tile to finish adds the first's partial and stores Y
+    // (64-bit tickets [8][4096] by blockIdx.x mod 8 at the workspace start).
+    uint64_t *tickets = nullptr;
+    // Device flag raised when an XCD-local exchange found its splits on
+    // different XCDs (the tile is then summed through memory instead).
+    uint32_t *placement_flag = nullptr;
+};
+
+// Needs N % 128 == 0, 16-byte aligned W and activation rows, K >= 32.
+bool gemm6_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
+size_t gemm6_workspace_bytes(int64_t M, int64_t K, int64_t N);
+hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
+
+}  // namespace mcq4

@@ -4,7 +4,7 @@
 // rows kb*32 .. kb*32+31 (coalesced across the wave along n) and writes the 18
 // block bytes with 2-byte stores.  These are one-time conversion kernels; the
 // hot path is the matmul.
-#include "q4_common.h"
+#include "i4_common.h"
 
 namespace mcq4 {
 
@@ -16,31 +16,37 @@ __device__ __forceinline__ _Float16 to_half_exact(float v) {
     return (_Float16)v;
 }
 
-// Reference rule, quantization.py:333-369.  Every step is one fp32 IEEE
-// operation rounded to nearest even (the file is compiled with
-// -ffp-contract=off, and '/' is the correctly rounded divide): amax/7, x/d, +8, then
-// round-half-even (rintf under the default rounding mode) and clamp.
+// Reference rule, quantization.py:333-369, for a weight of dtype DT (fp32,
+// fp16 or bf16).  The reference runs every step as a torch op on the weight's
+// own dtype, so each step here is one fp32 IEEE operation (the file is
+// compiled with -ffp-contract=off, and '/' is the correctly rounded divide)
+// followed by a rounding to DT: amax (exact), amax/7, x/d, +8, round half to
+// even (rintf, exact in DT), clamp.  For fp16 and bf16 the fp32 result rounded
+// to DT equals the correctly rounded DT operation (fp32 carries more than
+// 2p + 2 bits for both, so the double rounding is innocuous).  d is stored as
+// fp16 (d.to(float16), quantization.py:352), one more rounding for bf16.
+template <int DT>
 __global__ void __launch_bounds__(256)
-quantize_ref_kernel(const float *__restrict__ W, int64_t ldw, int nb, int N,
+quantize_ref_kernel(const void *__restrict__ W, int64_t ldw, int nb, int N,
                     uint8_t *__restrict__ out) {
 #pragma clang fp contract(off)
     const int n = blockIdx.x * blockDim.x + threadIdx.x;
     const int kb = blockIdx.y;
     if (n >= N || kb >= nb) return;
-    const float *src = W + (int64_t)kb * QK * ldw + n;
+    const int64_t base = (int64_t)kb * QK * ldw + n;
     float x[QK];
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < QK; ++j) {
-        x[j] = src[(int64_t)j * ldw];
+        x[j] = load_dt(W, base + (int64_t)j * ldw, DT);
         amax = fmaxf(amax, fabsf(x[j]));
     }
-    float d = amax / 7.0f;
+    float d = round_dt(amax / 7.0f, DT);
     d = (d > 0.0f) ? d : 1.0f;
     uint32_t q[QK];
 #pragma unroll
     for (int j = 0; j < QK; ++j) {
-        float t = x[j] / d + 8.0f;
+        const float t = round_dt(round_dt(x[j] / d, DT) + 8.0f, DT);
         float r = __builtin_rintf(t);
         r = fminf(fmaxf(r, 0.0f), 15.0f);
         q[j] = (uint32_t)r;
@@ -127,7 +133,19 @@ hipError_t launch_quantize(bool llama_rule, const float *W, int64_t ldw, int nb,
     if (llama_rule)
         hipLaunchKernelGGL(quantize_llama_kernel, grid, block, 0, s, W, ldw, nb, N, out);
     else
-        hipLaunchKernelGGL(quantize_ref_kernel, grid, block, 0, s, W, ldw, nb, N, out);
+        hipLaunchKernelGGL(quantize_ref_kernel<DT_F32>, grid, block, 0, s, (const void *)W, ldw, nb, N, out);
+    return hipGetLastError();
+}
+
+hipError_t launch_quantize_typed(int w_dtype, const void *W, int64_t ldw, int nb, int N,
+                                 uint8_t *out, hipStream_t s) {
+    dim3 grid((N + 255) / 256, nb), block(256);
+    if (w_dtype == DT_F16)
+        hipLaunchKernelGGL(quantize_ref_kernel<DT_F16>, grid, block, 0, s, W, ldw, nb, N, out);
+    else if (w_dtype == DT_BF16)
+        hipLaunchKernelGGL(quantize_ref_kernel<DT_BF16>, grid, block, 0, s, W, ldw, nb, N, out);
+    else
+        hipLaunchKernelGGL(quantize_ref_kernel<DT_F32>, grid, block, 0, s, W, ldw, nb, N, out);
     return hipGetLastError();
 }
 

@@ -251,13 +251,6 @@ SkinnyCfg skinny_config(int64_t M, int64_t K, int64_t N) {
     c.WAVES = nb >= 256 ? 16 : 8;
     c.S = 1;
     c.U = 8;
-    if (const char *env = getenv("MCQ4_SKINNY_CFG")) {  // "NT,WAVES,S,U" (tuning aid)
-        int nt, w, sk, u;
-        if (sscanf(env, "%d,%d,%d,%d", &nt, &w, &sk, &u) == 4 && (nt == 1 || nt == 2 || nt == 4) &&
-            (w == 4 || w == 8 || w == 16) && sk >= 1 && sk <= 64 && (u == 4 || u == 8 || u == 16)) {
-            c.NT = nt; c.WAVES = w; c.S = sk; c.U = u;
-        }
-    }
     if ((N + 16 * c.NT - 1) / (16 * c.NT) > COUNTER_SLOTS) c.S = 1;
     (void)M;
     return c;
@@ -291,8 +284,7 @@ hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
                         int64_t ldy, int M, int K, int N, void *ws, int *n_done, hipStream_t s);
 
 static bool use_decode_lds(const uint8_t *W, int64_t N, int64_t ldx) {
-    if (const char *env = getenv("MCQ4_DECODE_PATH"))  // "direct" forces this file's kernel
-        if (env[0] == 'd') return false;
+    if (opt_is("MCQ4_DECODE_PATH", 'd')) return false;   // "direct" forces this file's kernel
     return decode_lds_supported(W, N, ldx);
 }
 

@@ -365,12 +365,23 @@ def matmul_int8(
 
 
 class Int4Linear(nn.Module):
-    """INT4 quantized linear layer (quantization.py:457-613).
+    """Linear layer over per-group INT4 weights (API of quantization.py:457-613).
 
-    ``weight_packed [in/2, out]`` uint8, ``scales``/``zeros [G, out]`` and ``bias``
-    are buffers.  ``dequant_on_load=True`` keeps a dequantized fp16 weight and
-    runs a plain fp16 matmul; ``keep_quantized()`` drops it and runs the INT4
-    kernels on every forward.
+    State (the serialized format, kept as in the reference): buffers
+    ``weight_packed [in/2, out]`` uint8, ``scales`` / ``zeros [G, out]`` in the
+    layer's dtype (fp32 when none is given) and ``bias [out]`` (or a ``None``
+    parameter).
+
+    Two execution modes:
+
+    * dense (``dequantize()``, the default after ``from_float``): a dequantized
+      copy of the weight, never serialized, feeds a plain GEMM; activations are
+      cast to that copy's dtype (fp16 by default) and the result back;
+    * quantized (``keep_quantized()``): every forward runs the INT4 kernels of
+      ``matmul_int4`` on the packed weight -- 4x less weight traffic, which is
+      what a memory-bound decode step wants.
+
+    Inputs of any rank ``[..., in]`` are flattened to 2-D for the kernels.
     """
 
     def __init__(
@@ -388,35 +399,40 @@ class Int4Linear(nn.Module):
         self.out_features = out_features
         self.group_size = group_size
         self._dequant_on_load = dequant_on_load
-        self.register_buffer(
-            "weight_packed",
-            torch.zeros((in_features // 2, out_features), dtype=torch.uint8, device=device))
-        num_groups = (in_features + group_size - 1) // group_size
-        self.register_buffer(
-            "scales",
-            torch.ones((num_groups, out_features), dtype=dtype or torch.float32, device=device))
-        self.register_buffer(
-            "zeros",
-            torch.zeros((num_groups, out_features), dtype=dtype or torch.float32, device=device))
         self._weight_dequant: Optional[torch.Tensor] = None
+        param_dtype = dtype if dtype is not None else torch.float32
+        groups = -(-in_features // group_size)
+        factory = {"device": device}
+        self.register_buffer("weight_packed",
+                             torch.zeros(in_features // 2, out_features, dtype=torch.uint8, **factory))
+        self.register_buffer("scales", torch.ones(groups, out_features, dtype=param_dtype, **factory))
+        self.register_buffer("zeros", torch.zeros(groups, out_features, dtype=param_dtype, **factory))
         if bias:
-            self.register_buffer(
-                "bias", torch.zeros(out_features, dtype=dtype or torch.float32, device=device))
+            self.register_buffer("bias", torch.zeros(out_features, dtype=param_dtype, **factory))
         else:
             self.register_parameter("bias", None)
 
+    # -- mode switches -------------------------------------------------------
     def dequantize(self, dtype: Optional[torch.dtype] = None) -> None:
-        """Materialise the dequantized weight (default fp16) for plain matmuls."""
-        if dtype is None:
-            dtype = torch.float16
-        self._weight_dequant = dequantize_int4(
-            self.weight_packed, self.scales, self.zeros, self.group_size, dtype)
+        """Switch to dense mode with a weight dequantized to ``dtype`` (fp16 by default)."""
+        target = torch.float16 if dtype is None else dtype
+        self._weight_dequant = dequantize_int4(self.weight_packed, self.scales, self.zeros,
+                                               self.group_size, target)
         self._dequant_on_load = True
 
     def keep_quantized(self) -> None:
-        """Drop the dequantized weight; forward then runs the INT4 kernels."""
-        self._weight_dequant = None
+        """Switch to quantized mode: free the dense copy, run the INT4 kernels."""
         self._dequant_on_load = False
+        self._weight_dequant = None
+
+    # -- construction --------------------------------------------------------
+    @torch.no_grad()
+    def _load_from_dense(self, weight_in_out: torch.Tensor, bias: Optional[torch.Tensor]) -> None:
+        packed, scales, zeros = quantize_int4(weight_in_out, self.group_size)
+        for name, value in (("weight_packed", packed), ("scales", scales), ("zeros", zeros)):
+            getattr(self, name).copy_(value)
+        if bias is not None:
+            self.bias.copy_(bias)
 
     @classmethod
     def from_float(
@@ -425,36 +441,31 @@ class Int4Linear(nn.Module):
         group_size: int = 128,
         dequant_on_load: bool = True,
     ) -> "Int4Linear":
-        """Quantize an ``nn.Linear`` (its weight ``[out, in]`` transposed to ``[in, out]``)."""
-        q_linear = cls(
-            in_features=module.in_features,
-            out_features=module.out_features,
-            group_size=group_size,
-            bias=module.bias is not None,
-            device=module.weight.device,
-            dtype=module.weight.dtype,
-            dequant_on_load=dequant_on_load,
-        )
-        weight = module.weight.data.T.contiguous()
-        W_packed, scales, zeros = quantize_int4(weight, group_size)
-        q_linear.weight_packed.copy_(W_packed)
-        q_linear.scales.copy_(scales)
-        q_linear.zeros.copy_(zeros)
-        if module.bias is not None:
-            q_linear.bias.copy_(module.bias.data)
+        """Quantize an ``nn.Linear``: its ``[out, in]`` weight is packed as ``[in, out]``."""
+        w = module.weight
+        layer = cls(module.in_features, module.out_features, group_size=group_size,
+                    bias=module.bias is not None, device=w.device, dtype=w.dtype,
+                    dequant_on_load=dequant_on_load)
+        layer._load_from_dense(w.detach().t().contiguous(),
+                               None if module.bias is None else module.bias.detach())
         if dequant_on_load:
-            q_linear.dequantize()
-        return q_linear
+            layer.dequantize()
+        return layer
+
+    # -- compute -------------------------------------------------------------
+    def _dense(self, x: torch.Tensor) -> torch.Tensor:
+        w = self._weight_dequant
+        return (x.to(w.dtype) @ w).to(x.dtype)
+
+    def _quantized(self, x: torch.Tensor) -> torch.Tensor:
+        lead = x.shape[:-1]
+        y2 = matmul_int4(x.reshape(-1, x.shape[-1]), self.weight_packed, self.scales, self.zeros,
+                         self.group_size)
+        return y2.reshape(*lead, self.out_features)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self._weight_dequant is not None:
-            x_half = x.half() if x.dtype != torch.float16 else x
-            y = (x_half @ self._weight_dequant).to(x.dtype)
-        else:
-            y = matmul_int4(x, self.weight_packed, self.scales, self.zeros, self.group_size)
-        if self.bias is not None:
-            y = y + self.bias
-        return y
+        y = self._dense(x) if self._weight_dequant is not None else self._quantized(x)
+        return y if self.bias is None else y + self.bias
 
     def extra_repr(self) -> str:
         mode = "fast_fp16" if self._weight_dequant is not None else "int4_kernel"

@@ -52,20 +52,37 @@ def _stream(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_DTYPE_CODES = {torch.float32: _lib.MCQ4_DTYPE_F32, torch.float16: _lib.MCQ4_DTYPE_F16,
+                torch.bfloat16: _lib.MCQ4_DTYPE_BF16}
+
+
 def _quantize(weight: torch.Tensor, llama_rule: bool) -> torch.Tensor:
     K, N = weight.shape
     assert K % QK4_0 == 0, f"K ({K}) must be divisible by {QK4_0}"   # quantization.py:329
     _require_device(weight)
-    w = weight if weight.dtype == torch.float32 else weight.float()
-    if w.stride(1) != 1 or w.stride(0) < N or w.data_ptr() % 4:
+    # The reference rule rounds every step in the weight's dtype (fp32, fp16 and
+    # bf16 run natively); other float dtypes are quantized from fp32, and the
+    # llama.cpp rule (a benchmark generator) always runs in fp32.
+    if llama_rule or weight.dtype not in _DTYPE_CODES:
+        w = weight.float()
+    else:
+        w = weight
+    esz = w.element_size()
+    if w.stride(1) != 1 or w.stride(0) < N or w.data_ptr() % esz:
         w = w.contiguous()
     blocks = torch.empty((K // QK4_0, N, BLOCK_Q4_0_SIZE), dtype=torch.uint8, device=w.device)
     if K == 0 or N == 0:
         return blocks
-    fn = _lib.lib.mcq4_quantize_q4_0_llama if llama_rule else _lib.lib.mcq4_quantize_q4_0
     with torch.cuda.device(w.device):
-        _lib.check(fn(w.data_ptr(), w.stride(0), K, N, blocks.data_ptr(), _stream(w.device)),
-                   fn.__name__)
+        if llama_rule:
+            _lib.check(_lib.lib.mcq4_quantize_q4_0_llama(w.data_ptr(), w.stride(0), K, N,
+                                                         blocks.data_ptr(), _stream(w.device)),
+                       "mcq4_quantize_q4_0_llama")
+        else:
+            _lib.check(_lib.lib.mcq4_quantize_q4_0_typed(w.data_ptr(), _DTYPE_CODES[w.dtype],
+                                                         w.stride(0), K, N, blocks.data_ptr(),
+                                                         _stream(w.device)),
+                       "mcq4_quantize_q4_0_typed")
     return blocks
 
 
@@ -75,9 +92,8 @@ def quantize_ggml_q4_0(weight: torch.Tensor) -> torch.Tensor:
     Per block of 32 rows of a column: ``d = amax/7`` (1 when amax is 0),
     ``q = round_half_even(x/d + 8)`` clamped to [0, 15]; bytes 0..1 hold fp16(d),
     byte ``2+i`` holds ``q[2i] | q[2i+1] << 4`` (quantization.py:333-369).
-    fp32 weights reproduce the reference bit for bit; other float dtypes are
-    quantized from their exact fp32 upcast (the reference rounds each step in
-    the weight's own dtype instead).
+    As in the reference, every step is rounded to the weight's own dtype (fp32,
+    fp16 or bf16), so the bytes match the reference's for each of them.
     """
     return _quantize(weight, llama_rule=False)
 
@@ -149,11 +165,15 @@ _workspace = _Workspace()
 
 
 def matmul_ggml_q4_0(X: torch.Tensor, W_blocks: torch.Tensor) -> torch.Tensor:
-    """``Y[M, N] = X[M, K] @ dequant(W_blocks)`` with fp16 inputs and fp32 accumulation.
+    """``Y[M, N] = X[M, K] @ dequant(W_blocks)``, returned in ``X.dtype``.
 
-    ``X`` is used as fp16 (as the reference's GPU binding does, quantization.py:448);
-    the result is returned in ``X.dtype`` (quantization.py:452-454).  M <= 64 runs
-    the decode kernel, larger M the prefill MFMA GEMM.
+    fp16 X runs the MFMA kernels: fp16 weights ``(q-8)*d`` (one rounding),
+    fp32 accumulation, fp16 result (the reference's GPU kernel,
+    native/quant_kernels.metal:1738-1886).  bf16 and fp32 X follow the
+    reference's own path for those dtypes (quantization.py:452-454): the
+    weight dequantized to X's dtype, fp32 accumulation, the result in X's
+    dtype -- so bf16 activations beyond the fp16 range stay finite.  M <= 64
+    runs the decode kernels, larger M the prefill GEMM.
     """
     num_blocks_per_col, N, _ = W_blocks.shape
     K = num_blocks_per_col * QK4_0
@@ -163,23 +183,32 @@ def matmul_ggml_q4_0(X: torch.Tensor, W_blocks: torch.Tensor) -> torch.Tensor:
         raise RuntimeError(f"X must be 2-D [M, K], got shape {tuple(X.shape)}")
     if W_blocks.dtype != torch.uint8 or W_blocks.shape[2] != BLOCK_Q4_0_SIZE:
         raise RuntimeError("W_blocks must be uint8 [K/32, N, 18]")
+    if X.dtype not in _DTYPE_CODES:
+        raise RuntimeError(f"X must be float16, bfloat16 or float32, got {X.dtype}")
     M = X.shape[0]
-    out_dtype = X.dtype
-    x = X if X.dtype == torch.float16 else X.half()
+    w = W_blocks if W_blocks.is_contiguous() else W_blocks.contiguous()
+    if w.data_ptr() % 2:
+        w = w.clone()
+    Y = torch.empty((M, N), dtype=X.dtype, device=X.device)
+    if M == 0 or N == 0:
+        return Y
+    if K == 0:
+        return Y.zero_()
+    stream = _stream(X.device)
+    if X.dtype != torch.float16:
+        x = X if (X.stride(1) == 1 and X.stride(0) >= K) else X.contiguous()
+        with torch.cuda.device(x.device):
+            _lib.check(_lib.lib.mcq4_matmul_q4_0(x.data_ptr(), _DTYPE_CODES[x.dtype], x.stride(0),
+                                                 w.data_ptr(), Y.data_ptr(), N, M, K, N, None, 0,
+                                                 stream),
+                       "mcq4_matmul_q4_0")
+        return Y
+    x = X
     if x.stride(1) != 1 or x.stride(0) % 8 or x.stride(0) < K or x.data_ptr() % 16:
         x = x.contiguous()
         if x.data_ptr() % 16:
             x = x.clone()
-    w = W_blocks if W_blocks.is_contiguous() else W_blocks.contiguous()
-    if w.data_ptr() % 2:
-        w = w.clone()
-    Y = torch.empty((M, N), dtype=torch.float16, device=x.device)
-    if M == 0 or N == 0:
-        return Y.to(out_dtype)
-    if K == 0:
-        return Y.zero_().to(out_dtype)
     need = int(_lib.lib.mcq4_matmul_workspace_bytes(M, K, N))
-    stream = _stream(x.device)
     ws_ptr, ws_bytes = None, 0
     if need:
         ws = _workspace.get(x.device, stream, need)
@@ -189,4 +218,4 @@ def matmul_ggml_q4_0(X: torch.Tensor, W_blocks: torch.Tensor) -> torch.Tensor:
                                                  Y.data_ptr(), N, M, K, N, ws_ptr, ws_bytes,
                                                  stream),
                    "mcq4_matmul_q4_0_f16")
-    return Y if out_dtype == torch.float16 else Y.to(out_dtype)
+    return Y

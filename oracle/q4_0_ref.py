@@ -37,8 +37,9 @@ Parity status of each function (how it is pinned):
 * ``quantize_ref_rule``: pinned by known-answer blocks (zero block, single-hot
   +a / -a at elements 0, 1, 16, 31, exact half-way ties resolved half-to-even),
   by the invariants ``q in [1, 15]`` and round-trip error ``<= d/2``, and by the
-  independent C restatement.  Tie cases at inexact quotients are pinned only by
-  the torch-semantics test (torch's own divide / round / half cast on CPU).
+  independent C restatement (fp32).  Tie cases at inexact quotients, and the
+  per-step rounding of fp16 / bf16 weights, are pinned by the torch-semantics
+  tests (the reference's own torch ops run on CPU in each dtype).
 * ``quantize_llama_rule``: known answers (max-signed element -> q = 0, zero
   block -> d = 0, q = 8) and the C restatement.
 * ``matmul_f64`` / ``matmul_f32``: float64 brute force over explicit loops on
@@ -65,22 +66,37 @@ def _pack(d32: np.ndarray, q: np.ndarray) -> np.ndarray:
     """
     nb, _, N = q.shape
     out = np.zeros((nb, N, BLOCK_Q4_0_SIZE), dtype=np.uint8)
-    out[:, :, 0:2] = d32.astype(np.float16).view(np.uint8).reshape(nb, N, 2)
+    with np.errstate(over="ignore"):
+        out[:, :, 0:2] = d32.astype(np.float16).view(np.uint8).reshape(nb, N, 2)
     qt = np.ascontiguousarray(q.transpose(0, 2, 1))        # [nb, N, 32]
     out[:, :, 2:18] = qt[:, :, 0::2] | (qt[:, :, 1::2] << 4)
     return out
 
 
-def quantize_ref_rule(weight: np.ndarray) -> np.ndarray:
-    """Restates quantization.py:307-371 (``quantize_ggml_q4_0``) for fp32 weights."""
-    w = np.ascontiguousarray(weight, dtype=np.float32)
+def quantize_ref_rule(weight: np.ndarray, dtype: str = "float32") -> np.ndarray:
+    """Restates quantization.py:307-371 (``quantize_ggml_q4_0``).
+
+    ``dtype`` is the weight's torch dtype ("float32", "float16" or "bfloat16";
+    for bfloat16 pass fp32 values that are bf16-representable).  The reference
+    runs each step as a torch op in that dtype (:338, :341, :342, :347), which
+    on CPU is the fp32 operation rounded to the dtype; ``d.to(float16)`` (:352)
+    is one more rounding for bf16.
+    """
+    from .int4_ref import round_to
+    code = {"float32": "f32", "float16": "f16", "bfloat16": "bf16"}[dtype]
+    if dtype == "float32":
+        w = np.ascontiguousarray(weight, dtype=np.float32)
+    else:
+        w = round_to(np.asarray(weight, dtype=np.float32), code)
+        assert np.array_equal(w, np.asarray(weight, dtype=np.float32)), "weight not representable in dtype"
     K, N, nb = _check_weight(w)
+    rnd = (lambda v: v) if dtype == "float32" else (lambda v: round_to(v, code))
     wb = w.reshape(nb, QK4_0, N)                                  # :335
-    amax = np.abs(wb).max(axis=1)                                 # :338
-    d = amax / np.float32(7.0)                                    # :341
+    amax = np.abs(wb).max(axis=1)                                 # :338, exact
+    d = rnd(amax / np.float32(7.0))                               # :341
     d = np.where(d > 0, d, np.float32(1.0)).astype(np.float32)    # :342
-    with np.errstate(divide="ignore", invalid="ignore"):
-        t = (wb / d[:, None, :]) + np.float32(8.0)                # :347, fp32 ops
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
+        t = rnd(rnd(wb / d[:, None, :]) + np.float32(8.0))        # :347, one op at a time
     q = np.clip(np.round(t), 0, 15).astype(np.uint8)              # round half to even
     return _pack(d, q)
 
@@ -133,6 +149,19 @@ def matmul_f32(X: np.ndarray, blocks: np.ndarray) -> np.ndarray:
     nb = blocks.shape[0]
     assert X.shape[1] == nb * QK4_0, f"X K dim ({X.shape[1]}) must match weight K ({nb * QK4_0})"
     return X.astype(np.float32) @ dequantize(blocks, np.float32)
+
+
+def matmul_xdtype(X: np.ndarray, blocks: np.ndarray, dtype: str) -> np.ndarray:
+    """The reference's path for non-fp16 activations (quantization.py:452-454):
+    ``W = dequantize(blocks, X.dtype)`` (the exact fp32 product rounded once to
+    ``dtype``), ``Y = X @ W`` summed in float64 here, then rounded to ``dtype``.
+    ``X`` holds values representable in ``dtype`` ("float32" or "bfloat16")."""
+    from .int4_ref import round_to
+    code = {"float32": "f32", "bfloat16": "bf16"}[dtype]
+    nb = blocks.shape[0]
+    assert X.shape[1] == nb * QK4_0, f"X K dim ({X.shape[1]}) must match weight K ({nb * QK4_0})"
+    W = round_to(dequantize(blocks, np.float32), code).astype(np.float64)
+    return round_to((X.astype(np.float64) @ W).astype(np.float32), code)
 
 
 def matmul_f64(X: np.ndarray, blocks: np.ndarray) -> np.ndarray:

@@ -23,3 +23,31 @@ def dev():
     if not torch.cuda.is_available():
         pytest.skip("no ROCm GPU")
     return torch.device("cuda:0")
+
+
+class _ReloadingEnviron(type(os.environ)):
+    """os.environ whose MCQ4_* writes also re-read the library's switches.
+
+    libmcq4.so reads its MCQ4_* test switches once (and again only on
+    mcq4_reload_options), never per call; the tests flip them through
+    os.environ / monkeypatch, so each such write reloads them here.
+    """
+
+    def _reload(self, key):
+        if str(key).startswith("MCQ4_"):
+            try:
+                from metalops_amd import _lib
+            except ImportError:        # library not built: nothing to reload
+                return
+            _lib.reload_options()
+
+    def __setitem__(self, key, value):
+        super().__setitem__(key, value)
+        self._reload(key)
+
+    def __delitem__(self, key):
+        super().__delitem__(key)
+        self._reload(key)
+
+
+os.environ.__class__ = _ReloadingEnviron

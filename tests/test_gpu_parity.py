@@ -49,14 +49,21 @@ def _check_rows(Y, Yref, tol=TOL):
 
 
 @pytest.mark.parametrize("K,N", [(32, 1), (32, 7), (64, 33), (352, 257), (4096, 96)])
-@pytest.mark.parametrize("rule", ["ref", "llama"])
+@pytest.mark.parametrize("rule", ["ref", "ref_f16", "ref_bf16", "llama"])
 def test_quantize_bit_exact(dev, K, N, rule):
+    """Reference rule for fp32, fp16 and bf16 weights (every step rounded in the
+    weight's dtype, quantization.py:335-347) and the llama.cpp generator rule."""
     mo = _mo()
     W = _weights(K, N, seed=K * 7 + N, outliers=True)
     W[:32, 0] = 0.0  # an all-zero block
-    if rule == "ref":
-        got = mo.quantize_ggml_q4_0(W.to(dev)).cpu().numpy()
-        want = ref.quantize_ref_rule(W.numpy())
+    if K >= 64 and N >= 2:
+        W[32:64, 1] = torch.randn(32) * 1e-7            # fp16 subnormal range: amax/7 -> 0 in fp16
+    if rule.startswith("ref"):
+        tdt, name = {"ref": (torch.float32, "float32"), "ref_f16": (torch.float16, "float16"),
+                     "ref_bf16": (torch.bfloat16, "bfloat16")}[rule]
+        Wd = W.to(tdt)
+        got = mo.quantize_ggml_q4_0(Wd.to(dev)).cpu().numpy()
+        want = ref.quantize_ref_rule(Wd.float().numpy(), name)
     else:
         got = mo.quantize_ggml_q4_0_llama(W.to(dev)).cpu().numpy()
         want = ref.quantize_llama_rule(W.numpy())
@@ -124,7 +131,7 @@ def test_matmul_matches_f64_bruteforce(dev):
     _check_rows(Y, ref.matmul_f64(X.numpy(), blocks), tol=2e-3)
 
 
-def test_matmul_deterministic_and_dtype(dev):
+def test_matmul_deterministic(dev):
     mo = _mo()
     W = _weights(2048, 384, seed=1)
     X = _acts(8, 2048, seed=2)
@@ -132,9 +139,37 @@ def test_matmul_deterministic_and_dtype(dev):
     y1 = mo.matmul_ggml_q4_0(X.to(dev), b)
     y2 = mo.matmul_ggml_q4_0(X.to(dev), b)
     assert torch.equal(y1, y2)
-    y32 = mo.matmul_ggml_q4_0(X.float().to(dev), b)
-    assert y32.dtype == torch.float32
-    assert torch.equal(y32, y1.float())
+
+
+@pytest.mark.parametrize("tdtype,name", [(torch.float32, "float32"), (torch.bfloat16, "bfloat16")])
+@pytest.mark.parametrize("M,K,N", [(1, 352, 257), (5, 1024, 96), (33, 512, 130), (130, 2048, 264)])
+def test_matmul_activation_dtypes(dev, tdtype, name, M, K, N):
+    """bf16 / fp32 activations follow the reference's path for them
+    (quantization.py:452-454): W dequantized to X's dtype, the product in X's
+    dtype, the result in X's dtype.  Oracle: the same rounding of W, float64
+    sums; bar 1e-2 of the row's max (bf16 output rounding is 2^-9 relative) and
+    1e-5 for fp32."""
+    mo = _mo()
+    W = _weights(K, N, seed=M + K, outliers=True)
+    g = torch.Generator().manual_seed(M * 5 + N)
+    X = torch.randn(M, K, generator=g).to(tdtype)
+    blocks = ref.quantize_llama_rule(W.numpy())
+    Y = mo.matmul_ggml_q4_0(X.to(dev), torch.from_numpy(blocks).to(dev))
+    assert Y.dtype == tdtype and Y.shape == (M, N)
+    Yref = ref.matmul_xdtype(X.float().numpy(), blocks, name)
+    _check_rows(Y.float().cpu().numpy(), Yref, tol=TOL if tdtype == torch.bfloat16 else 1e-5)
+
+
+def test_matmul_bf16_beyond_fp16_range(dev):
+    """bf16 activations of magnitude 1e6 (inf in fp16): finite results equal to
+    the reference's bf16 path, where an fp16 cast would give inf."""
+    mo = _mo()
+    W = _weights(256, 64, seed=3)
+    X = (torch.randn(4, 256, generator=torch.Generator().manual_seed(4)) * 1e6).to(torch.bfloat16)
+    blocks = ref.quantize_ref_rule(W.numpy())
+    Y = mo.matmul_ggml_q4_0(X.to(dev), torch.from_numpy(blocks).to(dev))
+    assert torch.isfinite(Y.float()).all()
+    _check_rows(Y.float().cpu().numpy(), ref.matmul_xdtype(X.float().numpy(), blocks, "bfloat16"))
 
 
 def _full_size_check(dev, M, K, N, outliers=False):
@@ -159,7 +194,8 @@ def _full_size_check(dev, M, K, N, outliers=False):
 
 @pytest.mark.parametrize("M,K,N", [
     (1, 4096, 12288), (1, 4096, 4096), (1, 4096, 11008), (1, 11008, 4096),
-    (4, 4096, 14336), (8, 14336, 4096), (16, 4096, 14336), (16, 14336, 4096),
+    (4, 4096, 14336), (8, 4096, 14336), (16, 4096, 14336),
+    (4, 14336, 4096), (8, 14336, 4096), (16, 14336, 4096),
 ])
 def test_matmul_decode_configs(dev, M, K, N):
     _full_size_check(dev, M, K, N)
@@ -175,18 +211,19 @@ def test_matmul_lm_head(dev):
     _full_size_check(dev, 512, 4096, 128256)
 
 
-# Every kernel variant on ragged and full shapes: the launchers read these
-# environment variables on each call, so a test can pin the variant it checks.
+def test_matmul_ragged_down(dev):
+    """K = 11008 (43 K blocks of 256, not a multiple of the K tile) at M = 1 and 512."""
+    _full_size_check(dev, 1, 11008, 4096)
+    _full_size_check(dev, 512, 11008, 4096, outliers=True)
+
+
+# Every kernel variant on ragged and full shapes, pinned through the library's
+# MCQ4_* switches (re-read on each environment write, tests/conftest.py).
 PATHS = {
     "gemv_dma": {},
-    "gemv_dma_ring1": {"MCQ4_GEMV_RING": "1"},
-    "gemv_dma_ring3": {"MCQ4_GEMV_RING": "3"},
-    "gemv_dma_w8": {"MCQ4_GEMV_WAVES": "8"},
-    "gemv_dma_w16": {"MCQ4_GEMV_WAVES": "16"},
 
     "decode_lds_m1": {"MCQ4_GEMV_PATH": "off"},
     "gemvm": {},
-    "gemvm_w8": {"MCQ4_GEMVM_WAVES": "8"},
     "gemvm_split2": {"MCQ4_GEMVM_SPLIT": "2"},
     "gemvm_split8": {"MCQ4_GEMVM_SPLIT": "8"},
     "gemvm_split4": {"MCQ4_GEMVM_SPLIT": "4"},
@@ -201,41 +238,21 @@ PATHS = {
     "gemm_sync": {"MCQ4_GEMM_PATH": "sync"},
     "gemm_async_bm256": {"MCQ4_GEMM_PATH": "async", "MCQ4_GEMM2_BM": "256"},
     "gemm_async_bm128": {"MCQ4_GEMM_PATH": "async", "MCQ4_GEMM2_BM": "128"},
-    "gemm3_bm256": {"MCQ4_GEMM_PATH": "3", "MCQ4_GEMM2_BM": "256"},
-    "gemm3_bm128": {"MCQ4_GEMM_PATH": "3", "MCQ4_GEMM2_BM": "128"},
-    "gemm4_bm256": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM2_BM": "256"},
-    "gemm4_bm128": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM2_BM": "128"},
-    "gemm4_split3": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM4_SPLIT": "3"},
-    "gemm4_wgm4_bm256": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM4_WGM": "4", "MCQ4_GEMM2_BM": "256"},
-    "gemm4_wgm4_bm128": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM4_WGM": "4", "MCQ4_GEMM2_BM": "128"},
-    "gemm4_split5_bm256": {"MCQ4_GEMM_PATH": "4", "MCQ4_GEMM4_SPLIT": "5", "MCQ4_GEMM2_BM": "256"},
-    "gemm5_bm256": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM2_BM": "256"},
-    "gemm5_bm128": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM2_BM": "128"},
-    "gemm5_split3": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM4_SPLIT": "3"},
-    "gemm5_split5_bm256": {"MCQ4_GEMM_PATH": "5", "MCQ4_GEMM4_SPLIT": "5", "MCQ4_GEMM2_BM": "256"},
     "gemm6": {"MCQ4_GEMM_PATH": "6"},
-    "gemm6_split3": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "3"},
-    "gemm6_wgm1": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_WGM": "1"},
-    "gemm6_wgm1_split3": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_WGM": "1", "MCQ4_GEMM4_SPLIT": "3"},
-    "gemm6_split2": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "2"},
-    "gemm6_split2_reduce": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "2", "MCQ4_XCD_LOCAL": "0"},
-    "gemm6_wgm2_split2": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_WGM": "2", "MCQ4_GEMM4_SPLIT": "2"},
-    "gemm6_split4": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "4"},
-    "gemm6_split8": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "8"},
-    "gemm6_split16": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM4_SPLIT": "16"},
+    "gemm6_split3": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "3"},
+    "gemm6_split2": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "2"},
+    "gemm6_split2_reduce": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "2", "MCQ4_XCD_LOCAL": "0"},
+    "gemm6_split4": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "4"},
+    "gemm6_split8": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "8"},
+    "gemm6_split16": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "16"},
 }
 PATH_SHAPES = {
     "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
                  (1, 16384, 272), (1, 14336, 4096)],
-    "gemv_dma_ring1": [(1, 352, 264), (1, 2048, 1040)],
-    "gemv_dma_ring3": [(1, 352, 264), (1, 11008, 4096), (1, 4096, 12288)],
-    "gemv_dma_w8": [(1, 352, 264), (1, 16384, 272), (1, 4096, 4096), (1, 11008, 2064)],
-    "gemv_dma_w16": [(1, 1024, 20480), (1, 352, 16400)],
 
     "decode_lds_m1": [(1, 352, 264), (1, 4096, 1032)],
     "gemvm": [(2, 32, 16), (3, 352, 264), (4, 1024, 4104), (5, 11008, 512), (8, 4096, 14336),
               (11, 2048, 1040), (16, 14336, 4096), (16, 352, 8200)],
-    "gemvm_w8": [(2, 352, 264), (7, 4096, 1040), (16, 11008, 512)],
     "gemvm_split2": [(2, 352, 264), (9, 4096, 1040), (16, 14336, 4096), (5, 11008, 512)],
     "gemvm_split8": [(16, 2048, 1032), (3, 14336, 512), (12, 512, 200)],
     "gemvm_split4": [(16, 4096, 1040), (6, 11008, 264), (13, 352, 8200)],
@@ -251,31 +268,11 @@ PATH_SHAPES = {
     "gemm_sync": [(65, 352, 70), (200, 1024, 264), (300, 2048, 520)],
     "gemm_async_bm256": [(65, 352, 72), (257, 1024, 264), (300, 2048, 520), (512, 4096, 776)],
     "gemm_async_bm128": [(65, 352, 72), (129, 1024, 264), (300, 2048, 520), (384, 4096, 776)],
-    "gemm3_bm256": [(65, 352, 72), (257, 1024, 264), (300, 2048, 520), (512, 4096, 776), (2048, 4096, 1024)],
-    "gemm3_bm128": [(65, 352, 72), (129, 1024, 264), (300, 2048, 520), (384, 4096, 776)],
-    "gemm4_bm256": [(65, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
-                    (100, 32, 256), (70, 64, 384)],
-    "gemm4_bm128": [(65, 352, 128), (129, 1024, 384), (300, 2048, 512), (384, 4096, 896), (100, 96, 256),
-                    (128, 4096, 4096), (512, 11008, 512)],
-    "gemm4_split3": [(200, 352, 384), (129, 1024, 256), (300, 4096, 640)],
-    "gemm4_wgm4_bm256": [(65, 352, 128), (257, 1024, 384), (512, 4096, 768), (2048, 4096, 1024), (128, 4096, 512)],
-    "gemm4_wgm4_bm128": [(65, 352, 128), (300, 2048, 512), (384, 4096, 896), (512, 11008, 512)],
-    "gemm4_split5_bm256": [(257, 352, 256), (100, 2048, 512)],
-    "gemm5_bm256": [(65, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
-                    (100, 32, 256), (70, 64, 384), (513, 96, 256)],
-    "gemm5_bm128": [(65, 352, 128), (129, 1024, 384), (300, 2048, 512), (384, 4096, 896), (100, 96, 256),
-                    (128, 4096, 4096), (512, 11008, 512)],
-    "gemm5_split3": [(200, 352, 384), (129, 1024, 256), (300, 4096, 640)],
-    "gemm5_split5_bm256": [(257, 352, 256), (100, 2048, 512)],
     "gemm6": [(129, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
               (200, 32, 256), (130, 64, 384), (513, 96, 256), (2048, 11008, 512)],
     "gemm6_split3": [(200, 352, 384), (300, 4096, 640)],
-    "gemm6_wgm1": [(129, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
-                   (200, 32, 256), (130, 64, 384), (513, 96, 256), (2048, 11008, 512)],
-    "gemm6_wgm1_split3": [(200, 352, 384), (300, 4096, 640)],
     "gemm6_split2": [(200, 352, 384), (300, 4096, 640), (512, 4096, 1024), (129, 1024, 2304)],
     "gemm6_split2_reduce": [(300, 4096, 640), (129, 1024, 2304)],
-    "gemm6_wgm2_split2": [(300, 4096, 640), (513, 1024, 2304)],
     "gemm6_split4": [(200, 2048, 384), (300, 4096, 640), (512, 11008, 1024)],
     "gemm6_split8": [(129, 4096, 256), (512, 11008, 512), (300, 8192, 768)],
     "gemm6_split16": [(200, 16384, 256), (130, 8192, 384)],
@@ -285,9 +282,7 @@ PATH_SHAPES = {
 @pytest.mark.parametrize("path,M,K,N", [(p, *s) for p, shapes in PATH_SHAPES.items() for s in shapes])
 def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM", "MCQ4_GEMV_PATH",
-              "MCQ4_GEMV_RING", "MCQ4_GEMVM_WAVES", "MCQ4_GEMM4_SPLIT", "MCQ4_GEMM4_WGM",
-              "MCQ4_GEMV_WAVES", "MCQ4_GEMM6_WGM", "MCQ4_GEMM5_SCHED", "MCQ4_GEMVM_SPLIT",
-              "MCQ4_XCD_LOCAL"):
+              "MCQ4_GEMM6_SPLIT", "MCQ4_GEMVM_SPLIT", "MCQ4_XCD_LOCAL"):
         monkeypatch.delenv(k, raising=False)
     for k, v in PATHS[path].items():
         monkeypatch.setenv(k, v)
@@ -308,11 +303,11 @@ def test_split_exchange_matches_reduce(dev, monkeypatch, M, K, N, split):
     reduction kernel add the same partials in the same order (two splits of the
     GEMM: p0 + p1, which commutes), so the outputs are identical bits."""
     print(f"split exchange {split} M={M} K={K} N={N}", flush=True)
-    for k in ("MCQ4_GEMM_PATH", "MCQ4_GEMM6_WGM", "MCQ4_XCD_LOCAL", "MCQ4_GEMM4_SPLIT", "MCQ4_GEMVM_SPLIT",
-              "MCQ4_GEMV_PATH", "MCQ4_GEMVM_WAVES"):
+    for k in ("MCQ4_GEMM_PATH", "MCQ4_XCD_LOCAL", "MCQ4_GEMM6_SPLIT", "MCQ4_GEMVM_SPLIT",
+              "MCQ4_GEMV_PATH"):
         monkeypatch.delenv(k, raising=False)
     if split.startswith("gemm"):
-        monkeypatch.setenv("MCQ4_GEMM4_SPLIT", split[-1])
+        monkeypatch.setenv("MCQ4_GEMM6_SPLIT", split[-1])
     else:
         monkeypatch.setenv("MCQ4_GEMVM_SPLIT", split[-1])
     mo = _mo()

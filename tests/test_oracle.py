@@ -143,6 +143,60 @@ def test_quantize_ref_matches_torch_cpu_semantics():
     np.testing.assert_array_equal(C.quantize_ref_rule(W.numpy()), out)
 
 
+def _torch_reference_quantize(W: torch.Tensor) -> tuple[np.ndarray, np.ndarray]:
+    """The reference's own steps (quantization.py:335-369) run by torch on CPU in
+    W's dtype; returns (d bytes [nb, N, 2], packed nibbles [nb, N, 16])."""
+    K, N = W.shape
+    nb = K // 32
+    wb = W.view(nb, 32, N)
+    d = wb.abs().amax(dim=1) / 7.0
+    d = torch.where(d > 0, d, torch.ones_like(d))
+    q = ((wb / d.unsqueeze(1)) + 8.0).round().clamp(0, 15).to(torch.uint8)
+    q_t = q.permute(0, 2, 1)
+    packed = (q_t[:, :, 0::2] | (q_t[:, :, 1::2] << 4)).numpy()
+    dbytes = d.to(torch.float16).contiguous().view(torch.uint8).view(nb, N, 2).numpy()
+    return dbytes, packed
+
+
+@pytest.mark.parametrize("tdtype,name", [(torch.float16, "float16"), (torch.bfloat16, "bfloat16")])
+def test_quantize_ref_half_dtypes_match_torch(tdtype, name):
+    """fp16 / bf16 weights: the reference rounds amax/7, x/d and +8 in the
+    weight's dtype.  The oracle's per-step rounding equals torch's CPU ops in
+    that dtype bit for bit -- on random data, on outliers, on tiny (subnormal
+    range) blocks where amax/7 rounds to zero in fp16, and on blocks built so
+    that x/d + 8 lands on exact half-way points in the dtype."""
+    g = torch.Generator().manual_seed(23)
+    K, N = 512, 67
+    W = torch.randn(K, N, generator=g) * 0.02
+    W[torch.rand(W.shape, generator=g) < 0.02] *= 10
+    W[0:32, 0] = torch.randn(32, generator=g) * 1e-7          # fp16 subnormal range
+    W[32:64, 1] = 0.0                                          # zero block -> d = 1
+    # exact ties: amax = 7 * 2^-3 -> d = 2^-3, x = (k + 0.5) d -> x/d + 8 = k + 8.5
+    W[64:96, 2] = torch.tensor([(k % 7 + 0.5) * 0.125 * (1 if k % 2 else -1) for k in range(32)])
+    W[64, 2] = 0.875
+    Wd = W.to(tdtype)
+    dbytes, packed = _torch_reference_quantize(Wd)
+    out = R.quantize_ref_rule(Wd.float().numpy(), name)
+    np.testing.assert_array_equal(out[:, :, 0:2], dbytes)
+    np.testing.assert_array_equal(out[:, :, 2:], packed)
+    # and the dtype matters: the fp32 rule gives other bytes on this data
+    assert not np.array_equal(R.quantize_ref_rule(Wd.float().numpy()), out)
+
+
+def test_quantize_ref_bf16_scale_overflows_fp16():
+    """A bf16 block with amax/7 beyond the fp16 range stores d = inf (the
+    reference's d.to(float16)) while q is still computed with the finite bf16 d."""
+    W = torch.zeros(32, 2, dtype=torch.bfloat16)
+    W[:, 0] = 1e6
+    W[3, 0] = -1e6
+    W[:, 1] = torch.linspace(-3, 3, 32).to(torch.bfloat16)
+    dbytes, packed = _torch_reference_quantize(W)
+    out = R.quantize_ref_rule(W.float().numpy(), "bfloat16")
+    np.testing.assert_array_equal(out[:, :, 0:2], dbytes)
+    np.testing.assert_array_equal(out[:, :, 2:], packed)
+    assert np.isinf(out[0, 0, 0:2].copy().view(np.float16)[0])
+
+
 def test_quantize_rejects_bad_k():
     with pytest.raises(AssertionError, match="divisible by 32"):
         R.quantize_ref_rule(np.zeros((33, 2), np.float32))
@@ -210,3 +264,23 @@ def test_fallback_torch_cpu_matches_dequant_then_matmul():
     X = rng.standard_normal((3, 128)).astype(np.float32)
     Y = R.fallback_torch_cpu(torch.from_numpy(X), torch.from_numpy(blocks)).numpy()
     np.testing.assert_allclose(Y, X @ R.dequantize(blocks, np.float32), rtol=1e-5, atol=1e-6)
+
+
+def test_matmul_xdtype_against_torch_fallback():
+    """The oracle's bf16 / fp32 path equals the reference fallback's steps run by
+    torch on CPU (dequantize to X.dtype, then X @ W) within the output rounding."""
+    g = torch.Generator().manual_seed(5)
+    W = torch.randn(256, 40, generator=g) * 0.02
+    blocks = R.quantize_ref_rule(W.numpy())
+    for tdt, name, tol in ((torch.bfloat16, "bfloat16", 1e-2), (torch.float32, "float32", 1e-6)):
+        X = torch.randn(3, 256, generator=g).to(tdt)
+        want = R.fallback_torch_cpu(X, torch.from_numpy(blocks)).float().numpy()
+        got = R.matmul_xdtype(X.float().numpy(), blocks, name)
+        err = np.abs(got - want).max(axis=1)
+        assert (err <= tol * np.abs(want).max(axis=1)).all()
+    # a wrong weight rounding (fp32 W with bf16 X) is caught at a tighter bar than the output rounding
+    X = torch.randn(2, 256, generator=g).to(torch.bfloat16)
+    Wb = R.dequantize(blocks, np.float32)
+    exact = X.float().numpy().astype(np.float64) @ Wb.astype(np.float64)
+    ref_w = R.matmul_xdtype(X.float().numpy(), blocks, "bfloat16")
+    assert np.abs(ref_w - exact).max() > 0
