@@ -115,6 +115,25 @@ int mcq4_matmul_q4_0(const void *X, int x_dtype, int64_t ldx, const uint8_t *W, 
                      size_t workspace_bytes, void *stream);
 
 /*
+ * Re-zeroes the counter area (the first 256 KiB) of a split-K workspace with a
+ * fill kernel on `stream`.  Every completed call leaves the area zero; a call
+ * that was interrupted (a failed launch, a killed stream) may not, and a
+ * workspace is then reset before its next use.  No counterpart in the
+ * reference (its Metal binding keeps no workspace).
+ */
+int mcq4_reset_workspace(void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Number of split-K tiles, on the current device, whose XCD-local exchange
+ * found a split that ran on another XCD than the summing workgroup and
+ * recomputed that split's partial instead of reading it (the results stay
+ * correct; on MI355X in its default partition mode the count stays 0).
+ * Synchronous (reads device counters); reset != 0 clears them.  Diagnostic
+ * only; no counterpart in the reference.
+ */
+int mcq4_split_fallback_count(uint64_t *count, int reset);
+
+/*
  * Re-reads the library's MCQ4_* test and experiment switches from the
  * environment (they are read once, at the first launch, and never per call).
  * No counterpart in the reference.

@@ -35,6 +35,8 @@ SIGNATURES = {
     "mcq4_matmul_q4_0_f16": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
     "mcq4_matmul_q4_0": (_int, [_p, _int, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
     "mcq4_reload_options": (_int, []),
+    "mcq4_reset_workspace": (_int, [_p, _sz, _p]),
+    "mcq4_split_fallback_count": (_int, [ctypes.POINTER(ctypes.c_uint64), _int]),
     "mcq4_quantize_int4": (_int, [_p, _int, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),
     "mcq4_dequantize_int4": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _p, _i64, _int, _p]),
     "mcq4_matmul_int4_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _int]),
@@ -89,6 +91,13 @@ def reload_options() -> None:
     The library reads them once, at its first launch, and again only here.
     """
     check(lib.mcq4_reload_options(), "mcq4_reload_options")
+
+
+def split_fallback_count(reset: bool = False) -> int:
+    """Split-K tiles recomputed because a split ran on another XCD (current device)."""
+    v = ctypes.c_uint64(0)
+    check(lib.mcq4_split_fallback_count(ctypes.byref(v), int(reset)), "mcq4_split_fallback_count")
+    return int(v.value)
 
 
 def check(status: int, func: str) -> None:

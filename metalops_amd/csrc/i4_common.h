@@ -51,6 +51,25 @@ __device__ __forceinline__ void store_dt(void *p, int64_t i, float v, int dt) {
     else ((uint16_t *)p)[i] = f32_to_bf16_bits(v);
 }
 
+// One output of the per-group INT4 (WB = 4, packed[K/2][N]) or INT8 (WB = 8,
+// int8 [K][N]) product over K rows [k0, k1): sum of x[k] * (q - z) * s in fp32.
+// The split-K recompute path of the XCD-local exchange (q4_common.h): slow,
+// taken only when a split ran on another XCD.
+template <int WB>
+__device__ __forceinline__ float i4_dot_range(const _Float16 *xrow, const uint8_t *P, const void *scales,
+                                           const void *zeros, int sz_dt, int N, int gs, int n, int k0,
+                                           int k1) {
+    float acc = 0.f;
+    for (int k = k0; k < k1; ++k) {
+        float q;
+        if constexpr (WB == 4) q = (float)((P[(int64_t)(k >> 1) * N + n] >> (4 * (k & 1))) & 0xF);
+        else q = (float)(int8_t)P[(int64_t)k * N + n];
+        const int64_t gi = (int64_t)(k / gs) * N + n;
+        acc += (float)xrow[k] * ((q - load_dt(zeros, gi, sz_dt)) * load_dt(scales, gi, sz_dt));
+    }
+    return acc;
+}
+
 // Fused activations of native/quant_kernels.metal: SiLU y / (1 + exp(-y))
 // (:996-998) and the tanh form of GELU (:1126-1132).
 template <int ACT>

@@ -26,6 +26,7 @@ struct I4GemmArgs {
     // stores act(sum) (64-bit tickets [8][4096] by blockIdx.x mod 8 at the
     // workspace start); null: i4_gemm_reduce_kernel.
     uint64_t *tickets = nullptr;
+    uint32_t foreign = 0;    // splits treated as run on another XCD (test switch)
 };
 
 // Sums the S partial tiles per output tile in split order and stores act(sum) as fp16.

@@ -36,6 +36,8 @@
 
 namespace mcq4 {
 
+MCQ4_SPLIT_FALLBACK_COUNTER(i4_gemm6_split_fallbacks)
+
 constexpr int J6_NS = 3;                        // stages (A slots) in flight
 constexpr int J6_ROWB = 128;                    // A bytes per row and stage (2 steps)
 constexpr int J6_BM = 128;
@@ -292,21 +294,40 @@ i4_gemm6_kernel(I4GemmArgs a) {
     if (!a.tickets) return;                       // the reduction kernel sums
     // Both splits of this tile run on this XCD (same blockIdx.x, grid.x a
     // multiple of 8): the second to arrive adds the other's partial from the
-    // XCD's L2 (p0 + p1 either way: fp32 addition commutes).
+    // XCD's L2, p0 + p1 (fp32 addition commutes).
     wait_vmcnt<0>();
     __syncthreads();
     uint64_t *cnt = a.tickets + (bid & 7) * 4096 + (bid >> 3);
     const uint32_t xcc = xcc_id();
     uint32_t *last_flag = (uint32_t *)smem;
     if (tid == 0) {
-        const uint64_t inc = xcd_ticket_inc(xcc);
+        const uint64_t inc = xcd_ticket_inc(xcc, z);
         const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *last_flag = (prev & 0xFF) != 1 ? 0u : xcd_ticket_local(prev + inc, xcc, 2) ? 1u : 2u;
+        // 1: the other split ran on this XCD (read its partial from the L2);
+        // 2: it did not (recompute it here).
+        *last_flag = (prev & 0xFF) != 1 ? 0u : (xcd_ticket_local_mask(prev + inc, xcc, 2) & ~a.foreign) == 3u ? 1u : 2u;
+        if (*last_flag == 2u) note_split_fallback();
     }
     __syncthreads();
     const uint32_t lf = *last_flag;
     if (!lf) return;
-    const float *other = a.partials + ((int64_t)tile_id * 2 + (1 - z)) * (BM * I4G_BN);
+    float *other = a.partials + ((int64_t)tile_id * 2 + (1 - z)) * (BM * I4G_BN);
+    if (lf == 2) {
+        // The other split ran on another XCD: its partial is not in this L2.
+        // Recompute it here into its slot (plain stores, this L2), then read it
+        // back as usual.  One output per thread and pass, nothing unrolled, so
+        // the accumulators stay in their registers.
+        const int o_lo = (int)((int64_t)a.nsteps * (1 - z) / 2) * 32;
+        const int o_hi = (int)((int64_t)a.nsteps * (2 - z) / 2) * 32;
+#pragma unroll 1
+        for (int v = tid; v < BM * I4G_BN; v += 256) {
+            const int m = min(m0 + v / I4G_BN, a.M - 1), nn = min(n0 + v % I4G_BN, N - 1);
+            other[v] = i4_dot_range<4>(a.X + (int64_t)m * a.ldx, a.P, a.scales, a.zeros, SZ, N, a.spg * 32, nn,
+                                       o_lo, o_hi);
+        }
+        wait_vmcnt<0>();
+        __syncthreads();
+    }
     _Float16 *Y = (_Float16 *)a.Y;
     const int n = wcol0 + 2 * lrow;
 #pragma unroll
@@ -324,8 +345,8 @@ i4_gemm6_kernel(I4GemmArgs a) {
             if (m < a.M && n < N) {
                 half2_t v;
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    v[j] = lf == 1 ? (_Float16)activate<ACT>(acc[i][j][r] + o[r][j]) : (_Float16)__builtin_nanf("");
+                for (int j = 0; j < TN; ++j)     // p0 + p1 in split order
+                    v[j] = (_Float16)activate<ACT>(z == 0 ? acc[i][j][r] + o[r][j] : o[r][j] + acc[i][j][r]);
                 *(half2_t *)(Y + (int64_t)m * a.ldy + n) = v;
             }
         }
@@ -401,6 +422,7 @@ hipError_t launch_i4_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *P, con
                            int gs, int act, void *ws, hipStream_t s) {
     const J6Cfg c = i4_gemm6_config(M, K, N);
     I4GemmArgs a;
+    a.foreign = split_foreign_mask();
     a.X = X; a.ldx = ldx; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y; a.ldy = ldy;
     a.M = M; a.nsteps = K / 32; a.N = N; a.spg = gs / 32;
     a.tiles_n = (N + I4G_BN - 1) / I4G_BN;

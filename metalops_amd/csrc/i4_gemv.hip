@@ -44,6 +44,8 @@
 
 namespace mcq4 {
 
+MCQ4_SPLIT_FALLBACK_COUNTER(i4_gemv_split_fallbacks)
+
 // Two tile shapes (template NC = weight columns per lane):
 //   * NC = 8: 128-column tiles (128-byte row pieces), 4 waves per workgroup,
 //     K split over workgroups.  Default.
@@ -75,6 +77,7 @@ struct I4GemvArgs {
     float *part;              // [tiles][S][M][TC] when S > 1
     uint32_t *counters;       // [tiles]; with xl, 64-bit tickets [8][4096] by blockIdx.x mod 8
     int xl;                   // XCD-local split exchange (grid.x a multiple of 8)
+    uint32_t foreign;         // splits treated as run on another XCD (test switch)
 };
 
 // Scales and zeros of the lane's NC columns (fp32 slot layout: TC scales then
@@ -331,7 +334,8 @@ i4_gemv_kernel(I4GemvArgs a) {
     float *part = a.part + ((int64_t)t * a.S + sp) * M * TC;
     if (a.xl) {
         // Every split of this tile runs on this XCD: the partials go through its
-        // L2 (plain stores, L1-bypassing loads); the ticket checks the placement.
+        // L2 (plain stores, L1-bypassing loads); the ticket records each split's
+        // XCD, and a split found elsewhere is recomputed (q4_common.h).
         uint64_t *cnt = (uint64_t *)a.counters + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
         const uint32_t xcc = xcc_id();
         for (int v = tid; v < M * TC; v += IW * 64) {
@@ -345,14 +349,16 @@ i4_gemv_kernel(I4GemvArgs a) {
         __syncthreads();
         uint32_t *last_flag = (uint32_t *)smem;
         if (tid == 0) {
-            const uint64_t inc = xcd_ticket_inc(xcc);
+            const uint64_t inc = xcd_ticket_inc(xcc, sp);
             const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u
-                         : xcd_ticket_local(prev + inc, xcc, a.S) ? 1u : 2u;
+            const uint32_t local = xcd_ticket_local_mask(prev + inc, xcc, a.S) & ~a.foreign;
+            *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u : 0x10000u | local;
+            if ((prev & 0xFF) == (uint64_t)(a.S - 1) && local != (1u << a.S) - 1) note_split_fallback();
         }
         __syncthreads();
         const uint32_t lf = *last_flag;
         if (!lf) return;
+        const uint32_t local = lf & 0xFFFF;        // splits whose partial is in this L2
         const float *base = a.part + (int64_t)t * a.S * M * TC;
         for (int v = tid; v < M * TC; v += IW * 64) {
             const int row = v / TC, cl = v % TC;
@@ -361,13 +367,20 @@ i4_gemv_kernel(I4GemvArgs a) {
                 float pv[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) pv[i] = load_l2_f32(base, (min(q0 + i, a.S - 1) * M * TC + v) * 4);
+                if (local != (1u << a.S) - 1 && col0 + cl < N) {   // splits from another XCD: recompute
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        if (q0 + i < a.S && !((local >> (q0 + i)) & 1))
+                            pv[i] = i4_dot_range<WB>(a.X + (int64_t)row * a.ldx, a.P, a.scales, a.zeros, SZ, N,
+                                                     a.spg * KS, col0 + cl,
+                                                     min((q0 + i) * IW * a.spw, a.nsteps) * KS,
+                                                     min((q0 + i + 1) * IW * a.spw, a.nsteps) * KS);
+                }
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
                     if (q0 + i < a.S) sum += pv[i];
             }
-            if (col0 + cl < N)
-                a.Y[(int64_t)row * a.ldy + col0 + cl] =
-                    lf == 1 ? (_Float16)activate<ACT>(sum) : (_Float16)__builtin_nanf("");
+            if (col0 + cl < N) a.Y[(int64_t)row * a.ldy + col0 + cl] = (_Float16)activate<ACT>(sum);
         }
         if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
@@ -528,7 +541,7 @@ hipError_t launch_i4_gemv(const _Float16 *X, int64_t ldx, const uint8_t *P, cons
     a.X = X; a.ldx = ldx; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y; a.ldy = ldy;
     a.M = M; a.N = N; a.nsteps = K / ks; a.spg = gs / ks;
     a.spw = c.spw; a.S = c.S;
-    a.part = nullptr; a.counters = nullptr;
+    a.part = nullptr; a.counters = nullptr; a.foreign = split_foreign_mask();
     const int ntiles = (N + 16 * c.nc - 1) / (16 * c.nc);
     a.xl = 0;
     if (c.S > 1) {

@@ -36,8 +36,8 @@
 //     tile in split order.  Default (XL): the grid's x extent is a multiple of
 //     8, so every split of a tile has the same linear id mod 8 and runs on one
 //     XCD; the partials go through that XCD's L2 (plain stores, L1-bypassing
-//     loads) and the 64-bit ticket verifies the placement (a violation writes
-//     NaN rather than a wrong sum).  Otherwise agent-scope stores and loads, as
+//     loads); the 64-bit ticket records each split's XCD, and a split found on
+//     another XCD is recomputed by the last arrival rather than read.  Otherwise agent-scope stores and loads, as
 //     in the general INT4 GEMV.  Store act(sum) as fp16.
 //
 // Int8 weights (WB = 8, W int8 [K][N], M <= 16): a step is 32 byte rows (4 KiB,
@@ -52,6 +52,8 @@
 #include "i4_common.h"
 
 namespace mcq4 {
+
+MCQ4_SPLIT_FALLBACK_COUNTER(i4_gemv1_split_fallbacks)
 
 constexpr int I1_W = 8;          // waves per workgroup
 constexpr int I1_TC = 128;       // tile columns
@@ -72,6 +74,7 @@ struct I4Gemv1Args {
     int64_t ldx, ldy;     // row strides of X and Y (elements)
     float *part;          // [tiles][S][M][128] when S > 1
     uint32_t *counters;   // [tiles]
+    uint32_t foreign;     // splits treated as run on another XCD (test switch)
 };
 
 constexpr int I1_SZSLOT = 1024; // scale/zero bytes per group (one 16-byte-per-lane copy)
@@ -330,8 +333,9 @@ i4_gemv1_kernel(I4Gemv1Args a) {
     // Split K: once this workgroup's partial is stored, one lane takes a ticket;
     // the workgroup that draws the last sums every split's partial in split
     // order.  XL: the partials were plain stores into this XCD's L2 (every split
-    // of the tile runs here, which the 64-bit ticket verifies; a violation
-    // writes NaN) and are read back through the L2.  Otherwise they went out
+    // of the tile runs here; the 64-bit ticket records each split's XCD, and a
+    // split found elsewhere is recomputed, q4_common.h) and are read back
+    // through the L2.  Otherwise they went out
     // write-through (agent-scope atomic stores) and come back with L2-bypassing
     // loads.
     wait_vmcnt<0>();
@@ -343,25 +347,37 @@ i4_gemv1_kernel(I4Gemv1Args a) {
         uint64_t *cnt = (uint64_t *)a.counters + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
         const uint32_t xcc = xcc_id();
         if (tid == 0) {
-            const uint64_t inc = xcd_ticket_inc(xcc);
+            const uint64_t inc = xcd_ticket_inc(xcc, sp);
             const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u
-                         : xcd_ticket_local(prev + inc, xcc, a.S) ? 1u : 2u;
+            const uint32_t local = xcd_ticket_local_mask(prev + inc, xcc, a.S) & ~a.foreign;
+            *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u : 0x10000u | local;
+            if ((prev & 0xFF) == (uint64_t)(a.S - 1) && local != (1u << a.S) - 1) note_split_fallback();
         }
         __syncthreads();
         const uint32_t lf = *last_flag;
         if (!lf) return;
+        const uint32_t local = lf & 0xFFFF;        // splits whose partial is in this L2
+        constexpr int KS = 32;                     // K per step (both weight widths)
         for (int v = tid; v < nout; v += I1_W * 64) {
             float sum = 0.f;
             for (int q0 = 0; q0 < a.S; q0 += 8) {
                 float pv[8];
 #pragma unroll
                 for (int i = 0; i < 8; ++i) pv[i] = load_l2_f32(base, (min(q0 + i, a.S - 1) * nout + v) * 4);
+                if (local != (1u << a.S) - 1) {    // splits from another XCD: recompute
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        if (q0 + i < a.S && !((local >> (q0 + i)) & 1))
+                            pv[i] = i4_dot_range<WB>(a.X + (int64_t)(v / I1_TC) * a.ldx, a.P, a.scales, a.zeros,
+                                                     SZ, N, a.spg * KS, col0 + v % I1_TC,
+                                                     min((q0 + i) * I1_W * a.spw, a.nsteps) * KS,
+                                                     min((q0 + i + 1) * I1_W * a.spw, a.nsteps) * KS);
+                }
 #pragma unroll
                 for (int i = 0; i < 8; ++i)
                     if (q0 + i < a.S) sum += pv[i];
             }
-            y_at(v) = lf == 1 ? (_Float16)activate<ACT>(sum) : (_Float16)__builtin_nanf("");
+            y_at(v) = (_Float16)activate<ACT>(sum);
         }
         if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
@@ -518,7 +534,7 @@ hipError_t launch_i4_gemv1(const _Float16 *X, int64_t ldx, const uint8_t *P, con
     a.ngr_max = c.ngr_max;
     a.M = M; a.ldx = ldx; a.ldy = ldy;
     a.wave_bytes = (int)i1_wave_bytes(M, c, wb);
-    a.part = nullptr; a.counters = nullptr;
+    a.part = nullptr; a.counters = nullptr; a.foreign = split_foreign_mask();
     if (c.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.counters = (uint32_t *)ws;

@@ -31,6 +31,12 @@ hipError_t launch_gemm2(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
                         int64_t ldy, int M, int K, int N, hipStream_t s);
 hipError_t launch_quantize_typed(int w_dtype, const void *W, int64_t ldw, int nb, int N,
                                  uint8_t *out, hipStream_t s);
+hipError_t launch_zero_counters(void *ws, hipStream_t s);
+hipError_t q4_gemvm_split_fallbacks(uint64_t *count, bool reset);
+hipError_t q4_gemm6_split_fallbacks(uint64_t *count, bool reset);
+hipError_t i4_gemv_split_fallbacks(uint64_t *count, bool reset);
+hipError_t i4_gemv1_split_fallbacks(uint64_t *count, bool reset);
+hipError_t i4_gemm6_split_fallbacks(uint64_t *count, bool reset);
 hipError_t launch_q4_xact(const void *X, int x_dt, int64_t ldx, const uint8_t *W, void *Y,
                           int64_t ldy, int64_t M, int64_t K, int64_t N, hipStream_t s);
 }  // namespace mcq4
@@ -239,6 +245,28 @@ int mcq4_matmul_q4_0(const void *X, int x_dtype, int64_t ldx, const uint8_t *W, 
     (void)workspace; (void)workspace_bytes;
     return hip_status(mcq4::launch_q4_xact(X, x_dtype, ldx, W, Y, ldy, M, K, N, (hipStream_t)stream),
                       "matmul launch");
+}
+
+int mcq4_reset_workspace(void *workspace, size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    if (!workspace) return fail(MCQ4_ERR_INVALID_ARG, "null workspace");
+    if (workspace_bytes < mcq4::COUNTER_BYTES)
+        return fail(MCQ4_ERR_WORKSPACE, "workspace of %zu bytes is smaller than its %zu-byte counter area",
+                    workspace_bytes, (size_t)mcq4::COUNTER_BYTES);
+    if (!aligned(workspace, 16)) return fail(MCQ4_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
+    return hip_status(mcq4::launch_zero_counters(workspace, (hipStream_t)stream), "workspace reset launch");
+}
+
+int mcq4_split_fallback_count(uint64_t *count, int reset) {
+    g_err[0] = 0;
+    if (!count) return fail(MCQ4_ERR_INVALID_ARG, "null pointer");
+    *count = 0;
+    hipError_t (*const readers[])(uint64_t *, bool) = {
+        mcq4::q4_gemvm_split_fallbacks, mcq4::q4_gemm6_split_fallbacks, mcq4::i4_gemv_split_fallbacks,
+        mcq4::i4_gemv1_split_fallbacks, mcq4::i4_gemm6_split_fallbacks};
+    for (auto rd : readers)
+        if (int st = hip_status(rd(count, reset != 0), "split fallback counter")) return st;
+    return MCQ4_OK;
 }
 
 }  // extern "C"

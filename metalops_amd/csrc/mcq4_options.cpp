@@ -22,6 +22,7 @@ const char *const kNames[] = {
     "MCQ4_GEMVM_SPLIT",     // 1 | 2 | 4 | 8: K splits of the batched decode GEMV
     "MCQ4_DECODE_PATH",     // direct: the register-load decode kernel
     "MCQ4_GEMM2_BM",        // 128 | 256: row tile of the fallback prefill kernel
+    "MCQ4_SPLIT_FOREIGN",   // mask: split-K splits treated as run on another XCD (recompute path)
     // per-group INT4 / INT8 path
     "MCQ4_I4_PATH",         // generic: the general kernel for everything
     "MCQ4_I4_GEMV1",        // 0 | 1 | 4 | 8: async-copy decode GEMV routing
@@ -64,6 +65,10 @@ const char *opt(const char *name) {
     for (int i = 0; i < kN; ++i)
         if (strcmp(kNames[i], name) == 0) return s->set[i] ? s->value[i].c_str() : nullptr;
     return nullptr;
+}
+uint32_t split_foreign_mask() {
+    const char *v = opt("MCQ4_SPLIT_FOREIGN");
+    return v ? (uint32_t)strtoul(v, nullptr, 0) : 0u;
 }
 }  // namespace mcq4
 

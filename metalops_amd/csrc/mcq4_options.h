@@ -4,6 +4,8 @@
 // the last (re)load, or nullptr when it was unset.
 #pragma once
 
+#include <stdint.h>
+
 namespace mcq4 {
 const char *opt(const char *name);
 // True when the named switch is set and its value starts with `c`.
@@ -11,4 +13,8 @@ inline bool opt_is(const char *name, char c) {
     const char *v = opt(name);
     return v && v[0] == c;
 }
+// Splits of an XCD-local split-K exchange that the kernels treat as having run
+// on another XCD (bit q = split q): MCQ4_SPLIT_FOREIGN, a test switch that
+// drives the recompute path on hardware where the placement always holds.
+uint32_t split_foreign_mask();
 }  // namespace mcq4

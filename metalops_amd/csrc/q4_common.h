@@ -65,22 +65,70 @@ __device__ __forceinline__ void wait_vmcnt() {
 // share an XCD and its L2.  Partials exchanged among them can stay in that L2:
 // plain stores (L1 is write-through), then L1-bypassing loads, instead of
 // write-through stores and loads that go to memory.  The arrival ticket stays
-// a device-coherent atomic, and each arrival also adds 1 to its XCD's 5-bit
-// field (bits 8 + 5x), so the last arrival can check that every split ran on
-// its own XCD.
+// a device-coherent atomic.  Split sp adds 1 + (xcc << (8 + 3 sp)): bits 0..7
+// count the arrivals and the 3-bit field of each split records the XCD it ran
+// on (S <= 16 splits fit in 56 bits).  The last arrival reads the partials of
+// the splits that ran on its own XCD from its L2; should the placement ever
+// differ (another partition mode or part), a split from another XCD is not
+// read -- its partial sits in that XCD's L2 -- but recomputed from the inputs
+// by the last arrival itself, and the file's fallback counter is raised.
+constexpr int XCD_SPLIT_MAX = 16;
 __device__ __forceinline__ uint32_t xcc_id() {
     uint32_t x;
     asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
     return x & 7;
 }
-__device__ __forceinline__ uint64_t xcd_ticket_inc(uint32_t xcc) {
-    return 1ull + (1ull << (8 + 5 * xcc));
+__host__ __device__ __forceinline__ uint64_t xcd_ticket_inc(uint32_t xcc, int sp) {
+    return 1ull + ((uint64_t)xcc << (8 + 3 * sp));
 }
-// True when all `S` arrivals counted in `total` (ticket value after the last
-// one) came from XCD `xcc`.
-__device__ __forceinline__ bool xcd_ticket_local(uint64_t total, uint32_t xcc, int S) {
-    return ((total >> (8 + 5 * xcc)) & 31) == (uint64_t)S;
+// Bit q set when split q (< S) of the completed ticket `total` ran on XCD `xcc`.
+__host__ __device__ __forceinline__ uint32_t xcd_ticket_local_mask(uint64_t total, uint32_t xcc, int S) {
+    uint32_t m = 0;
+    for (int q = 0; q < S; ++q)
+        if (((total >> (8 + 3 * q)) & 7) == xcc) m |= 1u << q;
+    return m;
 }
+
+// Per-file count of split-K tiles whose partials had to be recomputed (the
+// placement above did not hold), readable from the host.  Each translation unit
+// that uses the exchange instantiates it once with its reader's name.
+#define MCQ4_SPLIT_FALLBACK_COUNTER(reader)                                                  \
+    static __device__ unsigned long long g_split_fallbacks;                                  \
+    __device__ __forceinline__ void note_split_fallback() {                                  \
+        __hip_atomic_fetch_add(&g_split_fallbacks, 1ull, __ATOMIC_RELAXED,                   \
+                               __HIP_MEMORY_SCOPE_AGENT);                                    \
+    }                                                                                        \
+    hipError_t reader(uint64_t *count, bool reset) {                                         \
+        unsigned long long v = 0;                                                            \
+        hipError_t e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_split_fallbacks), sizeof(v));    \
+        if (e == hipSuccess && reset) {                                                      \
+            const unsigned long long z = 0;                                                  \
+            e = hipMemcpyToSymbol(HIP_SYMBOL(g_split_fallbacks), &z, sizeof(z));             \
+        }                                                                                    \
+        *count += v;                                                                         \
+        return e;                                                                            \
+    }
+
+// One output of the q4_0 product over K blocks [kb0, kb1): sum of x[k] times
+// the fp16 weight (q - 8)*d, in fp32 -- the split-K recompute path of the
+// exchange above (slow, taken only when a split ran on another XCD).
+__device__ __forceinline__ float q4_dot_range(const _Float16 *xrow, const uint8_t *W, int N, int n,
+                                                  int kb0, int kb1) {
+    float acc = 0.f;
+    for (int kb = kb0; kb < kb1; ++kb) {
+        const uint16_t *b = (const uint16_t *)(W + ((int64_t)kb * N + n) * BLOCK_BYTES);
+        const float d = (float)__builtin_bit_cast(_Float16, b[0]);
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t w = b[1 + i];
+            for (int e = 0; e < 4; ++e) {
+                const _Float16 wv = (_Float16)((float)((int)((w >> (4 * e)) & 0xF) - 8) * d);
+                acc += (float)xrow[kb * QK + 4 * i + e] * (float)wv;
+            }
+        }
+    }
+    return acc;
+}
+
 // fp32 load at byte offset `off` from the workgroup-uniform `base`, bypassing
 // L1 (sc0) so it is served by the XCD's L2.
 __device__ __forceinline__ float load_l2_f32(const float *base, int off) {

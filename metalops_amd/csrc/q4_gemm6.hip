@@ -30,6 +30,8 @@
 
 namespace mcq4 {
 
+MCQ4_SPLIT_FALLBACK_COUNTER(q4_gemm6_split_fallbacks)
+
 constexpr int G6_NS = 3;                       // stages (A slots) in flight
 constexpr int G6_ROWB = 128;                   // A bytes per row and stage (2 steps)
 constexpr int G6_WN = 64;                      // columns per wave
@@ -278,21 +280,39 @@ q4_gemm6_kernel(Gemm6Args a) {
     if (!a.tickets) return;                       // the reduce kernel sums
     // Both splits of this tile run on this XCD (same blockIdx.x, grid.x a
     // multiple of 8): the partials stay in its L2.  The second to arrive adds
-    // the other's partial (p0 + p1 either way: fp32 addition commutes).
+    // the other's partial, p0 + p1 (fp32 addition commutes, so the order of
+    // arrival does not matter).
     wait_vmcnt<0>();
     __syncthreads();
     uint64_t *cnt = a.tickets + (bid & 7) * 4096 + (bid >> 3);
     const uint32_t xcc = xcc_id();
     uint32_t *last_flag = (uint32_t *)smem;
     if (tid == 0) {
-        const uint64_t inc = xcd_ticket_inc(xcc);
+        const uint64_t inc = xcd_ticket_inc(xcc, z);
         const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *last_flag = (prev & 0xFF) != 1 ? 0u : xcd_ticket_local(prev + inc, xcc, 2) ? 1u : 2u;
+        // 1: the other split ran on this XCD (read its partial from the L2);
+        // 2: it did not (recompute it here).
+        *last_flag = (prev & 0xFF) != 1 ? 0u : (xcd_ticket_local_mask(prev + inc, xcc, 2) & ~a.foreign) == 3u ? 1u : 2u;
+        if (*last_flag == 2u) note_split_fallback();
     }
     __syncthreads();
     const uint32_t lf = *last_flag;
     if (!lf) return;
-    const float *other = a.partials + ((int64_t)tile_id * 2 + (1 - z)) * (BM * G6_BN);
+    float *other = a.partials + ((int64_t)tile_id * 2 + (1 - z)) * (BM * G6_BN);
+    if (lf == 2) {
+        // The other split ran on another XCD: its partial is not in this L2.
+        // Recompute it here into its slot (plain stores, this L2), then read it
+        // back as usual.  One output per thread and pass, nothing unrolled, so
+        // the accumulators stay in their registers.
+        const int o_lo = (int)((int64_t)a.nb * (1 - z) / 2), o_hi = (int)((int64_t)a.nb * (2 - z) / 2);
+#pragma unroll 1
+        for (int v = tid; v < BM * G6_BN; v += 256) {
+            const int m = min(m0 + v / G6_BN, a.M - 1), n = min(n0 + v % G6_BN, a.N - 1);
+            other[v] = q4_dot_range(a.X + (int64_t)m * a.ldx, a.W, a.N, n, o_lo, o_hi);
+        }
+        wait_vmcnt<0>();
+        __syncthreads();
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -307,7 +327,8 @@ q4_gemm6_kernel(Gemm6Args a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int m = m0 + wm * WM + i * 32 + 8 * (r >> 2) + rsub + (r & 3), n = n0 + nl;
-                const float v = lf == 1 ? acc[i][j][r] + o[r] : __builtin_nanf("");
+                // p0 + p1 in split order
+                const float v = z == 0 ? acc[i][j][r] + o[r] : o[r] + acc[i][j][r];
                 if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (_Float16)v;
             }
         }
@@ -375,6 +396,7 @@ hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
     a.tiles_m = (M + G6_BM - 1) / G6_BM;
     a.S = gemm6_splits(M, K, N);
     a.partials = nullptr;
+    a.foreign = split_foreign_mask();
     if (a.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.partials = (float *)((char *)ws + COUNTER_BYTES);

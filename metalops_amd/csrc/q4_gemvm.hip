@@ -25,6 +25,8 @@
 
 namespace mcq4 {
 
+MCQ4_SPLIT_FALLBACK_COUNTER(q4_gemvm_split_fallbacks)
+
 constexpr int GM_B = 8;                      // K blocks per item
 constexpr int GM_ROW = 288;                  // strip bytes per K block (16 columns)
 constexpr int GM_WCH = GM_B * 18;            // 144 strip chunks per item
@@ -45,6 +47,7 @@ struct GemvMArgs {
     // last split of each workgroup sums the partials (64-bit tickets [8][4096]
     // by blockIdx.x mod 8 at the workspace start); null: the reduction kernel.
     uint64_t *tickets;
+    uint32_t foreign;    // splits treated as run on another XCD (test switch)
 };
 
 // RB row blocks of 16 activation rows (M <= 16 RB): each K-block row's B
@@ -234,13 +237,16 @@ q4_gemvm_kernel(GemvMArgs a) {
     const uint32_t xcc = xcc_id();
     uint32_t *last_flag = (uint32_t *)smem;       // the ring is idle from here
     if (tid == 0) {
-        const uint64_t inc = xcd_ticket_inc(xcc);
+        const uint64_t inc = xcd_ticket_inc(xcc, sp);
         const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u : xcd_ticket_local(prev + inc, xcc, a.S) ? 1u : 2u;
+        const uint32_t local = xcd_ticket_local_mask(prev + inc, xcc, a.S) & ~a.foreign;
+        *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u : 0x10000u | local;
+        if ((prev & 0xFF) == (uint64_t)(a.S - 1) && local != (1u << a.S) - 1) note_split_fallback();
     }
     __syncthreads();
     const uint32_t lf = *last_flag;
     if (!lf) return;
+    const uint32_t local = lf & 0xFFFF;            // splits whose partial is in this L2
     const int64_t pstride = (int64_t)a.M * 16 * a.ntiles;         // floats per split
     for (int v = tid; v < TPW * 256 * RB; v += WAVES * 64) {   // v = (rb, j, row, col)
         const int j = (v >> 8) % TPW, rr = 16 * (v / (256 * TPW)) + ((v >> 4) & 15), col = v & 15;
@@ -255,13 +261,20 @@ q4_gemvm_kernel(GemvMArgs a) {
         float pv[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q)
-            pv[q] = q < a.S && (RB > 1 || q != sp)
+            pv[q] = q < a.S && (RB > 1 || q != sp) && ((local >> q) & 1)
                         ? load_l2_f32(a.part, (int)(((int64_t)q * pstride + (base - a.part)) * 4)) : own;
+        if (local != (1u << a.S) - 1) {            // splits from another XCD: recompute
+#pragma unroll
+            for (int q = 0; q < 8; ++q)
+                if (q < a.S && !((local >> q) & 1))
+                    pv[q] = q4_dot_range(a.X + (int64_t)rr * a.ldx, a.W, a.N, n, min(q * a.bps * GM_B, a.nb),
+                                         min((q + 1) * a.bps * GM_B, a.nb));
+        }
         float t = 0.f;
 #pragma unroll
         for (int q = 0; q < 8; ++q)
             if (q < a.S) t += pv[q];
-        a.Y[(int64_t)rr * a.ldy + n] = lf == 1 ? (_Float16)t : (_Float16)__builtin_nanf("");
+        a.Y[(int64_t)rr * a.ldy + n] = (_Float16)t;
     }
     if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -375,6 +388,7 @@ hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
     a.S = p.S; a.bps = p.bps;
     a.part = nullptr;
     a.tickets = nullptr;
+    a.foreign = split_foreign_mask();
     if (p.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.part = (float *)((char *)ws + COUNTER_BYTES);

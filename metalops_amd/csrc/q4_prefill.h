@@ -24,9 +24,7 @@ struct Gemm6Args {
     // second split of a tile to finish adds the first's partial and stores Y
     // (64-bit tickets [8][4096] by blockIdx.x mod 8 at the workspace start).
     uint64_t *tickets = nullptr;
-    // Device flag raised when an XCD-local exchange found its splits on
-    // different XCDs (the tile is then summed through memory instead).
-    uint32_t *placement_flag = nullptr;
+    uint32_t foreign = 0;    // splits treated as run on another XCD (test switch)
 };
 
 // Needs N % 128 == 0, 16-byte aligned W and activation rows, K >= 32.

@@ -162,3 +162,21 @@ hipError_t launch_dequant(const uint8_t *blocks, int nb, int N, void *out, int64
 }
 
 }  // namespace mcq4
+
+// ---- workspace counter area -------------------------------------------------
+namespace mcq4 {
+
+// Zero-fills `n16` 16-byte words (a kernel rather than hipMemsetAsync, so the
+// call can sit in a captured HIP graph).
+__global__ void __launch_bounds__(256) zero16_kernel(uint4_t *p, int64_t n16) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n16) p[i] = uint4_t{0u, 0u, 0u, 0u};
+}
+
+hipError_t launch_zero_counters(void *ws, hipStream_t s) {
+    const int64_t n16 = (int64_t)COUNTER_BYTES / 16;
+    hipLaunchKernelGGL(zero16_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s, (uint4_t *)ws, n16);
+    return hipGetLastError();
+}
+
+}  // namespace mcq4

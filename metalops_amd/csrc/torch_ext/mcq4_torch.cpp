@@ -8,7 +8,7 @@
 // zero-filled once (every call leaves its counters zero).
 #include <torch/extension.h>
 #include <c10/hip/HIPStream.h>
-#include <c10/hip/HIPGuard.h>
+#include <c10/core/DeviceGuard.h>
 
 #include <map>
 #include <mutex>
@@ -48,7 +48,7 @@ torch::Tensor matmul_ggml_q4_0(torch::Tensor X, torch::Tensor W_blocks) {
     auto Y = torch::empty({M, N}, x.options());
     if (M == 0 || N == 0) return Y;
     if (K == 0) return Y.zero_();
-    c10::hip::HIPGuard guard(x.device());
+    const c10::DeviceGuard guard(x.device());   // generic: torch labels ROCm devices "cuda"
     hipStream_t stream = c10::hip::getCurrentHIPStream(x.get_device()).stream();
     const size_t need = mcq4_matmul_workspace_bytes(M, K, N);
     torch::Tensor ws;

@@ -222,12 +222,12 @@ def _matmul(X, W_packed, scales, zeros, group_size, act):
             xdt = _DT[x.dtype]
             need = int(_lib.lib.mcq4_matmul_int4_workspace_bytes(M, K, N, group_size, xdt))
             stream = _stream(x.device)
-            ws_ptr, ws_bytes = None, 0
+            ws, ws_ptr, ws_bytes = None, None, 0
             if need:
                 ws = _workspace.get(x.device, stream, need)
                 ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
             fn = getattr(_lib.lib, _FN[act])
-            with torch.cuda.device(x.device):
+            with torch.cuda.device(x.device), _workspace.guard(ws, stream):
                 _lib.check(fn(x.data_ptr(), xdt, x.stride(0), p.data_ptr(), s.data_ptr(),
                               z.data_ptr(), _DT[s.dtype], Y.data_ptr(), N, M, K, N, group_size,
                               ws_ptr, ws_bytes, stream),
@@ -302,7 +302,7 @@ def fused_rmsnorm_linear_int4(X, W_norm, W_packed, scales, zeros, eps, group_siz
     stream = _stream(x.device)
     ws = _workspace.get(x.device, stream, need + 256)
     base = (ws.data_ptr() + 255) // 256 * 256
-    with torch.cuda.device(x.device):
+    with torch.cuda.device(x.device), _workspace.guard(ws, stream, base):
         _lib.check(_lib.lib.mcq4_fused_rmsnorm_linear_int4(
             x.data_ptr(), x.stride(0), wn.data_ptr(), float(eps), p.data_ptr(), s.data_ptr(),
             z.data_ptr(), _DT[s.dtype], Y.data_ptr(), N, M, K, N, group_size, base,
@@ -351,11 +351,11 @@ def matmul_int8(
             xdt = _DT[x.dtype]
             need = int(_lib.lib.mcq4_matmul_int8_workspace_bytes(M, K, N, group_size, xdt))
             stream = _stream(x.device)
-            ws_ptr, ws_bytes = None, 0
+            ws, ws_ptr, ws_bytes = None, None, 0
             if need:
                 ws = _workspace.get(x.device, stream, need)
                 ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
-            with torch.cuda.device(x.device):
+            with torch.cuda.device(x.device), _workspace.guard(ws, stream):
                 _lib.check(_lib.lib.mcq4_matmul_int8(x.data_ptr(), xdt, x.stride(0), w.data_ptr(),
                                                      s.data_ptr(), z.data_ptr(), _DT[s.dtype],
                                                      Y.data_ptr(), N, M, K, N, group_size, ws_ptr,

@@ -16,6 +16,7 @@ and returns without synchronising, like the reference's Metal binding
 """
 from __future__ import annotations
 
+import contextlib
 import threading
 from typing import Optional
 
@@ -140,7 +141,9 @@ class _Workspace:
     """Per-device, zero-initialised split-K workspace reused across calls.
 
     The kernels leave the arrival counters at zero after every call, so the
-    buffer is zero-filled once when (re)allocated and never cleared again.
+    buffer is zero-filled once when (re)allocated; a call that fails is
+    followed by a reset of its counter area on the same stream (``guard``),
+    so an interrupted call cannot poison later ones.
     One buffer per (device, stream), so concurrent streams never share one; a
     larger request allocates a new buffer through PyTorch's stream-ordered
     caching allocator.
@@ -159,6 +162,17 @@ class _Workspace:
                 buf = torch.zeros(size, dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
+
+    @contextlib.contextmanager
+    def guard(self, buf: Optional[torch.Tensor], stream: int, base: Optional[int] = None):
+        """Resets the counter area at ``base`` (default: the buffer's start) if the body raises."""
+        try:
+            yield
+        except Exception:
+            if buf is not None:
+                ptr = buf.data_ptr() if base is None else base
+                _lib.lib.mcq4_reset_workspace(ptr, buf.numel() - (ptr - buf.data_ptr()), stream)
+            raise
 
 
 _workspace = _Workspace()
@@ -209,11 +223,11 @@ def matmul_ggml_q4_0(X: torch.Tensor, W_blocks: torch.Tensor) -> torch.Tensor:
         if x.data_ptr() % 16:
             x = x.clone()
     need = int(_lib.lib.mcq4_matmul_workspace_bytes(M, K, N))
-    ws_ptr, ws_bytes = None, 0
+    ws, ws_ptr, ws_bytes = None, None, 0
     if need:
         ws = _workspace.get(x.device, stream, need)
         ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
-    with torch.cuda.device(x.device):
+    with torch.cuda.device(x.device), _workspace.guard(ws, stream):
         _lib.check(_lib.lib.mcq4_matmul_q4_0_f16(x.data_ptr(), x.stride(0), w.data_ptr(),
                                                  Y.data_ptr(), N, M, K, N, ws_ptr, ws_bytes,
                                                  stream),

@@ -1,0 +1,93 @@
+"""Split-K exchange when a split ran on another XCD.
+
+On MI355X the placement the XCD-local exchange relies on always holds, so the
+recompute path (the last arrival recomputes a split whose partial sits in
+another XCD's L2) is driven here by the test switch MCQ4_SPLIT_FOREIGN, which
+makes the kernels treat the masked splits as foreign.  Each kernel that uses the
+exchange must then still give the oracle's result (the recompute sums in fp32
+too, so results stay within the usual bar of the default path's), and the
+library's fallback counter must count the recomputed tiles.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import int4_ref as R4
+from oracle import q4_0_ref as R
+
+pytestmark = pytest.mark.gpu
+
+
+def _rows_close(Y, Yref, tol=1e-2):
+    Y = np.asarray(Y, np.float64)
+    Yref = np.asarray(Yref, np.float64)
+    assert np.isfinite(Y).all()
+    err = np.abs(Y - Yref).max(axis=1)
+    assert (err <= tol * np.abs(Yref).max(axis=1)).all(), f"max err {err.max()}"
+
+
+def _q4_case(dev, M, K, N):
+    import metalops_amd as mo
+    g = torch.Generator().manual_seed(M + K + N)
+    W = torch.randn(K, N, generator=g) * 0.02
+    X = torch.randn(M, K, generator=g).half()
+    blocks = R.quantize_llama_rule(W.numpy())
+    b = torch.from_numpy(blocks).to(dev)
+    return (lambda: mo.matmul_ggml_q4_0(X.to(dev), b)), R.matmul_f32(X.numpy(), blocks)
+
+
+def _i4_case(dev, M, K, N, gs, wb):
+    import metalops_amd as mo
+    g = torch.Generator().manual_seed(M + K + N)
+    X = torch.randn(M, K, generator=g).half().to(dev)
+    if wb == 4:
+        W = (torch.randn(K, N, generator=g) * 0.02).half().to(dev)    # fp16 scales/zeros
+        p, s, z = mo.quantize_int4(W, gs)
+        Yref = R4.matmul_f32(X.float().cpu().numpy(), p.cpu().numpy(), s.float().cpu().numpy(),
+                             z.float().cpu().numpy(), gs)
+        return (lambda: mo.matmul_int4(X, p, s, z, gs)), Yref
+    q = torch.randint(-128, 128, (K, N), generator=g, dtype=torch.int8)
+    s = (torch.rand(K // gs, N, generator=g) * 0.02).half()
+    z = torch.randint(-4, 4, (K // gs, N), generator=g).half()
+    Yref = R4.matmul_int8_f32(X.float().cpu().numpy(), q.numpy(), s.float().numpy(), z.float().numpy(), gs)
+    args = [t.to(dev) for t in (q, s, z)]
+    return (lambda: mo.matmul_int8(X, *args, gs)), Yref
+
+
+CASES = [
+    # (name, environment, case builder args)
+    ("q4_gemvm_s2", {"MCQ4_GEMVM_SPLIT": "2"}, ("q4", 16, 14336, 4096)),
+    ("q4_gemvm_s8", {"MCQ4_GEMVM_SPLIT": "8"}, ("q4", 12, 2048, 1032)),
+    ("q4_gemm6_s2", {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "2"}, ("q4", 300, 4096, 640)),
+    ("i4_gemv1", {}, ("i4", 1, 4096, 4096, 128, 4)),
+    ("i4_gemv1_mr", {}, ("i4", 8, 11008, 4096, 128, 4)),
+    ("i4_gemv", {"MCQ4_I4_GEMV1": "0"}, ("i4", 4, 4096, 1040, 64, 4)),
+    ("i8_gemv", {"MCQ4_I4_GEMV1": "0"}, ("i4", 8, 4096, 1024, 128, 8)),
+    ("i4_gemm6_s2", {}, ("i4", 2048, 14336, 4096, 128, 4)),
+]
+
+
+@pytest.mark.parametrize("name,env,case", CASES, ids=[c[0] for c in CASES])
+def test_split_recompute_path(dev, monkeypatch, name, env, case):
+    from metalops_amd import _lib
+    print(f"split recompute {name} {case}", flush=True)
+    for k in ("MCQ4_GEMVM_SPLIT", "MCQ4_GEMM_PATH", "MCQ4_GEMM6_SPLIT", "MCQ4_I4_GEMV1", "MCQ4_XCD_LOCAL",
+              "MCQ4_SPLIT_FOREIGN", "MCQ4_I4_PATH", "MCQ4_I4_SPW1"):
+        monkeypatch.delenv(k, raising=False)
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    fn, Yref = _q4_case(dev, *case[1:]) if case[0] == "q4" else _i4_case(dev, *case[1:])
+    Y = fn()
+    torch.cuda.synchronize()
+    base = _lib.split_fallback_count(reset=True)
+    assert base == 0, "the default placement should never need the recompute path"
+    monkeypatch.setenv("MCQ4_SPLIT_FOREIGN", "0xffff")
+    Yf = fn()
+    torch.cuda.synchronize()
+    assert _lib.split_fallback_count(reset=True) > 0, "the recompute path did not run"
+    monkeypatch.delenv("MCQ4_SPLIT_FOREIGN")
+    _rows_close(Y.float().cpu().numpy(), Yref)
+    _rows_close(Yf.float().cpu().numpy(), Yref)
+    # and the next default call is unaffected (counters left zero)
+    Y2 = fn()
+    assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
