@@ -102,6 +102,23 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y,
                          void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Allocation-free variant of mcq4_matmul_q4_0_f16.  No counterpart in the
+ * reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments minus the workspace: the split-K workspace is the library's own
+ * device array (one per GPU, held until the process ends) of
+ * mcq4_matmul_noalloc_max_workspace_bytes() bytes (256 KiB of counters +
+ * 64 MiB); a shape whose mcq4_matmul_workspace_bytes exceeds it returns
+ * MCQ4_ERR_WORKSPACE.  Calls allocate nothing (no hipMalloc / hipFree, no
+ * allocating library routine).  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (two streams, two threads) race and give wrong
+ * results; serialise them.  Results are bit-identical to mcq4_matmul_q4_0_f16.
+ */
+int mcq4_matmul_q4_0_f16_noalloc(const void *X, int64_t ldx, const uint8_t *W, void *Y,
+                                 int64_t ldy, int64_t M, int64_t K, int64_t N, void *stream);
+size_t mcq4_matmul_noalloc_max_workspace_bytes(void);
+
+/*
  * matmul_ggml_q4_0 for activations of any float dtype (quantization.py:422-454).
  * x_dtype MCQ4_DTYPE_F16 is mcq4_matmul_q4_0_f16 (the fp16 MFMA kernels, the
  * semantics of the reference's GPU binding, core_mps.mm:5917-5975).

@@ -35,6 +35,8 @@ SIGNATURES = {
     "mcq4_matmul_q4_0_f16": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
     "mcq4_matmul_q4_0": (_int, [_p, _int, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
     "mcq4_reload_options": (_int, []),
+    "mcq4_matmul_q4_0_f16_noalloc": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p]),
+    "mcq4_matmul_noalloc_max_workspace_bytes": (_sz, []),
     "mcq4_reset_workspace": (_int, [_p, _sz, _p]),
     "mcq4_split_fallback_count": (_int, [ctypes.POINTER(ctypes.c_uint64), _int]),
     "mcq4_quantize_int4": (_int, [_p, _int, _i64, _i64, _i64, _i64, _p, _p, _p, _p]),

@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -90,6 +92,38 @@ int check_kn(int64_t K, int64_t N) {
     if (K / 32 > kMaxBlocksK || N > kMaxDim || (K / 32) * N * 18 > ((int64_t)1 << 40))
         return fail(MCQ4_ERR_SHAPE, "shape K=%lld N=%lld exceeds the supported size",
                     (long long)K, (long long)N);
+    return MCQ4_OK;
+}
+
+// Scratch of the allocation-free matmul entry point: one split-K workspace per
+// GPU in the library's own device memory (zero at load; every completed call
+// leaves its counter area zero again).  Host code uses only the per-device
+// address from hipGetSymbolAddress, never the array's name.
+constexpr size_t kNoAllocScratchBytes = mcq4::COUNTER_BYTES + ((size_t)64 << 20);
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::atomic<void *> g_scratch[kMaxDevices];
+std::atomic<bool> g_scratch_dirty[kMaxDevices];   // a failed call may have left counters set
+std::mutex g_scratch_mu;
+
+// The current device's scratch address, resolved once per device.
+int scratch_ptr(void **out, int *dev_out) {
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev)) return hip_status(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxDevices) return fail(MCQ4_ERR_INVALID_ARG, "device %d out of range", dev);
+    void *p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_acquire);
+        if (!p) {
+            if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)))
+                return hip_status(e, "hipGetSymbolAddress(scratch)");
+            if (!p) return fail(MCQ4_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    *dev_out = dev;
     return MCQ4_OK;
 }
 
@@ -267,6 +301,32 @@ int mcq4_split_fallback_count(uint64_t *count, int reset) {
     for (auto rd : readers)
         if (int st = hip_status(rd(count, reset != 0), "split fallback counter")) return st;
     return MCQ4_OK;
+}
+
+size_t mcq4_matmul_noalloc_max_workspace_bytes(void) { return kNoAllocScratchBytes; }
+
+int mcq4_matmul_q4_0_f16_noalloc(const void *X, int64_t ldx, const uint8_t *W, void *Y, int64_t ldy,
+                                 int64_t M, int64_t K, int64_t N, void *stream) {
+    g_err[0] = 0;
+    if (M > 0 && K > 0 && N > 0 && K % 32 == 0) {
+        const size_t need = mcq4_matmul_workspace_bytes(M, K, N);
+        if (need > kNoAllocScratchBytes)
+            return fail(MCQ4_ERR_WORKSPACE,
+                        "shape M=%lld K=%lld N=%lld needs a %zu-byte workspace; the allocation-free entry "
+                        "point holds at most %zu (use mcq4_matmul_q4_0_f16 with a caller workspace)",
+                        (long long)M, (long long)K, (long long)N, need, kNoAllocScratchBytes);
+    }
+    void *ws = nullptr;
+    int dev = 0;
+    if (int st = scratch_ptr(&ws, &dev)) return st;
+    if (g_scratch_dirty[dev].load(std::memory_order_acquire)) {
+        if (int st = hip_status(mcq4::launch_zero_counters(ws, (hipStream_t)stream), "scratch reset launch"))
+            return st;
+        g_scratch_dirty[dev].store(false, std::memory_order_release);
+    }
+    const int st = mcq4_matmul_q4_0_f16(X, ldx, W, Y, ldy, M, K, N, ws, kNoAllocScratchBytes, stream);
+    if (st == MCQ4_ERR_HIP) g_scratch_dirty[dev].store(true, std::memory_order_release);
+    return st;
 }
 
 }  // extern "C"
