@@ -11,7 +11,14 @@ Metric: q4_0 GEMV GB/s (% HBM peak) at M=1; q4_0 GEMM TFLOP/s
   the layer's weights (1.14 GB, beyond the 256 MB Infinity Cache) are rotated
   so reads come from HBM.  Steps are replayed from a HIP graph; the timed region
   is bracketed by HIP events recorded on the stream the kernels run on.
-* ``prefill``: the M=2048 GEMM configs (4096x14336 and 14336x4096) in TFLOP/s.
+* ``prefill``: the M=2048 GEMM configs (configs[3]: 4096x14336 and 14336x4096)
+  in TFLOP/s, with the same keys as the top level (``value``, ``unit``,
+  ``roofline``, ``cpu_baseline``).
+* ``configs``: every other BASELINE config point -- configs[0] (M=1 4096x4096),
+  configs[2] (M = 4, 8, 16 on 4096x14336 and 14336x4096) and configs[4]
+  (lm_head 4096x128256 and the ragged down 11008x4096 at M = 1 and 512): GB/s
+  and % of HBM peak for M <= 16, TFLOP/s and % of the fp16 MFMA peak for M >= 512.
+  Each is a graph of launches over weight copies rotated through >= 1 GB.
 * ``cpu_baseline``: the reference's CPU path (dequantize to fp16 on every call,
   then ``X @ W``; quantization.py:452-454) restated in oracle/, timed on this
   host's cores on a bounded sample.
@@ -35,13 +42,14 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
-FP16_PEAK_SCLK_MHZ = 2400.0  # the shader clock that peak is quoted at (256 CUs)
 
 # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the same
 # workloads (bench.py --part decode|prefill), each counter scaled by what it reads
 # for a plain 256 MiB device copy (FETCH_SIZE x 2, WRITE_SIZE x 1).  Figures and
 # commands: profiles/gemv_dma_llama7b_m1.md, profiles/gemm6_llama7b_m2048.md.
 DECODE_TRAFFIC_BYTES = 22995538       # average over the five projections
+DECODE_KERNEL = "q4_gemv_dma_kernel (decode GEMV, M=1)"
+PREFILL_KERNEL = "q4_gemm7_kernel (M=2048 K=4096 N=14336)"
 PREFILL_UP_TRAFFIC_BYTES = 597541990  # 538.6 MB read + 58.9 MB written
 
 DECODE_LAYER = [  # (name, K, N) -- Llama-2-7B projections, configs[1]
@@ -78,7 +86,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
-    p.add_argument("--part", choices=["all", "decode", "prefill", "copy", "int4-decode",
+    p.add_argument("--part", choices=["all", "decode", "prefill", "configs", "copy", "int4-decode",
                                       "int4-prefill"], default="all",
                    help="run one part only (for profiler passes); 'copy' runs a plain 256 MiB "
                         "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters")
@@ -121,6 +129,53 @@ def time_region(torch, stream, fn, steps, warmup, min_warm_s=0.2):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return start.elapsed_time(end) / 1e3, wall
+
+
+CONFIG_POINTS = [  # (config, M, K, N) -- every BASELINE point outside the headline layer
+    ("configs[0]", 1, 4096, 4096),
+    ("configs[2]", 4, 4096, 14336), ("configs[2]", 8, 4096, 14336), ("configs[2]", 16, 4096, 14336),
+    ("configs[2]", 4, 14336, 4096), ("configs[2]", 8, 14336, 4096), ("configs[2]", 16, 14336, 4096),
+    ("configs[4]", 1, 4096, 128256), ("configs[4]", 512, 4096, 128256),
+    ("configs[4]", 1, 11008, 4096), ("configs[4]", 512, 11008, 4096),
+]
+
+
+def shape_bench(mo, torch, dev, M, K, N, pool_bytes=1 << 30, reps=20, outliers=False):
+    """Average time of one matmul launch at (M, K, N): a HIP graph of one launch per
+    weight copy, the copies rotated through >= pool_bytes so reads come from HBM."""
+    copies = max(1, -(-pool_bytes // wbytes(K, N)))
+    ws = [make_weights(mo, torch, K, N, 31 * i + K + N, dev, outliers=outliers) for i in range(copies)]
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(M, K, generator=g, device=dev).half()
+    stream = torch.cuda.Stream(dev)
+    with torch.cuda.stream(stream):
+        mo.matmul_ggml_q4_0(x, ws[0])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for w in ws:
+            mo.matmul_ggml_q4_0(x, w)
+    secs, _ = time_region(torch, stream, lambda i: graph.replay(), reps, 3)
+    t = secs / (reps * copies)
+    del ws, graph
+    torch.cuda.empty_cache()
+    return t, copies
+
+
+def config_points(mo, torch, dev):
+    out = []
+    for cfg, M, K, N in CONFIG_POINTS:
+        t, copies = shape_bench(mo, torch, dev, M, K, N, reps=20 if M <= 16 else 5)
+        rec = {"config": cfg, "M": M, "K": K, "N": N, "us": round(t * 1e6, 2), "weight_copies": copies}
+        if M <= 16:
+            gbs = wbytes(K, N) / t / 1e9
+            rec.update({"GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+                        "GB/s_incl_x_y": round((wbytes(K, N) + 2 * M * (K + N)) / t / 1e9, 1)})
+        else:
+            tf = 2.0 * M * N * K / t / 1e12
+            rec.update({"TFLOP/s": round(tf, 1), "pct_mfma_peak": round(100 * tf / FP16_PEAK_TFLOPS, 2)})
+        out.append(rec)
+    return out
 
 
 def decode_bench(mo, torch, dev, args):
@@ -199,19 +254,42 @@ def prefill_bench(mo, torch, dev, iters=30, warmup=10):
     return out
 
 
-def measure_sclk(torch, dev, iters=20000, reps=3):
-    """Shader clock (MHz) under an MFMA load, from s_memtime against the 100 MHz
-    s_memrealtime (mcq4_measure_sclk): median over the waves of the last of `reps`
-    back-to-back runs, so the clock has settled under the power limit."""
-    from metalops_amd import _lib
-    ticks = torch.zeros(4096, dtype=torch.int64, device=dev)
-    stream = torch.cuda.current_stream(dev)
-    for _ in range(reps):
-        _lib.check(_lib.lib.mcq4_measure_sclk(ticks.data_ptr(), iters, stream.cuda_stream), "mcq4_measure_sclk")
-    torch.cuda.synchronize(dev)
-    t = ticks.view(-1, 2).double().cpu()
-    mhz = (100.0 * t[:, 0] / t[:, 1]).median().item()
-    return mhz
+def prefill_cpu_baseline(seconds_budget):
+    """Reference CPU path at the prefill size: dequantize to fp16 then X @ W
+    (quantization.py:452-454) at M = 2048 on the up shape (4096 x 14336) when a
+    call fits the budget, else the largest power-of-two M that does."""
+    import numpy as np
+    import torch
+
+    from oracle import q4_0_ref as ref
+
+    K, N = 4096, 14336
+    rng = np.random.default_rng(0)
+    W = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
+    blocks = torch.from_numpy(ref.quantize_llama_rule(W))
+    X = torch.from_numpy(rng.standard_normal((2048, K)).astype(np.float16))
+    M = 16
+    t0 = time.perf_counter()
+    ref.fallback_torch_cpu(X[:M], blocks)                 # warm-up
+    per = time.perf_counter() - t0
+    while M < 2048 and per * 2 * 3 <= seconds_budget:     # 3 timed calls at 2M still fit
+        M *= 2
+        t0 = time.perf_counter()
+        ref.fallback_torch_cpu(X[:M], blocks)             # also the warm-up at this M
+        per = time.perf_counter() - t0
+    n, t0 = 0, time.perf_counter()
+    while n < 1 or (time.perf_counter() - t0 + per <= seconds_budget and n < 20):
+        ref.fallback_torch_cpu(X[:M], blocks)
+        n += 1
+    per = (time.perf_counter() - t0) / n
+    return {
+        "value": round(2.0 * M * K * N / per / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"up K=4096 N=14336 at M={M} fp16: dequantize + X@W per call (quantization.py:452-454), "
+                  f"torch CPU, {n} calls, {per:.2f} s/call; os.cpu_count()={os.cpu_count()}",
+    }
 
 
 def make_i4_weights(mo, torch, K, N, seed, dev, outliers=False):
@@ -360,6 +438,8 @@ def run_part(mo, torch, dev, args):
                           "us_per_launch": round(t / dec["launches_step"] * 1e6, 3),
                           "weight_bytes_per_launch": dec["bytes_step"] / dec["launches_step"]}),
               flush=True)
+    elif args.part == "configs":
+        print(json.dumps({"part": "configs", "configs": config_points(mo, torch, dev)}), flush=True)
     elif args.part == "int4-prefill":
         print(json.dumps({"part": "int4-prefill", "configs": i4_prefill_bench(mo, torch, dev)}),
               flush=True)
@@ -394,17 +474,18 @@ def main():
     t_launch = t_step / dec["launches_step"]
     pre = prefill_bench(mo, torch, dev)
     pre_up = pre[0]
-    sclk = measure_sclk(torch, dev)
-    peak_sclk = FP16_PEAK_TFLOPS * sclk / FP16_PEAK_SCLK_MHZ
+    pre_tflops = sum(2.0 * p["M"] * p["K"] * p["N"] for p in pre) / sum(p["ms"] / 1e3 for p in pre) / 1e12
+    points = config_points(mo, torch, dev)
 
     i4_dec = i4_decode_bench(mo, torch, dev, args)
     i4_t = i4_dec["seconds"] / i4_dec["steps"]
     i4_gbs = i4_dec["bytes_step"] / i4_t / 1e9
     i4_pre = i4_prefill_bench(mo, torch, dev)
 
-    cpu = i4_cpu = None
+    cpu = i4_cpu = pre_cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_seconds)
+        pre_cpu = prefill_cpu_baseline(args.cpu_seconds)
         i4_cpu = i4_cpu_baseline(args.cpu_seconds / 2)
 
     line = {
@@ -439,10 +520,14 @@ def main():
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": DECODE_TRAFFIC_BYTES,
             "algorithmic_bytes_per_launch": dec["bytes_step"] // dec["launches_step"],
-            "kernel": "q4_gemv_dma_kernel (decode GEMV, M=1)",
+            "kernel": DECODE_KERNEL,
             "avg_launch_us": round(t_launch * 1e6, 3),
         },
         "prefill": {
+            "metric": "q4_0 GEMM TFLOP/s (% MFMA) at M=2048 (configs[3], up and down together)",
+            "value": round(pre_tflops, 1),
+            "unit": "TFLOP/s",
+            "pct_mfma_peak": round(100 * pre_tflops / FP16_PEAK_TFLOPS, 2),
             "configs": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in p.items()}
                         for p in pre],
             "roofline": {
@@ -452,15 +537,12 @@ def main():
                 "unit": "TFLOP/s",
                 "frac": round(pre_up["tflops"] / FP16_PEAK_TFLOPS, 4),
                 "traffic": PREFILL_UP_TRAFFIC_BYTES,
-                "kernel": "q4_gemm6_kernel<1> (M=2048 K=4096 N=14336)",
-                "sclk_mhz_mfma_load": round(sclk, 1),
-                "sclk_probe": "mcq4_measure_sclk: 512 workgroups of MFMA chains on random fp16 "
-                              "operands, s_memtime vs s_memrealtime; a full MFMA load, so a lower "
-                              "bound on the clock the GEMM itself runs at",
-                "peak_at_sclk": round(peak_sclk, 1),
-                "frac_at_sclk": round(pre_up["tflops"] / peak_sclk, 4),
+                "kernel": PREFILL_KERNEL,
+                "avg_launch_us": round(pre_up["ms"] * 1e3, 2),
             },
+            "cpu_baseline": pre_cpu,
         },
+        "configs": points,
         "cpu_baseline": cpu,
         "int4": {
             "workload": "same decode layer and prefill shapes, per-group INT4 (group 128, fp16 "

@@ -34,6 +34,10 @@ hipError_t launch_gemm2(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
 hipError_t launch_quantize_typed(int w_dtype, const void *W, int64_t ldw, int nb, int N,
                                  uint8_t *out, hipStream_t s);
 hipError_t launch_zero_counters(void *ws, hipStream_t s);
+size_t gemm7_workspace_bytes(int64_t M, int64_t K, int64_t N);
+bool gemm7_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N);
+hipError_t launch_gemm7(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
 hipError_t q4_gemvm_split_fallbacks(uint64_t *count, bool reset);
 hipError_t q4_gemm6_split_fallbacks(uint64_t *count, bool reset);
 hipError_t i4_gemv_split_fallbacks(uint64_t *count, bool reset);
@@ -70,7 +74,7 @@ bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 // Otherwise the async-copy GEMM (q4_gemm2) when its alignment needs hold and
 // the output has at least 128 tiles of 128x256; otherwise the register-staged
 // split-K kernel.  MCQ4_GEMM_PATH=sync|async|6 forces one kernel (tests).
-enum class Prefill { Sync, Async2, Staged6 };
+enum class Prefill { Sync, Async2, Staged6, Wide7 };
 Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
                        int64_t N) {
     const bool ok2 = mcq4::gemm2_supported(X, ldx, W, K, N);
@@ -79,6 +83,18 @@ Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t
         if (env[0] == 's') return Prefill::Sync;
         if (env[0] == 'a' && ok2) return Prefill::Async2;
         if (env[0] == '6' && ok6) return Prefill::Staged6;
+        if (env[0] == '7' && mcq4::gemm7_supported(X, ldx, W, M, K, N)) return Prefill::Wide7;
+    }
+    // The 256 x 256-tile GEMM (one wave per SIMD, half the dequant per MFMA)
+    // wins once its grid nearly fills the 256 CUs, or with half of that on long
+    // K where two K splits and their reduction cost little; the 128 x 256-tile
+    // q4_gemm6 is faster on smaller grids.  Measured (us, q4_gemm6 / q4_gemm7):
+    // M=2048 4096x14336 244 / 213, 14336x4096 235 / 209, 4096x4096 71 / 80;
+    // M=512 4096x128256 513 / 485, 11008x4096 57 / 61; M=1024 4096x14336
+    // 117 / 111; M=256 4096x14336 46 / 47.
+    if (ok6 && mcq4::gemm7_supported(X, ldx, W, M, K, N)) {
+        const int64_t t7 = ((M + 255) / 256) * ((N + 255) / 256);
+        if (t7 >= 192 || (t7 >= 96 && K >= 8192)) return Prefill::Wide7;
     }
     if (ok6) return Prefill::Staged6;
     if (ok2 && ((M + 127) / 128) * ((N + 255) / 256) >= 128) return Prefill::Async2;
@@ -213,7 +229,8 @@ size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M <= 0 || K <= 0 || N <= 0 || K % 32) return 0;
     if (M <= 32) return mcq4::skinny_workspace_bytes(M, K, N);
     // The largest of the split-K kernels' needs: an upper bound for any prefill kernel.
-    const size_t pre = std::max(mcq4::gemm_workspace_bytes(M, K, N), mcq4::gemm6_workspace_bytes(M, K, N));
+    const size_t pre = std::max({mcq4::gemm_workspace_bytes(M, K, N), mcq4::gemm6_workspace_bytes(M, K, N),
+                                 mcq4::gemm7_workspace_bytes(M, K, N)});
     // 33..64 rows run either family, depending on the pointers' alignment.
     return M <= 64 ? std::max(pre, mcq4::skinny_workspace_bytes(M, K, N)) : pre;
 }
@@ -251,6 +268,7 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
         hipStream_t st = (hipStream_t)stream;
         switch (prefill_kernel(x, ldx, W, M, K, N)) {
             case Prefill::Staged6: e = mcq4::launch_gemm6(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
+            case Prefill::Wide7: e = mcq4::launch_gemm7(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
             case Prefill::Async2: e = mcq4::launch_gemm2(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;
             default: e = mcq4::launch_gemm(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
         }

@@ -245,6 +245,9 @@ PATHS = {
     "gemm6_split4": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "4"},
     "gemm6_split8": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "8"},
     "gemm6_split16": {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "16"},
+    "gemm7": {"MCQ4_GEMM_PATH": "7"},
+    "gemm7_split2": {"MCQ4_GEMM_PATH": "7", "MCQ4_GEMM6_SPLIT": "2"},
+    "gemm7_split3": {"MCQ4_GEMM_PATH": "7", "MCQ4_GEMM6_SPLIT": "3"},
 }
 PATH_SHAPES = {
     "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
@@ -276,6 +279,10 @@ PATH_SHAPES = {
     "gemm6_split4": [(200, 2048, 384), (300, 4096, 640), (512, 11008, 1024)],
     "gemm6_split8": [(129, 4096, 256), (512, 11008, 512), (300, 8192, 768)],
     "gemm6_split16": [(200, 16384, 256), (130, 8192, 384)],
+    "gemm7": [(129, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
+              (200, 32, 256), (130, 64, 384), (513, 96, 256), (2048, 11008, 512), (65, 4096, 4096)],
+    "gemm7_split2": [(200, 352, 384), (300, 4096, 640), (512, 4096, 1024)],
+    "gemm7_split3": [(300, 4096, 640), (129, 2048, 2304)],
 }
 
 
