@@ -7,11 +7,17 @@
 // per-row math to one MFMA, two LDS reads and seven VALU instructions.
 //
 // Work decomposition
-//   * Column tile = 16 columns (a 288-byte strip row per K block).  Item = one
-//     tile's batch of B = 8 consecutive K blocks (8 strip rows, 2304 bytes).
-//   * Workgroup = 16 waves owning TPW tiles: wg, wg+G, ... (wg renumbered so
-//     consecutive tiles, which share 128-byte lines, run on one XCD).  Wave w
-//     owns batches b = w, w+16, ... of every one of those tiles and walks them
+//   * Column tile = TW columns (a TW*18-byte strip row per K block).  Item = one
+//     tile's batch of B = 2304 / (18 TW) consecutive K blocks (2304 bytes):
+//     TW = 16, B = 8 for the layer shapes; TW = 64, B = 2 for N >= 65536
+//     (lm_head), whose 1152-byte row pieces are nine whole 128-byte lines.
+//     A 16-column tile's 288-byte pieces straddle lines shared with the
+//     neighbouring tiles; a plain read of that pattern is 13-17% slower than one
+//     of 1152-byte pieces, but a 64-column tile leaves too few workgroups
+//     (N/64/TPW) to spread the per-row math over all CUs below N ~ 64K.
+//   * Workgroup = NW waves (16; 8 for N > 16384) owning TPW tiles: wg, wg+G, ...
+//     (wg renumbered so consecutive tiles, which share 128-byte lines, run on one
+//     XCD).  Wave w owns batches b = w, w+NW, ... of every one of those tiles and walks them
 //     batch-major: for each of its batches, the TPW tiles in turn.  The
 //     batch's activations therefore stay in registers across the tiles.
 //   * Copies: per item exactly three global_load_lds_dwordx4 (1 KiB each; 144
@@ -19,12 +25,12 @@
 //     slots; item k+R-1 is issued (into the slot item k-1 freed) before the wave
 //     waits for item k.  Rows past K re-copy row 0, so every item issues the same number of
 //     copies and the vmcnt waits are exact.
-//   * Activations: lane (c = l%16, g = l/16) loads elements 8g..8g+7 of each of
-//     the batch's 8 K blocks straight from global memory (all 16 lanes of a
-//     group load the same 16 bytes) and rearranges them to
+//   * Activations: lane (c = l%16, g = l/16) reads elements 8g..8g+7 of each of
+//     the batch's B K blocks from the wave's LDS copy (all 16 lanes of a group
+//     read the same 16 bytes) and rearranges them to
 //     x' = [x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16] (4 v_perm, 2 v_pk_mul).
-//   * Weights: lane (c, g) reads the qs dword w of elements 8g..8g+7 of column
-//     c.  Four v_and_or_b32 build the fp16 operand
+//   * Weights: for each 16-column group of the tile, lane (c, g) reads the qs
+//     dword w of elements 8g..8g+7 of column c of the group.  Four v_and_or_b32 build the fp16 operand
 //     [1024+q0, 1024+q4, 1024+16q1, 1024+16q5, 1024+q2, 1024+q6, 1024+16q3,
 //     1024+16q7] (low nibbles as is, high nibbles in place = times 16, which x'
 //     divides out).  Against the constant operand C = [1032, 1032, 1152, 1152,
@@ -33,7 +39,7 @@
 //     accumulator input of the per-item MFMA:
 //     mfma(x', B, -S)[0] = sum x*(q - 8), exact products, fp32 sums.
 //   * acc_tile += d * that, in fp32.
-//   * Epilogue: partials of the 16 waves per column summed through LDS in wave
+//   * Epilogue: partials of the waves per column summed through LDS in wave
 //     order (deterministic), stored as fp16.
 #include <algorithm>
 #include <atomic>
@@ -44,14 +50,14 @@
 
 namespace mcq4 {
 
-constexpr int GV_WAVES = 16;
-constexpr int GV_B = 8;                      // K blocks per item
-constexpr int GV_ROW = 288;                  // strip bytes per K block (16 columns)
-constexpr int GV_WCH = GV_B * 18;            // 144 strip chunks of 16 bytes per item
+constexpr int GV_ITEM = 2304;                // strip bytes per item
+constexpr int GV_WCH = GV_ITEM / 16;         // 144 strip chunks of 16 bytes per item
 constexpr int GV_LOADS = 3;                  // copies per item (chunks 0..143 of 192)
-constexpr int GV_SLOT = GV_WCH * 16 + 64;    // 2304 strip bytes + read overhang
+constexpr int GV_SLOT = GV_ITEM + 64;        // + read overhang
+constexpr int GV_WIDE = 64;                  // tile width of the large-N plan
+constexpr int GV_WIDE_MIN_TILES = 1024;      // 64-column tiles from N = 65536 on
 constexpr int GV_TPW_MAX = 4;                // tiles per workgroup
-constexpr int GV_XB_MAX = 4;                 // batches per wave (K <= 16*4*8*32 = 16384)
+constexpr int GV_K_MAX = 16384;
 constexpr int GV_RING = 2;                   // items in flight per wave (1 and 3 measured slower)
 constexpr int GV_NT = 2;                     // cache policy of the weight copies: non-temporal
 
@@ -73,10 +79,15 @@ __device__ __forceinline__ void gv_wait(int pending) {
     wait_vmcnt<0>();
 }
 
-template <int R, int TPW, int NW>
+template <int R, int TPW, int NW, int TW>
 __global__ void __launch_bounds__(NW * 64)
 q4_gemv_dma_kernel(GemvArgs a) {
     static_assert(R >= 1 && R <= 3 && TPW >= 1 && TPW <= GV_TPW_MAX, "config");
+    constexpr int ROWB = TW * BLOCK_BYTES;   // strip bytes per K block
+    constexpr int B = GV_ITEM / ROWB;        // K blocks per item
+    constexpr int CPR = ROWB / 16;           // 16-byte chunks per strip row
+    constexpr int NG = TW / 16;              // 16-column MFMA groups per tile
+    static_assert(B * ROWB == GV_ITEM && NG * 16 == TW, "tile width");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -84,10 +95,12 @@ q4_gemv_dma_kernel(GemvArgs a) {
     const int c = lane & 15, g = lane >> 4;
     const uint32_t grow = (uint32_t)a.N * BLOCK_BYTES;
 
-    // LDS: [NW waves x R slots][NW waves x activations][partials: TPW x NW waves x 16]
-    uint8_t *ring = smem + wave * (R * GV_SLOT);
-    uint8_t *xs = smem + NW * R * GV_SLOT + wave * a.xw;
-    float *red = (float *)(smem + NW * (R * GV_SLOT + a.xw));
+    // LDS: [NW waves x activations][NW waves x R slots]; the partials (TPW x NW
+    // waves x TW floats) reuse the slots once every wave is done with them, which
+    // keeps a 64-column 8-wave workgroup at 46 KiB (three per CU).
+    uint8_t *xs = smem + wave * a.xw;
+    uint8_t *ring = smem + NW * a.xw + wave * (R * GV_SLOT);
+    float *red = (float *)(smem + NW * a.xw);
 
     const int G = (int)gridDim.x, G8 = G & ~7;
     int wg = (int)blockIdx.x;
@@ -99,20 +112,20 @@ q4_gemv_dma_kernel(GemvArgs a) {
     const int nmine = nbm * ntl;
 
     // Copy geometry per lane and copy i: strip chunk q = lane + 64 i of an item
-    // (row q/18, 16-byte piece q%18); q >= 144 is masked off.
+    // (row q/CPR, 16-byte piece q%CPR); q >= 144 is masked off.
     int crow[GV_LOADS];
     uint32_t coff[GV_LOADS];
 #pragma unroll
     for (int i = 0; i < GV_LOADS; ++i) {
         const int q = lane + 64 * i;
-        crow[i] = q < GV_WCH ? q / 18 : 0;
-        coff[i] = q < GV_WCH ? (uint32_t)(q / 18) * grow + 16u * (uint32_t)(q % 18) : 0u;
+        crow[i] = q < GV_WCH ? q / CPR : 0;
+        coff[i] = q < GV_WCH ? (uint32_t)(q / CPR) * grow + 16u * (uint32_t)(q % CPR) : 0u;
     }
     // Item (batch index m of this wave, tile j) into ring slot `slot`.
     auto issue = [&](int m, int j, int slot) {
-        const int row0 = (wave + NW * m) * GV_B;
-        const int rows = min(GV_B, a.nb - row0);
-        const uint8_t *wb = a.W + (int64_t)tile(j) * GV_ROW + (int64_t)row0 * grow;
+        const int row0 = (wave + NW * m) * B;
+        const int rows = min(B, a.nb - row0);
+        const uint8_t *wb = a.W + (int64_t)tile(j) * ROWB + (int64_t)row0 * grow;
 #pragma unroll
         for (int i = 0; i < GV_LOADS; ++i) {
             // Rows past K re-copy row 0 (valid memory, never read back).
@@ -132,15 +145,15 @@ q4_gemv_dma_kernel(GemvArgs a) {
         islot = islot + 1 == R ? 0 : islot + 1;
         if (++ij == ntl) { ij = 0; ++im; }
     };
-    // Activations of all my batches first (512 bytes each: lanes 0..31 copy row
-    // lane/4, piece lane%4; rows past K clamp to the last row), so they are
+    // Activations of all my batches first (64 B bytes each: lanes 0..4B-1 copy
+    // row lane/4, piece lane%4; rows past K clamp to the last row), so they are
     // older than every weight copy and land before the first item does.
     for (int m = 0; m < nbm; ++m) {
-        const int r = min((wave + NW * m) * GV_B + (lane >> 2), a.nb - 1);
-        if (lane < 32)
+        const int r = min((wave + NW * m) * B + (lane >> 2), a.nb - 1);
+        if (lane < 4 * B)
             __builtin_amdgcn_global_load_lds(
                 (void *)((const uint8_t *)a.X + (int64_t)r * (QK * 2) + 16 * (lane & 3)),
-                (__attribute__((address_space(3))) void *)(xs + m * (GV_B * 64)), 16, 0, 0);
+                (__attribute__((address_space(3))) void *)(xs + m * (B * 64)), 16, 0, 0);
     }
     // R-1 items ahead; each iteration issues one more before it waits, into the
     // slot the previous item freed.
@@ -158,16 +171,17 @@ q4_gemv_dma_kernel(GemvArgs a) {
     const float4_t z = {0.f, 0.f, 0.f, 0.f};
     const half2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
 
-    float acc[TPW];
+    float acc[TPW][NG];
 #pragma unroll
-    for (int j = 0; j < TPW; ++j) acc[j] = 0.f;
+    for (int j = 0; j < TPW; ++j)
+#pragma unroll
+        for (int q = 0; q < NG; ++q) acc[j][q] = 0.f;
 
     int k = 0, slot = 0;
     for (int m = 0; m < nbm; ++m) {
-        const int row0 = (wave + NW * m) * GV_B;
-        const int rows = min(GV_B, a.nb - row0);
-        half8_t xq[GV_B];
-        float4_t negs[GV_B];
+        const int rows = min(B, a.nb - (wave + NW * m) * B);
+        half8_t xq[B];
+        float4_t negs[B];
 #pragma unroll
         for (int j = 0; j < TPW; ++j) {
             if (j < ntl) {
@@ -177,9 +191,9 @@ q4_gemv_dma_kernel(GemvArgs a) {
                     // they were copied before any weights, so at most the items in
                     // flight (this one included) are newer.
                     gv_wait<R + 1>(min(R, nmine - k));
-                    const uint32_t xa = lds_addr(xs + m * (GV_B * 64) + 16 * g);
+                    const uint32_t xa = lds_addr(xs + m * (B * 64) + 16 * g);
 #pragma unroll
-                    for (int u = 0; u < GV_B; ++u) {
+                    for (int u = 0; u < B; ++u) {
                         const uint4_t x = bitcast<uint4_t>(*(const lds_half8 *)(lds_ptr(xa) + u * 64));
                         const uint32_t h15 = __builtin_amdgcn_perm(x[2], x[0], 0x07060302u);   // x1, x5
                         const uint32_t h37 = __builtin_amdgcn_perm(x[3], x[1], 0x07060302u);   // x3, x7
@@ -193,29 +207,32 @@ q4_gemv_dma_kernel(GemvArgs a) {
                 }
                 gv_wait<R>(min(R - 1, nmine - 1 - k));
                 const uint32_t base = lds_addr(ring + slot * GV_SLOT);
-                const uint32_t qa = base + qal, da = base + doff;
-                auto row = [&](int u) {
-                    const lds_u32 *qp = (const lds_u32 *)(lds_ptr(qa) + u * GV_ROW);
-                    const uint32_t q0 = qp[0], q1 = qp[1];
-                    const uint32_t w = __builtin_amdgcn_alignbit(q1, q0, qsh);
-                    const uint32_t w8 = __builtin_amdgcn_alignbit(q1, q0, qsh + 8);
-                    const float d = (float)bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(da) + u * GV_ROW));
-                    const uint4_t bq = {and_or(w, mlo, c64), and_or(w, mhi, c64),
-                                        and_or(w8, mlo, c64), and_or(w8, mhi, c64)};
-                    const float4_t blk =
-                        __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], bitcast<half8_t>(bq), negs[u], 0, 0, 0);
-                    return d * blk[0];
-                };
-                if (rows == GV_B) {
-                    float part[GV_B];
 #pragma unroll
-                    for (int u = 0; u < GV_B; ++u) part[u] = row(u);
+                for (int grp = 0; grp < NG; ++grp) {
+                    const uint32_t qa = base + grp * 288 + qal, da = base + grp * 288 + doff;
+                    auto row = [&](int u) {
+                        const lds_u32 *qp = (const lds_u32 *)(lds_ptr(qa) + u * ROWB);
+                        const uint32_t q0 = qp[0], q1 = qp[1];
+                        const uint32_t w = __builtin_amdgcn_alignbit(q1, q0, qsh);
+                        const uint32_t w8 = __builtin_amdgcn_alignbit(q1, q0, qsh + 8);
+                        const float d = (float)bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(da) + u * ROWB));
+                        const uint4_t bq = {and_or(w, mlo, c64), and_or(w, mhi, c64),
+                                            and_or(w8, mlo, c64), and_or(w8, mhi, c64)};
+                        const float4_t blk =
+                            __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], bitcast<half8_t>(bq), negs[u], 0, 0, 0);
+                        return d * blk[0];
+                    };
+                    if (rows == B) {
+                        float part[B];
 #pragma unroll
-                    for (int u = 0; u < GV_B; ++u) acc[j] += part[u];
-                } else {
+                        for (int u = 0; u < B; ++u) part[u] = row(u);
 #pragma unroll
-                    for (int u = 0; u < GV_B; ++u)
-                        if (u < rows) acc[j] += row(u);
+                        for (int u = 0; u < B; ++u) acc[j][grp] += part[u];
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < B; ++u)
+                            if (u < rows) acc[j][grp] += row(u);
+                    }
                 }
                 // All reads of this slot are done before the next iteration refills it.
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -225,84 +242,102 @@ q4_gemv_dma_kernel(GemvArgs a) {
         }
     }
 
-    // Partials (lanes 0..15 hold column c = lane), then the ordered wave sum.
+    // Partials (lanes 0..15 hold column 16 grp + lane), then the ordered wave sum.
+    __syncthreads();                              // every wave's last slot is read
     if (lane < 16) {
 #pragma unroll
         for (int j = 0; j < TPW; ++j)
-            if (j < ntl) red[(j * NW + wave) * 16 + lane] = nbm > 0 ? acc[j] : 0.f;
+            if (j < ntl)
+#pragma unroll
+                for (int grp = 0; grp < NG; ++grp)
+                    red[(j * NW + wave) * TW + grp * 16 + lane] = nbm > 0 ? acc[j][grp] : 0.f;
     }
     __syncthreads();
-    for (int v = tid; v < ntl * 16; v += NW * 64) {
-        const int j = v >> 4, col = v & 15;
+    for (int v = tid; v < ntl * TW; v += NW * 64) {
+        const int j = v / TW, col = v % TW;
         float s = 0.f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) s += red[(j * NW + w) * 16 + col];
-        a.Y[tile(j) * 16 + col] = (_Float16)s;
+        for (int w = 0; w < NW; ++w) s += red[(j * NW + w) * TW + col];
+        a.Y[tile(j) * TW + col] = (_Float16)s;
     }
 }
 
-static size_t gemv_lds_bytes(int R, int tpw, int xw, int nw) {
-    return (size_t)nw * (R * GV_SLOT + xw) + (size_t)tpw * nw * 16 * sizeof(float);
+static size_t gemv_lds_bytes(int R, int tpw, int xw, int nw, int tw) {
+    return (size_t)nw * xw + std::max((size_t)nw * R * GV_SLOT, (size_t)tpw * nw * tw * sizeof(float));
 }
 
-template <int R, int TPW, int NW>
+template <int R, int TPW, int NW, int TW>
 static hipError_t launch_gemv_t(const GemvArgs &a, int grid, hipStream_t s) {
-    const size_t lds = gemv_lds_bytes(R, TPW, a.xw, NW);
+    const size_t lds = gemv_lds_bytes(R, TPW, a.xw, NW, TW);
+    if (lds > 160 * 1024) return hipErrorInvalidValue;
     static std::atomic<uint64_t> done{0};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)q4_gemv_dma_kernel<R, TPW, NW>,
+        e = hipFuncSetAttribute((const void *)q4_gemv_dma_kernel<R, TPW, NW, TW>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL((q4_gemv_dma_kernel<R, TPW, NW>), dim3(grid), dim3(NW * 64), lds, s, a);
+    hipLaunchKernelGGL((q4_gemv_dma_kernel<R, TPW, NW, TW>), dim3(grid), dim3(NW * 64), lds, s, a);
     return hipGetLastError();
 }
 
 template <int R, int NW>
 static hipError_t launch_gemv_r(const GemvArgs &a, int grid, int tpw, hipStream_t s) {
     switch (tpw) {
-        case 1: return launch_gemv_t<R, 1, NW>(a, grid, s);
-        case 2: return launch_gemv_t<R, 2, NW>(a, grid, s);
-        case 3: return launch_gemv_t<R, 3, NW>(a, grid, s);
-        default: return launch_gemv_t<R, 4, NW>(a, grid, s);
+        case 1: return launch_gemv_t<R, 1, NW, 16>(a, grid, s);
+        case 2: return launch_gemv_t<R, 2, NW, 16>(a, grid, s);
+        case 3: return launch_gemv_t<R, 3, NW, 16>(a, grid, s);
+        default: return launch_gemv_t<R, 4, NW, 16>(a, grid, s);
     }
 }
 
 // True when the M == 1 kernel applies: 16-byte aligned weights and
 // activations, 18*N a multiple of 16 (N % 8 == 0), at least one whole 16-column
-// tile and at most GV_XB_MAX batches per wave (K <= 16384).
+// tile and K <= 16384.
 bool gemv_dma_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t N) {
     if (opt_is("MCQ4_GEMV_PATH", 'o')) return false;   // "off": use the batched decode kernel
     return N % 8 == 0 && N >= 16 && ((uintptr_t)W % 16) == 0 &&
-           ((uintptr_t)X % 16) == 0 && K >= QK && K <= GV_WAVES * GV_XB_MAX * GV_B * QK &&
+           ((uintptr_t)X % 16) == 0 && K >= QK && K <= GV_K_MAX &&
            N * 18 * 8 < ((int64_t)1 << 31);
 }
 
-// Launches the M == 1 kernel over the whole 16-column tiles; *n_done returns the
-// number of leading columns covered.
+// Launches the M == 1 kernel over the whole 16-column tiles (64-column tiles
+// for N >= 65536, N % 64 == 0); *n_done returns the number of leading columns
+// covered.
 hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int K, int N,
                            int *n_done, hipStream_t s) {
     GemvArgs a;
     a.X = X; a.W = W; a.Y = Y;
     a.nb = K / QK; a.N = N;
+    if (N % GV_WIDE == 0 && N / GV_WIDE >= GV_WIDE_MIN_TILES) {
+        // Eight-wave workgroups of four 64-column tiles, two per CU (N = 128256:
+        // 50.0-50.3 us against 54.6-54.8 us with 16-column tiles, same box).
+        constexpr int B = GV_ITEM / (GV_WIDE * BLOCK_BYTES);
+        a.ntiles = N / GV_WIDE;
+        a.nbt = (a.nb + B - 1) / B;
+        *n_done = N;
+        const int grid = (a.ntiles + GV_TPW_MAX - 1) / GV_TPW_MAX;
+        a.xw = ((a.nbt + 7) / 8) * B * 64;
+        return launch_gemv_t<GV_RING, GV_TPW_MAX, 8, GV_WIDE>(a, grid, s);
+    }
+    constexpr int B = GV_ITEM / (16 * BLOCK_BYTES);
     a.ntiles = N / 16;
-    a.nbt = (a.nb + GV_B - 1) / GV_B;
+    a.nbt = (a.nb + B - 1) / B;
     *n_done = a.ntiles * 16;
     // One 16-wave workgroup per CU and up to GV_TPW_MAX tiles each.  Larger N
-    // (lm_head: more than 1024 tiles) runs 8-wave workgroups of GV_TPW_MAX tiles,
-    // two per CU, backfilled as they finish (measured 56 vs 66 us at N = 128256;
-    // 16 waves stay faster on the layer shapes).
+    // (more than 1024 tiles) runs 8-wave workgroups of GV_TPW_MAX tiles, two per
+    // CU, backfilled as they finish (16-column tiles at N = 128256: 56 vs 66 us
+    // with 16 waves; 16 waves stay faster on the layer shapes).
     const int nw = a.ntiles > 256 * GV_TPW_MAX ? 8 : 16;
     const int per_round = nw == 16 ? 256 : 512;
     int grid = std::min(a.ntiles, per_round);
     if (a.ntiles > per_round * GV_TPW_MAX) grid = (a.ntiles + GV_TPW_MAX - 1) / GV_TPW_MAX;
     const int tpw = (a.ntiles + grid - 1) / grid;
-    a.xw = ((a.nbt + nw - 1) / nw) * GV_B * 64;                   // my batches' activations
+    a.xw = ((a.nbt + nw - 1) / nw) * B * 64;                      // my batches' activations
     if (nw == 8) return launch_gemv_r<GV_RING, 8>(a, grid, tpw, s);
     return launch_gemv_r<GV_RING, 16>(a, grid, tpw, s);
 }

@@ -221,6 +221,7 @@ def test_matmul_ragged_down(dev):
 # MCQ4_* switches (re-read on each environment write, tests/conftest.py).
 PATHS = {
     "gemv_dma": {},
+    "gemv_dma_wide": {},
 
     "decode_lds_m1": {"MCQ4_GEMV_PATH": "off"},
     "gemvm": {},
@@ -252,6 +253,9 @@ PATHS = {
 PATH_SHAPES = {
     "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
                  (1, 16384, 272), (1, 14336, 4096)],
+    # 64-column tiles (N >= 65536, N % 64 == 0): one K block, odd block counts
+    # (a last item of one row) and waves without batches.
+    "gemv_dma_wide": [(1, 32, 65536), (1, 352, 65536), (1, 2080, 65600), (1, 4096, 70016)],
 
     "decode_lds_m1": [(1, 352, 264), (1, 4096, 1032)],
     "gemvm": [(2, 32, 16), (3, 352, 264), (4, 1024, 4104), (5, 11008, 512), (8, 4096, 14336),
