@@ -157,25 +157,45 @@ def shape_bench(mo, torch, dev, M, K, N, pool_bytes=1 << 30, reps=20, outliers=F
             mo.matmul_ggml_q4_0(x, w)
     secs, _ = time_region(torch, stream, lambda i: graph.replay(), reps, 3)
     t = secs / (reps * copies)
-    del ws, graph
+    del graph
+    t_read = read_ceiling(torch, stream, ws, reps) / copies if M <= 16 else None
+    del ws
     torch.cuda.empty_cache()
-    return t, copies
+    return t, copies, t_read
 
 
 def config_points(mo, torch, dev):
     out = []
     for cfg, M, K, N in CONFIG_POINTS:
-        t, copies = shape_bench(mo, torch, dev, M, K, N, reps=20 if M <= 16 else 5)
+        t, copies, t_read = shape_bench(mo, torch, dev, M, K, N, reps=20 if M <= 16 else 5)
         rec = {"config": cfg, "M": M, "K": K, "N": N, "us": round(t * 1e6, 2), "weight_copies": copies}
         if M <= 16:
             gbs = wbytes(K, N) / t / 1e9
             rec.update({"GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-                        "GB/s_incl_x_y": round((wbytes(K, N) + 2 * M * (K + N)) / t / 1e9, 1)})
+                        "GB/s_incl_x_y": round((wbytes(K, N) + 2 * M * (K + N)) / t / 1e9, 1),
+                        "read_ceiling_GB/s": round(wbytes(K, N) / t_read / 1e9, 1)})
         else:
             tf = 2.0 * M * N * K / t / 1e12
             rec.update({"TFLOP/s": round(tf, 1), "pct_mfma_peak": round(100 * tf / FP16_PEAK_TFLOPS, 2)})
         out.append(rec)
     return out
+
+
+def read_ceiling(torch, stream, weights, reps):
+    """Seconds per pass of plain reads (mcq4_read_probe, one launch per weight) over
+    `weights` in order, captured in one HIP graph -- the HBM read rate the same
+    bytes reach with launches of the same sizes and nothing else to do."""
+    from metalops_amd import _lib
+    sink = torch.zeros(4, dtype=torch.int32, device=weights[0].device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        cs = torch.cuda.current_stream().cuda_stream
+        for w in weights:
+            _lib.check(_lib.lib.mcq4_read_probe(w.data_ptr(), w.numel() * w.element_size(),
+                                                sink.data_ptr(), cs), "mcq4_read_probe")
+    secs, _ = time_region(torch, stream, lambda i: graph.replay(), reps, 3)
+    del graph
+    return secs / reps
 
 
 def decode_bench(mo, torch, dev, args):
@@ -229,7 +249,9 @@ def decode_bench(mo, torch, dev, args):
         steps = args.steps
     bytes_step = sum(wbytes(K, N) for _, K, N in DECODE_LAYER)
     xy_step = sum(2 * K + 2 * N for _, K, N in DECODE_LAYER)
+    read_s = read_ceiling(torch, stream, [w for layer in layers for w in layer], 20) / R
     return {
+        "read_ceiling_s": read_s,
         "seconds": secs, "steps": steps, "wall": wall,
         "bytes_step": bytes_step, "xy_step": xy_step,
         "launches_step": len(DECODE_LAYER), "copies": R,
@@ -512,6 +534,14 @@ def main():
         },
         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "gbs_incl_x_y": round((dec["bytes_step"] + dec["xy_step"]) / t_step / 1e9, 1),
+        # The same weight bytes read by a plain streaming kernel, one launch per
+        # projection, in a graph: what the launch sizes allow, before any math.
+        "read_ceiling": {
+            "GB/s": round(dec["bytes_step"] / dec["read_ceiling_s"] / 1e9, 1),
+            "pct_hbm_peak": round(100 * dec["bytes_step"] / dec["read_ceiling_s"] / 1e9 / HBM_PEAK_GBS, 2),
+            "kernel": "read_probe_kernel (mcq4_read_probe: 16 KiB per 256-thread workgroup)",
+            "value_over_ceiling": round(dec["read_ceiling_s"] / t_step, 4),
+        },
         "roofline": {
             "bound": "hbm",
             "achieved": round(dec["bytes_step"] / dec["launches_step"] / t_launch / 1e9, 1),

@@ -1,6 +1,8 @@
-// Shader-clock measurement under an MFMA load (a measurement helper for the
-// benchmark; no counterpart in the reference).
+// Measurement helpers for the benchmark (no counterpart in the reference):
+// the shader clock under an MFMA load, and a plain streaming read that gives
+// the HBM read rate one launch of a given size can reach.
 //
+// Clock:
 // 512 workgroups of 4 waves (two waves per SIMD) each run `iters` rounds of four
 // independent v_mfma_f32_32x32x16_f16 chains on pseudo-random operands and
 // record, per wave, the shader clock ticks (s_memtime) and the 100 MHz
@@ -53,7 +55,34 @@ __global__ void __launch_bounds__(256, 2) sclk_probe_kernel(uint64_t *ticks, int
     }
 }
 
+// Plain read: workgroup b of 256 threads reads the 16 KiB at 16384 b (four
+// 16-byte loads per thread, all issued before any is used), XORs them and
+// stores only if the XOR hits a magic value (so the loads stay live).
+__global__ void __launch_bounds__(256) read_probe_kernel(const uint4_t *p, size_t n16, uint32_t *sink) {
+    const size_t base = (size_t)blockIdx.x * 1024 + threadIdx.x;
+    uint4_t v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const size_t i = base + 256 * u;
+        v[u] = i < n16 ? p[i] : uint4_t{0u, 0u, 0u, 0u};
+    }
+    uint32_t s = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) s ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    if (s == 0x9E3779B9u) sink[0] = s;
+}
+
 }  // namespace mcq4
+
+extern "C" int mcq4_read_probe(const void *src, size_t bytes, uint32_t *sink, void *stream) {
+    if (!src || !sink || bytes < 16 || ((uintptr_t)src & 15)) return MCQ4_ERR_INVALID_ARG;
+    const size_t n16 = bytes / 16;
+    const size_t grid = (n16 + 1023) / 1024;
+    if (grid > 0x7fffffffu) return MCQ4_ERR_SHAPE;
+    hipLaunchKernelGGL(mcq4::read_probe_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream,
+                       (const mcq4::uint4_t *)src, n16, sink);
+    return hipGetLastError() == hipSuccess ? MCQ4_OK : MCQ4_ERR_HIP;
+}
 
 extern "C" int mcq4_measure_sclk(uint64_t *ticks, int iters, void *stream) {
     if (!ticks || iters <= 0) return MCQ4_ERR_INVALID_ARG;

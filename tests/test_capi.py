@@ -173,6 +173,30 @@ def test_measure_sclk_validation():
     assert _lib.lib.mcq4_measure_sclk(ctypes.c_void_p(256), 0, None) == _lib.MCQ4_ERR_INVALID_ARG
 
 
+def test_read_probe_validation():
+    """Argument checks need no GPU: null pointers, fewer than 16 bytes and a source
+    that is not 16-byte aligned are rejected."""
+    f = _lib.lib.mcq4_read_probe
+    assert f(None, 1024, ctypes.c_void_p(256), None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert f(ctypes.c_void_p(256), 1024, None, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert f(ctypes.c_void_p(256), 8, ctypes.c_void_p(512), None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert f(ctypes.c_void_p(264), 1024, ctypes.c_void_p(512), None) == _lib.MCQ4_ERR_INVALID_ARG
+
+
+@pytest.mark.gpu
+def test_read_probe_leaves_sink():
+    """The probe reads and, for data whose workgroup XOR is not the magic value, leaves
+    the sink untouched."""
+    import torch
+    src = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    sink = torch.full((4,), 7, dtype=torch.int32, device="cuda")
+    s = torch.cuda.current_stream()
+    _lib.check(_lib.lib.mcq4_read_probe(src.data_ptr(), src.numel() + 5, sink.data_ptr(), s.cuda_stream),
+               "mcq4_read_probe")
+    torch.cuda.synchronize()
+    assert sink.tolist() == [7, 7, 7, 7]
+
+
 @pytest.mark.gpu
 def test_measure_sclk_plausible():
     """Every wave reports shader-clock and 100 MHz real-time ticks; the implied clock
