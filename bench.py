@@ -46,11 +46,11 @@ FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
 # HBM bytes per launch from rocprofv3 FETCH_SIZE / WRITE_SIZE passes over the same
 # workloads (bench.py --part decode|prefill), each counter scaled by what it reads
 # for a plain 256 MiB device copy (FETCH_SIZE x 2, WRITE_SIZE x 1).  Figures and
-# commands: profiles/gemv_dma_llama7b_m1.md, profiles/gemm6_llama7b_m2048.md.
-DECODE_TRAFFIC_BYTES = 22995538       # average over the five projections
+# commands: profiles/gemv_dma_llama7b_m1.md, profiles/q4_gemm7_llama7b_m2048.md.
+DECODE_TRAFFIC_BYTES = 22999449       # average over the five projections
 DECODE_KERNEL = "q4_gemv_dma_kernel (decode GEMV, M=1)"
 PREFILL_KERNEL = "q4_gemm7_kernel (M=2048 K=4096 N=14336)"
-PREFILL_UP_TRAFFIC_BYTES = 597541990  # 538.6 MB read + 58.9 MB written
+PREFILL_UP_TRAFFIC_BYTES = 361849343  # 302.7 MB read + 59.2 MB written
 
 DECODE_LAYER = [  # (name, K, N) -- Llama-2-7B projections, configs[1]
     ("qkv", 4096, 12288),
