@@ -273,8 +273,8 @@ int mcq4_fused_rmsnorm_linear_int4(const void *X, int64_t ldx, const void *w_nor
                                    size_t workspace_bytes, void *stream);
 
 /*
- * Measurement helper; no counterpart in the reference (the benchmark uses it to
- * restate the fp16 MFMA peak at the measured clock).  Runs 512 workgroups of 4
+ * Measurement helper; no counterpart in the reference (it measures the shader
+ * clock the power limit leaves under a dense MFMA load).  Runs 512 workgroups of 4
  * waves, each `iters` rounds of four v_mfma_f32_32x32x16_f16 chains on fresh
  * pseudo-random fp16 operands, and writes
  * per wave w the shader-clock ticks (s_memtime) and 100 MHz real-time ticks

@@ -69,11 +69,13 @@ constexpr int64_t kMaxDim = (int64_t)1 << 30;  // keeps 32-bit lane offsets safe
 
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Prefill kernel choice (M > 64).  Default, when N % 128 == 0 and the pointers
-// are 16-byte aligned: the LDS-staged GEMM with two waves per SIMD (q4_gemm6).
-// Otherwise the async-copy GEMM (q4_gemm2) when its alignment needs hold and
-// the output has at least 128 tiles of 128x256; otherwise the register-staged
-// split-K kernel.  MCQ4_GEMM_PATH=sync|async|6 forces one kernel (tests).
+// Prefill kernel choice (M > 64).  When N % 128 == 0 and the pointers are
+// 16-byte aligned: the 256 x 256-tile GEMM (q4_gemm7) on grids that nearly fill
+// the CUs, else the 128 x 256-tile LDS-staged GEMM with two waves per SIMD
+// (q4_gemm6).  Otherwise the async-copy GEMM (q4_gemm2) when its alignment
+// needs hold and the output has at least 128 tiles of 128x256; otherwise the
+// register-staged split-K kernel.  MCQ4_GEMM_PATH=sync|async|6|7 forces one
+// kernel (tests).
 enum class Prefill { Sync, Async2, Staged6, Wide7 };
 Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
                        int64_t N) {
