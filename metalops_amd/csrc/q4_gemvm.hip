@@ -411,12 +411,10 @@ hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
         if (!opt_is("MCQ4_XCD_LOCAL", '0') && p.S <= 8) a.tickets = (uint64_t *)ws;
     }
     if (M > 16) return launch_gemvm_w<8, 2>(a, p.grid, p.tpw, s);
-    if (p.waves == 16) {
-        if (M <= 4) return launch_gemvm_w<16, 1, 4>(a, p.grid, p.tpw, s);
-        if (M <= 8) return launch_gemvm_w<16, 1, 8>(a, p.grid, p.tpw, s);
-        return launch_gemvm_w<16, 1>(a, p.grid, p.tpw, s);
-    }
-    return launch_gemvm_w<8, 1>(a, p.grid, p.tpw, s);
+    // M <= 16: 16-wave workgroups (gemvm_plan).
+    if (M <= 4) return launch_gemvm_w<16, 1, 4>(a, p.grid, p.tpw, s);
+    if (M <= 8) return launch_gemvm_w<16, 1, 8>(a, p.grid, p.tpw, s);
+    return launch_gemvm_w<16, 1>(a, p.grid, p.tpw, s);
 }
 
 }  // namespace mcq4
