@@ -374,6 +374,9 @@ static GmPlan gemvm_plan(int64_t M, int64_t K, int64_t N) {
     if (M > 16) waves = 8;
     const int cap = waves == 8 && M <= 16 ? 512 : 256;
     int S = M >= 8 && ntiles <= cap && nbt >= 2 * waves ? 2 : 1;
+    // Past 8 rows four splits pay once each still has 12+ batches (M=16
+    // K=14336 N=4096: 13.2 against 14.2 us with two; M=8: 11.0 either way).
+    if (S == 2 && M > 8 && nbt >= 3 * waves) S = 4;
     if (const char *env = opt("MCQ4_GEMVM_SPLIT")) {
         const int v = atoi(env);
         S = v == 2 || v == 4 || v == 8 ? v : 1;
