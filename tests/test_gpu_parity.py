@@ -263,7 +263,7 @@ PATH_SHAPES = {
     "gemvm_split2": [(2, 352, 264), (9, 4096, 1040), (16, 14336, 4096), (5, 11008, 512)],
     "gemvm_split8": [(16, 2048, 1032), (3, 14336, 512), (12, 512, 200)],
     "gemvm_split4": [(16, 4096, 1040), (6, 11008, 264), (13, 352, 8200)],
-    "gemvm_split2_reduce": [(9, 4096, 1040), (16, 14336, 4096)],
+    "gemvm_split2_reduce": [(9, 4096, 1040), (16, 14336, 4096), (4, 4096, 1040), (8, 2048, 264)],
     "decode_lds": [(1, 352, 264), (40, 2048, 96), (64, 256, 64), (17, 1024, 520), (33, 4096, 1032)],
     "gemvm_rb2": [(17, 4096, 1024), (20, 2048, 4096), (32, 14336, 512), (31, 1024, 2048), (18, 352, 272),
                   (24, 4096, 1032), (29, 11008, 4096)],

@@ -58,6 +58,8 @@ CASES = [
     # (name, environment, case builder args)
     ("q4_gemvm_s2", {"MCQ4_GEMVM_SPLIT": "2"}, ("q4", 16, 14336, 4096)),
     ("q4_gemvm_s8", {"MCQ4_GEMVM_SPLIT": "8"}, ("q4", 12, 2048, 1032)),
+    ("q4_gemvm_rows4_s4", {"MCQ4_GEMVM_SPLIT": "4"}, ("q4", 3, 4096, 1040)),
+    ("q4_gemvm_rows8_s2", {"MCQ4_GEMVM_SPLIT": "2"}, ("q4", 7, 11008, 512)),
     ("q4_gemm6_s2", {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "2"}, ("q4", 300, 4096, 640)),
     ("i4_gemv1", {}, ("i4", 1, 4096, 4096, 128, 4)),
     ("i4_gemv1_mr", {}, ("i4", 8, 11008, 4096, 128, 4)),
