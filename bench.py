@@ -601,7 +601,7 @@ def main():
                     "unit": "TFLOP/s",
                     "frac": round(i4_pre[0]["tflops"] / FP16_PEAK_TFLOPS, 4),
                     "traffic": I4_PREFILL_UP_TRAFFIC_BYTES,
-                    "kernel": "i4_gemm6_kernel (M=2048 K=4096 N=14336)",
+                    "kernel": "i4_gemm7_kernel (M=2048 K=4096 N=14336)",
                 },
             },
             "cpu_baseline": i4_cpu,

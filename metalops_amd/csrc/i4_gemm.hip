@@ -433,18 +433,27 @@ hipError_t launch_i4_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *P, con
                            const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K, int N,
                            int gs, int act, void *ws, hipStream_t s);
 
-// Covers both prefill kernels (i4_gemm6 for 4-bit weights with 16-bit
-// scales/zeros, this one otherwise).
+bool i4_gemm7_supported(int wb, int sz_dt, int64_t M, int64_t K, int64_t N, int64_t gs, const _Float16 *X,
+                        int64_t ldx, const void *Y, int64_t ldy);
+size_t i4_gemm7_workspace_bytes(int64_t M, int64_t K, int64_t N);
+hipError_t launch_i4_gemm7(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
+                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K, int N,
+                           int gs, int act, void *ws, hipStream_t s);
+
+// Covers the three prefill kernels (i4_gemm7 and i4_gemm6 for 4-bit weights
+// with 16-bit scales/zeros, this one otherwise).
 size_t i4_gemm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     const I4GCfg c = i4_gemm_config(M, K, N);
     const int64_t t = ((M + c.bm - 1) / c.bm) * ((N + I4G_BN - 1) / I4G_BN);
     const size_t own = c.S == 1 ? 0 : COUNTER_BYTES + (size_t)t * c.S * c.bm * I4G_BN * sizeof(float);
-    return std::max(own, i4_gemm6_workspace_bytes(M, K, N));
+    return std::max({own, i4_gemm6_workspace_bytes(M, K, N), i4_gemm7_workspace_bytes(M, K, N)});
 }
 
 hipError_t launch_i4_gemm(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K,
                           int N, int gs, int act, void *ws, hipStream_t s, int wb) {
+    if (i4_gemm7_supported(wb, sz_dt, M, K, N, gs, X, ldx, Y, ldy))
+        return launch_i4_gemm7(X, ldx, P, scales, zeros, sz_dt, Y, ldy, M, K, N, gs, act, ws, s);
     if (i4_gemm6_supported(wb, sz_dt, K, N, gs, Y, ldy))
         return launch_i4_gemm6(X, ldx, P, scales, zeros, sz_dt, Y, ldy, M, K, N, gs, act, ws, s);
     const I4GCfg c = i4_gemm_config(M, K, N);

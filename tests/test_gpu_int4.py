@@ -251,6 +251,7 @@ def test_gemm6_split2_exchange_matches_reduce(mo, dev, monkeypatch, M, K, N, act
     print(f"i4_gemm6 split2 exchange M={M} K={K} N={N} act={act}", flush=True)
     for k in ("MCQ4_I4_GEMM6", "MCQ4_I4_PATH", "MCQ4_XCD_LOCAL"):
         monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("MCQ4_I4_GEMM7", "0")      # the shapes that i4_gemm7 would take
     gs = 128
     w, packed, s, z = _quant(mo, dev, K, N, gs, seed=M + N)
     X = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).half().to(dev)
@@ -267,6 +268,39 @@ def test_gemm6_split2_exchange_matches_reduce(mo, dev, monkeypatch, M, K, N, act
         if act:
             base = _silu(base.astype(np.float64))
         _check_rows(Y.float().cpu().numpy(), base)
+
+
+# i4_gemm7 (256 x 256 tiles): grids of 192+ tiles, or 96+ with K >= 8192 (two
+# K splits summed by the reduction kernel); ragged M, N % 256 == 128 (waves past
+# N), group sizes 32..128, bf16 scales, fused activations.
+GEMM7_CASES = [
+    (2048, 512, 6144, 128, R.F16, None), (1800, 1024, 6400, 64, R.F16, None),
+    (2048, 8192, 3200, 128, R.F16, None), (2048, 512, 6144, 32, R.BF16, None),
+    (1793, 8448, 3072, 128, R.BF16, "silu"), (2048, 512, 6144, 128, R.F16, "gelu"),
+]
+
+
+@pytest.mark.parametrize("M,K,N,gs,sz,act", GEMM7_CASES)
+def test_gemm7(mo, dev, monkeypatch, M, K, N, gs, sz, act):
+    print(f"i4_gemm7 M={M} K={K} N={N} gs={gs} sz={sz} act={act}", flush=True)
+    for k in ("MCQ4_I4_GEMM6", "MCQ4_I4_GEMM7", "MCQ4_I4_PATH", "MCQ4_XCD_LOCAL"):
+        monkeypatch.delenv(k, raising=False)
+    w, packed, s, z = _quant(mo, dev, K, N, gs, sz, seed=M + K)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).half().to(dev)
+    f = {None: mo.matmul_int4, "silu": mo.matmul_int4_silu, "gelu": mo.matmul_int4_gelu}[act]
+    Y = f(X, packed, s, z, gs)
+    Y2 = f(X, packed, s, z, gs)
+    assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
+    base = _ref(X, packed, s, z, gs)
+    if act == "silu":
+        base = _silu(base.astype(np.float64))
+    elif act == "gelu":
+        base = _gelu_tanh(base.astype(np.float64))
+    _check_rows(Y.float().cpu().numpy(), base)
+    # the 128 x 256-tile kernel agrees within the same bar
+    monkeypatch.setenv("MCQ4_I4_GEMM7", "0")
+    Y6 = f(X, packed, s, z, gs)
+    _check_rows(Y6.float().cpu().numpy(), base)
 
 
 def _silu(y):
