@@ -293,37 +293,36 @@ i4_gemm7_kernel(I4GemmArgs a) {
     }
     wait_vmcnt<0>();
 
-    // Epilogue: lane holds columns 2 lrow + j of the wave's 64.
+    // Epilogue: lane holds columns 2 lrow + j of the wave's 64.  Element-wise
+    // stores straight from the accumulators (packing column pairs first made
+    // the compiler spill 32 accumulators to scratch here).
     const int rsub = 4 * lhi;
     if (a.S == 1) {
         _Float16 *Y = (_Float16 *)a.Y;
-        const int n = wcol0 + 2 * lrow;
-        if (n >= N) return;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int m = m0 + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
-                if (m < a.M) {
-                    half2_t v;
+            for (int j = 0; j < TN; ++j) {
+                const int n = wcol0 + 2 * lrow + j;
 #pragma unroll
-                    for (int j = 0; j < TN; ++j) v[j] = (_Float16)activate<ACT>(acc[i][j][r]);
-                    *(half2_t *)(Y + (int64_t)m * a.ldy + n) = v;
+                for (int r = 0; r < 16; ++r) {
+                    const int m = m0 + i * 32 + 8 * (r >> 2) + rsub + (r & 3);
+                    if (m < a.M && n < N) Y[(int64_t)m * a.ldy + n] = (_Float16)activate<ACT>(acc[i][j][r]);
                 }
             }
         return;
     }
     float *part = a.partials + ((int64_t)tile_id * a.S + z) * (J7_BM * I4G_BN);
-    const int nl = wave * J7_WN + 2 * lrow;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int ml = i * 32 + 8 * (r >> 2) + rsub + (r & 3);
-            float2 v;
-            v.x = acc[i][0][r];
-            v.y = acc[i][1][r];
-            *(float2 *)(part + ml * I4G_BN + nl) = v;
+        for (int j = 0; j < TN; ++j) {
+            const int nl = wave * J7_WN + 2 * lrow + j;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int ml = i * 32 + 8 * (r >> 2) + rsub + (r & 3);
+                part[ml * I4G_BN + nl] = acc[i][j][r];
+            }
         }
 }
 
