@@ -65,7 +65,7 @@ CASES = [
     ("i4_gemv1_mr", {}, ("i4", 8, 11008, 4096, 128, 4)),
     ("i4_gemv", {"MCQ4_I4_GEMV1": "0"}, ("i4", 4, 4096, 1040, 64, 4)),
     ("i8_gemv", {"MCQ4_I4_GEMV1": "0"}, ("i4", 8, 4096, 1024, 128, 8)),
-    ("i4_gemm6_s2", {}, ("i4", 2048, 14336, 4096, 128, 4)),
+    ("i4_gemm6_s2", {"MCQ4_I4_GEMM7": "0"}, ("i4", 2048, 14336, 4096, 128, 4)),
 ]
 
 
@@ -74,7 +74,7 @@ def test_split_recompute_path(dev, monkeypatch, name, env, case):
     from metalops_amd import _lib
     print(f"split recompute {name} {case}", flush=True)
     for k in ("MCQ4_GEMVM_SPLIT", "MCQ4_GEMM_PATH", "MCQ4_GEMM6_SPLIT", "MCQ4_I4_GEMV1", "MCQ4_XCD_LOCAL",
-              "MCQ4_SPLIT_FOREIGN", "MCQ4_I4_PATH", "MCQ4_I4_SPW1"):
+              "MCQ4_SPLIT_FOREIGN", "MCQ4_I4_PATH", "MCQ4_I4_SPW1", "MCQ4_I4_GEMM7"):
         monkeypatch.delenv(k, raising=False)
     for k, v in env.items():
         monkeypatch.setenv(k, v)
