@@ -63,9 +63,9 @@ PREFILL = [("up", 2048, 4096, 14336), ("down", 2048, 14336, 4096)]
 I4_GROUP = 128
 # HBM bytes per launch of the INT4 kernels (rocprofv3 FETCH_SIZE / WRITE_SIZE over
 # bench.py --part int4-decode|int4-prefill, scaled as above; profiles/i4_gemv1_llama7b_m1.md,
-# profiles/i4_gemm6_llama7b_m2048.md).
+# profiles/i4_gemm7_llama7b_m2048.md).
 I4_DECODE_TRAFFIC_BYTES = 21934858   # 21.80 MB read + 0.13 MB written
-I4_PREFILL_UP_TRAFFIC_BYTES = 584072806   # 525.4 MB read + 58.7 MB written
+I4_PREFILL_UP_TRAFFIC_BYTES = 373744538   # 307.6 MB read + 66.1 MB written
 
 
 def wbytes(K, N):
