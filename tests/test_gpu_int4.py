@@ -623,3 +623,27 @@ def test_decode_random_shapes_int8(mo, dev, monkeypatch, M, K, N, gs):
     _check_rows(mo.matmul_int8(X, *args, gs).float().cpu().numpy(), Yref)
     monkeypatch.delenv("MCQ4_I4_GEMV1")
     _check_rows(mo.matmul_int8(X, *args, gs).float().cpu().numpy(), Yref)
+
+
+def _random_i4_cases(n, seed):
+    """Seeded random (M, K, N, gs, sz) over the decode GEMVs and the prefill GEMMs:
+    group sizes 32..128, fp16/bf16/fp32 scales, ragged and aligned N."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        M = int(rng.choice([1, 1, 2, 5, 8, 16, 17, 32, 33, 64, 130, 300, 520]))
+        gs = int(rng.choice([32, 64, 128]))
+        K = gs * int(rng.integers(1, max(2, 4096 // gs)))
+        N = int(rng.choice([int(rng.integers(1, 300)), 128 * int(rng.integers(1, 20)), 8 * int(rng.integers(1, 200))]))
+        sz = [R.F16, R.BF16, R.F32][int(rng.integers(0, 3))]
+        out.append((M, K, N, gs, sz))
+    return out
+
+
+@pytest.mark.parametrize("M,K,N,gs,sz", _random_i4_cases(32, 4242))
+def test_matmul_random_shapes(mo, dev, M, K, N, gs, sz):
+    print(f"random matmul_int4 M={M} K={K} N={N} gs={gs} sz={sz}", flush=True)
+    w, packed, s, z = _quant(mo, dev, K, N, gs, sz, seed=M + K + N)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(M + K)).half().to(dev)
+    Y = mo.matmul_int4(X, packed, s, z, gs)
+    _check_rows(Y.float().cpu().numpy(), _ref(X, packed, s, z, gs))

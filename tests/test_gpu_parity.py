@@ -335,3 +335,34 @@ def test_split_exchange_matches_reduce(dev, monkeypatch, M, K, N, split):
     assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
     assert torch.equal(Y.view(torch.int16), Y0.view(torch.int16))
 
+
+
+def _random_cases(n, seed):
+    """Seeded random (M, K, N, pad) shapes over every dispatch region: M from 1 to
+    600 (decode kernels, the small- and large-grid GEMMs), K any multiple of 32 up
+    to 4096, N ragged or aligned, and row strides past K (pad halves)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        M = int(rng.choice([1, 1, 2, 3, 4, 7, 8, 12, 16, 17, 24, 32, 33, 48, 64, 65, 96, 130, 257, 384, 600]))
+        K = 32 * int(rng.integers(1, 129))
+        N = int(rng.choice([int(rng.integers(1, 400)), 8 * int(rng.integers(1, 300)),
+                            128 * int(rng.integers(1, 24))]))
+        pad = int(rng.choice([0, 0, 8, 40]))
+        cases.append((M, K, N, pad))
+    return cases
+
+
+@pytest.mark.parametrize("M,K,N,pad", _random_cases(48, 20261202))
+def test_matmul_random_shapes(dev, M, K, N, pad):
+    """Random shapes and strides against the oracle's fp32 product, with the
+    reference-rule quantizer; the row stride of X is K + pad."""
+    print(f"random matmul M={M} K={K} N={N} pad={pad}", flush=True)
+    mo = _mo()
+    W = _weights(K, N, seed=M * 131 + K + N, outliers=True)
+    blocks = ref.quantize_ref_rule(W.numpy())
+    Xw = _acts(M, K + pad, seed=M + K + pad)
+    X = Xw[:, :K]
+    Y = mo.matmul_ggml_q4_0(Xw.to(dev)[:, :K], torch.from_numpy(blocks).to(dev))
+    assert Y.shape == (M, N) and Y.dtype == torch.float16
+    _check_rows(Y.float().cpu().numpy(), ref.matmul_f32(X.contiguous().numpy(), blocks))
