@@ -250,8 +250,27 @@ def decode_bench(mo, torch, dev, args):
     bytes_step = sum(wbytes(K, N) for _, K, N in DECODE_LAYER)
     xy_step = sum(2 * K + 2 * N for _, K, N in DECODE_LAYER)
     read_s = read_ceiling(torch, stream, [w for layer in layers for w in layer], 20) / R
+
+    # The same step with gate and up in one launch (matmul_ggml_q4_0_grouped):
+    # four launches instead of five, same weights and results.
+    def grouped_step(r):
+        qkv, o, gate, up, down = layers[r % R]
+        return [mo.matmul_ggml_q4_0(xs[4096], qkv), mo.matmul_ggml_q4_0(xs[4096], o),
+                *mo.matmul_ggml_q4_0_grouped(xs[4096], [gate, up]), mo.matmul_ggml_q4_0(xs[11008], down)]
+
+    ggraph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        grouped_step(0)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(ggraph, stream=stream):
+        for r in range(R):
+            grouped_step(r)
+    reps = max(1, min(steps, 20000) // R)
+    gsecs, _ = time_region(torch, stream, lambda i: ggraph.replay(), reps, 3)
+    del ggraph
     return {
         "read_ceiling_s": read_s,
+        "grouped_step_s": gsecs / (reps * R),
         "seconds": secs, "steps": steps, "wall": wall,
         "bytes_step": bytes_step, "xy_step": xy_step,
         "launches_step": len(DECODE_LAYER), "copies": R,
@@ -541,6 +560,13 @@ def main():
             "pct_hbm_peak": round(100 * dec["bytes_step"] / dec["read_ceiling_s"] / 1e9 / HBM_PEAK_GBS, 2),
             "kernel": "read_probe_kernel (mcq4_read_probe: 16 KiB per 256-thread workgroup)",
             "value_over_ceiling": round(dec["read_ceiling_s"] / t_step, 4),
+        },
+        # The layer with gate and up in one launch (matmul_ggml_q4_0_grouped, no
+        # reference counterpart): the same bytes in four launches.
+        "grouped_gate_up": {
+            "GB/s": round(dec["bytes_step"] / dec["grouped_step_s"] / 1e9, 1),
+            "pct_hbm_peak": round(100 * dec["bytes_step"] / dec["grouped_step_s"] / 1e9 / HBM_PEAK_GBS, 2),
+            "ms_per_step": round(dec["grouped_step_s"] * 1e3, 5),
         },
         "roofline": {
             "bound": "hbm",

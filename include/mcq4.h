@@ -119,6 +119,21 @@ int mcq4_matmul_q4_0_f16_noalloc(const void *X, int64_t ldx, const uint8_t *W, v
 size_t mcq4_matmul_noalloc_max_workspace_bytes(void);
 
 /*
+ * Several q4_0 products that share the activations: Y[g] = X @ dequant(W[g]) for
+ * g < count, every W[g] of shape [K/32][N][18] and every Y[g] [M][ldy] fp16.
+ * No counterpart in the reference (its API takes one weight per call); it is
+ * for decode loops that project one activation row through several weights --
+ * gate and up of an MLP -- and would otherwise pay a launch per weight.  W and
+ * Y are host arrays of device pointers.  At M == 1 with count <= 4, N % 16 == 0
+ * and 16-byte aligned weights this is one launch of the M == 1 kernel over all
+ * count * N columns; otherwise it calls mcq4_matmul_q4_0_f16 per weight (same
+ * workspace rules).
+ */
+int mcq4_matmul_q4_0_f16_grouped(const void *X, int64_t ldx, int count, const uint8_t *const *W,
+                                 void *const *Y, int64_t ldy, int64_t M, int64_t K, int64_t N,
+                                 void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * matmul_ggml_q4_0 for activations of any float dtype (quantization.py:422-454).
  * x_dtype MCQ4_DTYPE_F16 is mcq4_matmul_q4_0_f16 (the fp16 MFMA kernels, the
  * semantics of the reference's GPU binding, core_mps.mm:5917-5975).

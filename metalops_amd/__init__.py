@@ -13,6 +13,7 @@ from .quantization import (
     QK4_0,
     dequantize_ggml_q4_0,
     matmul_ggml_q4_0,
+    matmul_ggml_q4_0_grouped,
     quantize_ggml_q4_0,
     quantize_ggml_q4_0_llama,
 )
@@ -37,6 +38,7 @@ __all__ = [
     "quantize_ggml_q4_0_llama",
     "dequantize_ggml_q4_0",
     "matmul_ggml_q4_0",
+    "matmul_ggml_q4_0_grouped",
     "quantize_int4",
     "dequantize_int4",
     "matmul_int4",

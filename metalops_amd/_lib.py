@@ -34,6 +34,7 @@ SIGNATURES = {
     "mcq4_matmul_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "mcq4_matmul_q4_0_f16": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
     "mcq4_matmul_q4_0": (_int, [_p, _int, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
+    "mcq4_matmul_q4_0_f16_grouped": (_int, [_p, _i64, _int, _p, _p, _i64, _i64, _i64, _i64, _p, _sz, _p]),
     "mcq4_reload_options": (_int, []),
     "mcq4_matmul_q4_0_f16_noalloc": (_int, [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "mcq4_matmul_noalloc_max_workspace_bytes": (_sz, []),

@@ -45,6 +45,9 @@ hipError_t i4_gemv1_split_fallbacks(uint64_t *count, bool reset);
 hipError_t i4_gemm6_split_fallbacks(uint64_t *count, bool reset);
 hipError_t launch_q4_xact(const void *X, int x_dt, int64_t ldx, const uint8_t *W, void *Y,
                           int64_t ldy, int64_t M, int64_t K, int64_t N, hipStream_t s);
+bool gemv_dma_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t N);
+hipError_t launch_gemv_dma_group(const _Float16 *X, const uint8_t *const *W, _Float16 *const *Y, int count,
+                                 int K, int N, int *n_done, hipStream_t s);
 }  // namespace mcq4
 
 namespace {
@@ -276,6 +279,33 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
         }
     }
     return hip_status(e, "matmul launch");
+}
+
+int mcq4_matmul_q4_0_f16_grouped(const void *X, int64_t ldx, int count, const uint8_t *const *W,
+                                 void *const *Y, int64_t ldy, int64_t M, int64_t K, int64_t N,
+                                 void *workspace, size_t workspace_bytes, void *stream) {
+    g_err[0] = 0;
+    if (!W || !Y || count < 1) return fail(MCQ4_ERR_INVALID_ARG, "need count >= 1 weights and outputs");
+    for (int g = 0; g < count; ++g)
+        if (!W[g] || !Y[g]) return fail(MCQ4_ERR_INVALID_ARG, "null weight or output pointer %d", g);
+    // One launch for M == 1 when every weight takes the M == 1 kernel whole
+    // (16-byte aligned, N a multiple of 16) and there are at most 4 of them.
+    bool one = M == 1 && count <= 4 && N % 16 == 0 && X && aligned(X, 16) && ldx % 8 == 0 && ldx >= K &&
+               K > 0 && K % 32 == 0 && N > 0 && !check_kn(K, N);
+    for (int g = 0; one && g < count; ++g)
+        one = aligned(Y[g], 2) && mcq4::gemv_dma_supported((const _Float16 *)X, W[g], K, N * count);
+    g_err[0] = 0;
+    if (!one) {
+        for (int g = 0; g < count; ++g)
+            if (int st = mcq4_matmul_q4_0_f16(X, ldx, W[g], Y[g], ldy, M, K, N, workspace, workspace_bytes,
+                                              stream))
+                return st;
+        return MCQ4_OK;
+    }
+    int n_done = 0;
+    const hipError_t e = mcq4::launch_gemv_dma_group((const _Float16 *)X, W, (_Float16 *const *)Y, count, (int)K,
+                                                     (int)N, &n_done, (hipStream_t)stream);
+    return hip_status(e, "grouped matmul launch");
 }
 
 int mcq4_matmul_q4_0(const void *X, int x_dtype, int64_t ldx, const uint8_t *W, void *Y,

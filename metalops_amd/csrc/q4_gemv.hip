@@ -61,11 +61,16 @@ constexpr int GV_K_MAX = 16384;
 constexpr int GV_RING = 2;                   // items in flight per wave (1 and 3 measured slower)
 constexpr int GV_NT = 2;                     // cache policy of the weight copies: non-temporal
 
+constexpr int GV_GROUP_MAX = 4;              // weights sharing X in one launch
+
 struct GemvArgs {
     const _Float16 *X;
-    const uint8_t *W;
-    _Float16 *Y;
-    int nb, N, ntiles, nbt;                  // nbt = batches per tile
+    // Up to GV_GROUP_MAX weights of the same [K/32][N][18] shape, and their
+    // outputs: tile t is tile t % tiles_per_w of weight t / tiles_per_w.
+    const uint8_t *W[GV_GROUP_MAX];
+    _Float16 *Y[GV_GROUP_MAX];
+    int tiles_per_w;
+    int nb, N, ntiles, nbt;                  // N per weight; ntiles over all; nbt = batches per tile
     int xw;                                  // activation bytes per wave in LDS
 };
 
@@ -108,6 +113,18 @@ q4_gemv_dma_kernel(GemvArgs a) {
     // Tile j of this workgroup: wg + j*G.
     const int ntl = min(TPW, (a.ntiles - wg + G - 1) / G);         // >= 1 (grid <= ntiles)
     auto tile = [&](int j) { return wg + j * G; };
+    // Weight and output bases of tile j (the weight index is uniform: scalar selects).
+    const uint8_t *wt[TPW];
+    _Float16 *yt[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) {
+        const int t = j < ntl ? tile(j) : 0;
+        const int gi = t / a.tiles_per_w, lt = t - gi * a.tiles_per_w;
+        const uint8_t *w = gi == 0 ? a.W[0] : gi == 1 ? a.W[1] : gi == 2 ? a.W[2] : a.W[3];
+        _Float16 *y = gi == 0 ? a.Y[0] : gi == 1 ? a.Y[1] : gi == 2 ? a.Y[2] : a.Y[3];
+        wt[j] = w + (int64_t)lt * ROWB;
+        yt[j] = y + lt * TW;
+    }
     const int nbm = a.nbt > wave ? (a.nbt - wave + NW - 1) / NW : 0;  // my batches
     const int nmine = nbm * ntl;
 
@@ -125,7 +142,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
     auto issue = [&](int m, int j, int slot) {
         const int row0 = (wave + NW * m) * B;
         const int rows = min(B, a.nb - row0);
-        const uint8_t *wb = a.W + (int64_t)tile(j) * ROWB + (int64_t)row0 * grow;
+        const uint8_t *wb = wt[j] + (int64_t)row0 * grow;
 #pragma unroll
         for (int i = 0; i < GV_LOADS; ++i) {
             // Rows past K re-copy row 0 (valid memory, never read back).
@@ -258,7 +275,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
         float s = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) s += red[(j * NW + w) * TW + col];
-        a.Y[tile(j) * TW + col] = (_Float16)s;
+        yt[j][col] = (_Float16)s;
     }
 }
 
@@ -305,19 +322,27 @@ bool gemv_dma_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t 
            N * 18 * 8 < ((int64_t)1 << 31);
 }
 
-// Launches the M == 1 kernel over the whole 16-column tiles (64-column tiles
-// for N >= 65536, N % 64 == 0); *n_done returns the number of leading columns
+// Launches the M == 1 kernel for `count` weights of the same shape that share
+// X (count <= GV_GROUP_MAX; with count > 1, N % 16 == 0) over their whole
+// 16-column tiles (64-column tiles when N % 64 == 0 and the weights hold 1024 or
+// more of them); *n_done returns the number of leading columns of each weight
 // covered.
-hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int K, int N,
-                           int *n_done, hipStream_t s) {
+hipError_t launch_gemv_dma_group(const _Float16 *X, const uint8_t *const *W, _Float16 *const *Y, int count,
+                                 int K, int N, int *n_done, hipStream_t s) {
+    if (count < 1 || count > GV_GROUP_MAX || (count > 1 && N % 16)) return hipErrorInvalidValue;
     GemvArgs a;
-    a.X = X; a.W = W; a.Y = Y;
+    a.X = X;
+    for (int g = 0; g < GV_GROUP_MAX; ++g) {
+        a.W[g] = W[g < count ? g : 0];
+        a.Y[g] = Y[g < count ? g : 0];
+    }
     a.nb = K / QK; a.N = N;
-    if (N % GV_WIDE == 0 && N / GV_WIDE >= GV_WIDE_MIN_TILES) {
+    if (N % GV_WIDE == 0 && count * (N / GV_WIDE) >= GV_WIDE_MIN_TILES) {
         // Eight-wave workgroups of four 64-column tiles, two per CU (N = 128256:
         // 50.0-50.3 us against 54.6-54.8 us with 16-column tiles, same box).
         constexpr int B = GV_ITEM / (GV_WIDE * BLOCK_BYTES);
-        a.ntiles = N / GV_WIDE;
+        a.tiles_per_w = N / GV_WIDE;
+        a.ntiles = count * a.tiles_per_w;
         a.nbt = (a.nb + B - 1) / B;
         *n_done = N;
         const int grid = (a.ntiles + GV_TPW_MAX - 1) / GV_TPW_MAX;
@@ -325,9 +350,10 @@ hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int
         return launch_gemv_t<GV_RING, GV_TPW_MAX, 8, GV_WIDE>(a, grid, s);
     }
     constexpr int B = GV_ITEM / (16 * BLOCK_BYTES);
-    a.ntiles = N / 16;
+    a.tiles_per_w = N / 16;
+    a.ntiles = count * a.tiles_per_w;
     a.nbt = (a.nb + B - 1) / B;
-    *n_done = a.ntiles * 16;
+    *n_done = a.tiles_per_w * 16;
     // One 16-wave workgroup per CU and up to GV_TPW_MAX tiles each.  Larger N
     // (more than 1024 tiles) runs 8-wave workgroups of GV_TPW_MAX tiles, two per
     // CU, backfilled as they finish (16-column tiles at N = 128256: 56 vs 66 us
@@ -340,6 +366,13 @@ hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int
     a.xw = ((a.nbt + nw - 1) / nw) * B * 64;                      // my batches' activations
     if (nw == 8) return launch_gemv_r<GV_RING, 8>(a, grid, tpw, s);
     return launch_gemv_r<GV_RING, 16>(a, grid, tpw, s);
+}
+
+// The single-weight form: the whole 16-column tiles of W (64-column tiles for
+// N >= 65536, N % 64 == 0); *n_done returns the number of leading columns covered.
+hipError_t launch_gemv_dma(const _Float16 *X, const uint8_t *W, _Float16 *Y, int K, int N,
+                           int *n_done, hipStream_t s) {
+    return launch_gemv_dma_group(X, &W, &Y, 1, K, N, n_done, s);
 }
 
 }  // namespace mcq4

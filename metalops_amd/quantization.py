@@ -17,8 +17,9 @@ and returns without synchronising, like the reference's Metal binding
 from __future__ import annotations
 
 import contextlib
+import ctypes
 import threading
-from typing import Optional
+from typing import List, Optional, Sequence
 
 import torch
 
@@ -233,3 +234,49 @@ def matmul_ggml_q4_0(X: torch.Tensor, W_blocks: torch.Tensor) -> torch.Tensor:
                                                  stream),
                    "mcq4_matmul_q4_0_f16")
     return Y
+
+
+def matmul_ggml_q4_0_grouped(X: torch.Tensor, weights: Sequence[torch.Tensor]) -> List[torch.Tensor]:
+    """``[X @ dequant(W) for W in weights]`` -- several q4_0 weights of one shape
+    that share the activations (an MLP's gate and up), returned in ``X.dtype``.
+
+    No counterpart in the reference, whose API takes one weight per call; the
+    results are those of ``matmul_ggml_q4_0`` per weight (the same kernels'
+    arithmetic).  For one fp16 activation row and up to four weights with N a
+    multiple of 16 it is a single launch of the M == 1 kernel over all of their
+    columns, which saves a launch and a kernel tail per extra weight.
+    """
+    weights = list(weights)
+    if not weights:
+        return []
+    shape = tuple(weights[0].shape)
+    for w in weights:
+        if tuple(w.shape) != shape:
+            raise RuntimeError(f"grouped weights must share one shape, got {tuple(w.shape)} and {shape}")
+    num_blocks_per_col, N, _ = shape
+    K = num_blocks_per_col * QK4_0
+    assert X.shape[1] == K, f"X K dim ({X.shape[1]}) must match weight K ({K})"
+    _require_device(X, *weights)
+    if X.dim() != 2 or X.dtype != torch.float16 or X.shape[0] != 1 or N % 16 or len(weights) > 4:
+        return [matmul_ggml_q4_0(X, w) for w in weights]
+    for w in weights:
+        if w.dtype != torch.uint8 or w.shape[2] != BLOCK_Q4_0_SIZE:
+            raise RuntimeError("W_blocks must be uint8 [K/32, N, 18]")
+    ws = []
+    for w in weights:
+        w = w if w.is_contiguous() else w.contiguous()
+        ws.append(w.clone() if w.data_ptr() % 16 else w)
+    x = X
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.stride(0) < K or x.data_ptr() % 16:
+        x = x.contiguous()
+        if x.data_ptr() % 16:
+            x = x.clone()
+    Ys = [torch.empty((1, N), dtype=X.dtype, device=X.device) for _ in ws]
+    wp = (ctypes.c_void_p * len(ws))(*[w.data_ptr() for w in ws])
+    yp = (ctypes.c_void_p * len(Ys))(*[y.data_ptr() for y in Ys])
+    stream = _stream(X.device)
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.lib.mcq4_matmul_q4_0_f16_grouped(x.data_ptr(), x.stride(0), len(ws), wp, yp, N, 1, K, N,
+                                                         None, 0, stream),
+                   "mcq4_matmul_q4_0_f16_grouped")
+    return Ys

@@ -366,3 +366,37 @@ def test_matmul_random_shapes(dev, M, K, N, pad):
     Y = mo.matmul_ggml_q4_0(Xw.to(dev)[:, :K], torch.from_numpy(blocks).to(dev))
     assert Y.shape == (M, N) and Y.dtype == torch.float16
     _check_rows(Y.float().cpu().numpy(), ref.matmul_f32(X.contiguous().numpy(), blocks))
+
+
+@pytest.mark.parametrize("K,N,count", [(4096, 11008, 2), (4096, 4096, 3), (352, 64, 4), (11008, 4096, 2),
+                                       (4096, 32768, 2), (2080, 65536, 2), (32, 16, 2)])
+def test_matmul_grouped(dev, K, N, count):
+    """Weights sharing one activation row in one launch (gate and up): every output
+    within the bar of the oracle, and of the single-weight calls."""
+    print(f"grouped matmul K={K} N={N} count={count}", flush=True)
+    mo = _mo()
+    Ws = [_weights(K, N, seed=K + N + 17 * g, outliers=True) for g in range(count)]
+    blocks = [ref.quantize_llama_rule(W.numpy()) for W in Ws]
+    X = _acts(1, K, seed=K + count)
+    bd = [torch.from_numpy(b).to(dev) for b in blocks]
+    Ys = mo.matmul_ggml_q4_0_grouped(X.to(dev), bd)
+    assert len(Ys) == count
+    for g in range(count):
+        assert Ys[g].shape == (1, N) and Ys[g].dtype == torch.float16
+        _check_rows(Ys[g].float().cpu().numpy(), ref.matmul_f32(X.numpy(), blocks[g]))
+        _check_rows(Ys[g].float().cpu().numpy(), mo.matmul_ggml_q4_0(X.to(dev), bd[g]).float().cpu().numpy())
+
+
+def test_matmul_grouped_other_cases(dev):
+    """Rows > 1, more than four weights and N % 16 != 0 take the per-weight path
+    (the same results bit for bit); mismatched shapes are rejected."""
+    mo = _mo()
+    K, N = 256, 72
+    blocks = [torch.from_numpy(ref.quantize_llama_rule(_weights(K, N, seed=g).numpy())).to(dev) for g in range(5)]
+    for X in (_acts(3, K, seed=1).to(dev), _acts(1, K, seed=2).to(dev)):
+        Ys = mo.matmul_ggml_q4_0_grouped(X, blocks)
+        for g in range(5):
+            assert torch.equal(Ys[g].view(torch.int16), mo.matmul_ggml_q4_0(X, blocks[g]).view(torch.int16))
+    other = torch.from_numpy(ref.quantize_llama_rule(_weights(K, 64, seed=9).numpy())).to(dev)
+    with pytest.raises(RuntimeError):
+        mo.matmul_ggml_q4_0_grouped(_acts(1, K, seed=3).to(dev), [blocks[0], other])
