@@ -288,6 +288,8 @@ int mcq4_matmul_q4_0_f16_grouped(const void *X, int64_t ldx, int count, const ui
     if (!W || !Y || count < 1) return fail(MCQ4_ERR_INVALID_ARG, "need count >= 1 weights and outputs");
     for (int g = 0; g < count; ++g)
         if (!W[g] || !Y[g]) return fail(MCQ4_ERR_INVALID_ARG, "null weight or output pointer %d", g);
+    // The same argument checks as the per-weight calls, whichever path runs.
+    if (ldy < N) return fail(MCQ4_ERR_SHAPE, "ldy (%lld) < N (%lld)", (long long)ldy, (long long)N);
     // One launch for M == 1 when every weight takes the M == 1 kernel whole
     // (16-byte aligned, N a multiple of 16) and there are at most 4 of them.
     bool one = M == 1 && count <= 4 && N % 16 == 0 && X && aligned(X, 16) && ldx % 8 == 0 && ldx >= K &&

@@ -183,6 +183,22 @@ def test_read_probe_validation():
     assert f(ctypes.c_void_p(264), 1024, ctypes.c_void_p(512), None) == _lib.MCQ4_ERR_INVALID_ARG
 
 
+def test_grouped_validation():
+    """The grouped entry point's argument checks need no GPU: no weights, a null
+    weight or output pointer, and ldy < N are rejected on either path."""
+    f = _lib.lib.mcq4_matmul_q4_0_f16_grouped
+    w = (ctypes.c_void_p * 2)(256, 512)
+    y = (ctypes.c_void_p * 2)(1024, 2048)
+    x = ctypes.c_void_p(4096)
+    assert f(x, 64, 0, w, y, 64, 1, 64, 64, None, 0, None) == _lib.MCQ4_ERR_INVALID_ARG
+    assert f(x, 64, 2, None, y, 64, 1, 64, 64, None, 0, None) == _lib.MCQ4_ERR_INVALID_ARG
+    wn = (ctypes.c_void_p * 2)(256, None)
+    assert f(x, 64, 2, wn, y, 64, 1, 64, 64, None, 0, None) == _lib.MCQ4_ERR_INVALID_ARG
+    for m in (1, 3):                              # one-launch form and per-weight form
+        assert f(x, 64, 2, w, y, 32, m, 64, 64, None, 0, None) == _lib.MCQ4_ERR_SHAPE
+        assert b"ldy" in _lib.lib.mcq4_last_error()
+
+
 @pytest.mark.gpu
 def test_read_probe_leaves_sink():
     """The probe reads and, for data whose workgroup XOR is not the magic value, leaves
