@@ -21,7 +21,8 @@ Metric: q4_0 GEMV GB/s (% HBM peak) at M=1; q4_0 GEMM TFLOP/s
   Each is a graph of launches over weight copies rotated through >= 1 GB.
 * ``cpu_baseline``: the reference's CPU path (dequantize to fp16 on every call,
   then ``X @ W``; quantization.py:452-454) restated in oracle/, timed on this
-  host's cores on a bounded sample.
+  host's cores on a bounded sample; ``secondary`` is the same call at fp32
+  (``X.float() @ dequant_f32``).
 * ``int4``: the per-group INT4 path (quantization.py:26-239) on the same decode
   layer and prefill shapes, group size 128 with fp16 scales and zeros (an fp16
   model's weights), with its own roofline and CPU baseline.
@@ -309,20 +310,26 @@ def prefill_cpu_baseline(seconds_budget):
     W = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
     blocks = torch.from_numpy(ref.quantize_llama_rule(W))
     X = torch.from_numpy(rng.standard_normal((2048, K)).astype(np.float16))
-    M = 16
-    t0 = time.perf_counter()
-    ref.fallback_torch_cpu(X[:M], blocks)                 # warm-up
-    per = time.perf_counter() - t0
-    while M < 2048 and per * 2 * 3 <= seconds_budget:     # 3 timed calls at 2M still fit
-        M *= 2
+
+    def timed(x, budget):
+        M = 16
         t0 = time.perf_counter()
-        ref.fallback_torch_cpu(X[:M], blocks)             # also the warm-up at this M
+        ref.fallback_torch_cpu(x[:M], blocks)                 # warm-up
         per = time.perf_counter() - t0
-    n, t0 = 0, time.perf_counter()
-    while n < 1 or (time.perf_counter() - t0 + per <= seconds_budget and n < 20):
-        ref.fallback_torch_cpu(X[:M], blocks)
-        n += 1
-    per = (time.perf_counter() - t0) / n
+        while M < 2048 and per * 2 * 3 <= budget:             # 3 timed calls at 2M still fit
+            M *= 2
+            t0 = time.perf_counter()
+            ref.fallback_torch_cpu(x[:M], blocks)             # also the warm-up at this M
+            per = time.perf_counter() - t0
+        n, t0 = 0, time.perf_counter()
+        while n < 1 or (time.perf_counter() - t0 + per <= budget and n < 20):
+            ref.fallback_torch_cpu(x[:M], blocks)
+            n += 1
+        return M, n, (time.perf_counter() - t0) / n
+
+    M, n, per = timed(X, seconds_budget * 2 / 3)
+    # The secondary figure: the same call at fp32 (X.float() @ dequant_f32).
+    M32, n32, per32 = timed(X.float(), seconds_budget / 3)
     return {
         "value": round(2.0 * M * K * N / per / 1e12, 4),
         "unit": "TFLOP/s",
@@ -330,6 +337,11 @@ def prefill_cpu_baseline(seconds_budget):
         "kind": "port",
         "sample": f"up K=4096 N=14336 at M={M} fp16: dequantize + X@W per call (quantization.py:452-454), "
                   f"torch CPU, {n} calls, {per:.2f} s/call; os.cpu_count()={os.cpu_count()}",
+        "secondary": {
+            "value": round(2.0 * M32 * K * N / per32 / 1e12, 4),
+            "unit": "TFLOP/s",
+            "sample": f"the same at fp32 (X.float() @ dequant_f32), M={M32}, {n32} calls, {per32:.2f} s/call",
+        },
     }
 
 
@@ -435,15 +447,22 @@ def cpu_baseline(seconds_budget):
     W = (rng.standard_normal((K, N)) * 0.02).astype(np.float32)
     blocks = torch.from_numpy(ref.quantize_llama_rule(W))
     X = torch.from_numpy(rng.standard_normal((1, K)).astype(np.float16))
-    ref.fallback_torch_cpu(X, blocks)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        ref.fallback_torch_cpu(X, blocks)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds_budget or n >= 10000:
-            break
+
+    def timed(x, budget):
+        ref.fallback_torch_cpu(x, blocks)  # warm-up
+        n, t0 = 0, time.perf_counter()
+        while True:
+            ref.fallback_torch_cpu(x, blocks)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget or n >= 10000:
+                return n, el
+
+    n, el = timed(X, seconds_budget * 2 / 3)
     per = el / n
+    # The secondary figure: the same call at fp32 (X.float() @ dequant_f32).
+    n32, el32 = timed(X.float(), seconds_budget / 3)
+    per32 = el32 / n32
     return {
         "value": wbytes(K, N) / per / 1e9,
         "unit": "GB/s",
@@ -452,6 +471,12 @@ def cpu_baseline(seconds_budget):
         "sample": f"O-proj K=N=4096 M=1 fp16: dequantize + X@W per call (quantization.py:452-454), "
                   f"torch CPU, {n} calls in {el:.1f}s ({per * 1e3:.2f} ms/call); "
                   f"os.cpu_count()={os.cpu_count()}",
+        "secondary": {
+            "value": wbytes(K, N) / per32 / 1e9,
+            "unit": "GB/s",
+            "sample": f"the same at fp32 (X.float() @ dequant_f32), {n32} calls in {el32:.1f}s "
+                      f"({per32 * 1e3:.2f} ms/call)",
+        },
     }
 
 
