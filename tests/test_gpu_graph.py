@@ -37,7 +37,8 @@ def _replay_check(dev, fn, out_ref, reps=4):
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (1, 4096, 128256 // 16), (8, 4096, 2048),
-                                   (128, 4096, 1024), (512, 11008, 512)])
+                                   (16, 14336, 4096), (128, 4096, 1024), (512, 11008, 512),
+                                   (2048, 4096, 14336), (2048, 14336, 4096)])
 def test_q4_0_graph_replay(mo, dev, M, K, N):
     g = torch.Generator(device=dev).manual_seed(M + N)
     W = torch.randn(K, N, generator=g, device=dev) * 0.02
@@ -57,3 +58,14 @@ def test_int4_graph_replay(mo, dev, M, K, N):
     X = torch.randn(M, K, generator=g, device=dev).half()
     ref = mo.matmul_int4(X, packed, s, z, gs).float().cpu().numpy()
     _replay_check(dev, lambda: mo.matmul_int4(X, packed, s, z, gs), ref)
+
+
+def test_q4_0_grouped_graph_replay(mo, dev):
+    """Gate and up in one launch, captured: every replay equals the eager call."""
+    g = torch.Generator(device=dev).manual_seed(5)
+    K, N = 4096, 11008
+    blocks = [mo.quantize_ggml_q4_0_llama(torch.randn(K, N, generator=g, device=dev) * 0.02) for _ in range(2)]
+    X = torch.randn(1, K, generator=g, device=dev).half()
+    refs = [y.float().cpu().numpy() for y in mo.matmul_ggml_q4_0_grouped(X, blocks)]
+    ref = np.concatenate(refs, axis=1)
+    _replay_check(dev, lambda: torch.cat(mo.matmul_ggml_q4_0_grouped(X, blocks), dim=1), ref)
