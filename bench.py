@@ -35,6 +35,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -106,10 +107,12 @@ def make_weights(mo, torch, K, N, seed, dev, outliers=False):
     return b
 
 
-def time_region(torch, stream, fn, steps, warmup, min_warm_s=0.2):
+def time_region(torch, stream, fn, steps, warmup, min_warm_s=0.2, stats=None):
     """Run fn(i) at least `warmup` times and for at least `min_warm_s` seconds (the
     GPU clocks ramp up after host-side setup), then time `steps` calls between HIP
-    events on `stream`."""
+    events on `stream`.  With a `stats` dict, events also split the same region into
+    up to 10 chunks and stats["median_call_s"] gets the median time per call over
+    the chunks."""
     t_w = time.perf_counter()
     i = 0
     with torch.cuda.stream(stream):
@@ -121,14 +124,26 @@ def time_region(torch, stream, fn, steps, warmup, min_warm_s=0.2):
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    chunk = max(1, steps // 10) if stats is not None else steps + 1
+    marks = []                                   # (event, calls so far)
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
         start.record(stream)
         for i in range(steps):
             fn(i)
+            if (i + 1) % chunk == 0 and i + 1 < steps:
+                ev = torch.cuda.Event(enable_timing=True)
+                ev.record(stream)
+                marks.append((ev, i + 1))
         end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    if stats is not None:
+        per, prev, prev_n = [], start, 0
+        for ev, n in marks + [(end, steps)]:
+            per.append(prev.elapsed_time(ev) / 1e3 / (n - prev_n))
+            prev, prev_n = ev, n
+        stats["median_call_s"] = statistics.median(per)
     return start.elapsed_time(end) / 1e3, wall
 
 
@@ -225,8 +240,10 @@ def decode_bench(mo, torch, dev, args):
         fn = one_step
         launches_per_call = len(DECODE_LAYER)
         calls = args.steps
-        secs, wall = time_region(torch, stream, fn, calls, args.warmup)
+        st = {}
+        secs, wall = time_region(torch, stream, fn, calls, args.warmup, stats=st)
         steps = calls
+        median_step_s = st["median_call_s"]
     else:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
@@ -246,8 +263,10 @@ def decode_bench(mo, torch, dev, args):
             else:
                 singles[i - full].replay()
 
-        secs, wall = time_region(torch, stream, fn, full + rem, max(1, args.warmup // R))
+        st = {}
+        secs, wall = time_region(torch, stream, fn, full + rem, max(1, args.warmup // R), stats=st)
         steps = args.steps
+        median_step_s = st["median_call_s"] / R if full else secs / steps
     bytes_step = sum(wbytes(K, N) for _, K, N in DECODE_LAYER)
     xy_step = sum(2 * K + 2 * N for _, K, N in DECODE_LAYER)
     read_s = read_ceiling(torch, stream, [w for layer in layers for w in layer], 20) / R
@@ -272,7 +291,7 @@ def decode_bench(mo, torch, dev, args):
     return {
         "read_ceiling_s": read_s,
         "grouped_step_s": gsecs / (reps * R),
-        "seconds": secs, "steps": steps, "wall": wall,
+        "seconds": secs, "steps": steps, "wall": wall, "median_step_s": median_step_s,
         "bytes_step": bytes_step, "xy_step": xy_step,
         "launches_step": len(DECODE_LAYER), "copies": R,
         "weight_pool_bytes": bytes_step * R,
@@ -288,10 +307,12 @@ def prefill_bench(mo, torch, dev, iters=30, warmup=10):
         x = torch.randn(M, K, generator=g, device=dev).half()
         with torch.cuda.stream(stream):
             mo.matmul_ggml_q4_0(x, w)
-        secs, _ = time_region(torch, stream, lambda i: mo.matmul_ggml_q4_0(x, w), iters, warmup)
+        st = {}
+        secs, _ = time_region(torch, stream, lambda i: mo.matmul_ggml_q4_0(x, w), iters, warmup, stats=st)
         t = secs / iters
         fl = 2.0 * M * N * K
-        out.append({"name": name, "M": M, "K": K, "N": N, "ms": t * 1e3, "tflops": fl / t / 1e12})
+        out.append({"name": name, "M": M, "K": K, "N": N, "ms": t * 1e3, "median_ms": st["median_call_s"] * 1e3,
+                    "tflops": fl / t / 1e12})
         del w, x
     return out
 
@@ -562,6 +583,7 @@ def main():
         "steps": dec["steps"],
         "warmup": args.warmup,
         "ms_per_step": round(t_step * 1e3, 5),
+        "median_ms_per_step": round(dec["median_step_s"] * 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
