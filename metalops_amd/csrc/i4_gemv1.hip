@@ -61,6 +61,7 @@ constexpr int I1_STEP = 2048;    // 4-bit weight bytes per step and tile (16 byt
 constexpr int I1_R = 3;          // ring slots (steps) per wave
 constexpr int I1_XB = 1024;      // activation bytes per wave (16 steps)
 constexpr int I1_SMAX = 16;      // K splits at most
+constexpr int I1_NT = 2;         // cache policy of the weight copies: non-temporal (read once)
 
 struct I4Gemv1Args {
     const _Float16 *X;
@@ -168,7 +169,8 @@ i4_gemv1_kernel(I4Gemv1Args a) {
 #pragma unroll
             for (int q = 0; q < WROWS / 8; ++q)           // byte rows 8q..8q+7
                 __builtin_amdgcn_global_load_lds((void *)(src + (int64_t)8 * q * N),
-                                                 (__attribute__((address_space(3))) void *)(dst + 1024 * q), 16, 0, 0);
+                                                 (__attribute__((address_space(3))) void *)(dst + 1024 * q), 16, 0,
+                                                 I1_NT);
             if constexpr (MR) {
 #pragma unroll
                 for (int rb = 0; rb < RB; ++rb)
