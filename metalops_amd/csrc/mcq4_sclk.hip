@@ -64,7 +64,7 @@ __global__ void __launch_bounds__(256) read_probe_kernel(const uint4_t *p, size_
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         const size_t i = base + 256 * u;
-        v[u] = i < n16 ? p[i] : uint4_t{0u, 0u, 0u, 0u};
+        v[u] = i < n16 ? __builtin_nontemporal_load(p + i) : uint4_t{0u, 0u, 0u, 0u};
     }
     uint32_t s = 0;
 #pragma unroll
