@@ -20,6 +20,7 @@ const char *const kNames[] = {
     "MCQ4_GEMM6_SPLIT",     // K splits of the prefill GEMM
     "MCQ4_GEMV_PATH",       // off: M == 1 through the batched decode kernels
     "MCQ4_GEMVM_SPLIT",     // 1 | 2 | 4 | 8: K splits of the batched decode GEMV
+    "MCQ4_GEMVM_HOIST",     // 0: batched decode GEMV rebuilds -S per item even with one batch per wave
     "MCQ4_DECODE_PATH",     // direct: the register-load decode kernel
     "MCQ4_GEMM2_BM",        // 128 | 256: row tile of the fallback prefill kernel
     "MCQ4_SPLIT_FOREIGN",   // mask: split-K splits treated as run on another XCD (recompute path)

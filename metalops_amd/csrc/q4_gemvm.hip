@@ -59,7 +59,10 @@ struct GemvMArgs {
 
 // RB row blocks of 16 activation rows (M <= 16 RB): each K-block row's B
 // operand is built once and feeds the MFMAs of every row block.
-template <int WAVES, int TPW, int RB, int GR>
+// HOIST: every wave has at most one batch (launcher), so its activations are
+// loaded once, and x' and -S are built once per wave: one MFMA per K-block row
+// instead of two (the registers the next batch's activations would take hold -S).
+template <int WAVES, int TPW, int RB, int GR, bool HOIST = false>
 __global__ void __launch_bounds__(WAVES * 64)
 q4_gemvm_kernel(GemvMArgs a) {
     static_assert(GR == 16 || (RB == 1 && (GR == 4 || GR == 8)), "row groups");
@@ -124,11 +127,14 @@ q4_gemvm_kernel(GemvMArgs a) {
     // Issue cursor: a batch's activation loads go right before its first copy.
     int im = 0, ij = 0, islot = 0;
     auto issue_next = [&]() {
-        if (ij == 0) load_x(im);
+        if (!HOIST && ij == 0) load_x(im);
         copy_item(im, ij, islot);
         islot ^= 1;
         if (++ij == ntl) { ij = 0; ++im; }
     };
+    if constexpr (HOIST) {
+        if (nmine > 0) load_x(0);
+    }
     if (nmine > 0) issue_next();
 
     const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
@@ -151,6 +157,7 @@ q4_gemvm_kernel(GemvMArgs a) {
     for (int m = 0; m < nbm; ++m) {
         const int rows = min(GM_B, a.nb - (b0 + wave + WAVES * m) * GM_B);
         half8_t xq[RB][GM_B];
+        float4_t nsh[HOIST ? RB : 1][HOIST ? GM_B : 1];
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -163,6 +170,7 @@ q4_gemvm_kernel(GemvMArgs a) {
                                __builtin_amdgcn_perm(x[3], x[1], 0x05040100u),     // x2, x6
                                bitcast<uint32_t>(bitcast<half2_t>(h37) * s16)};
             xq[rb][u] = bitcast<half8_t>(v);
+            if constexpr (HOIST) nsh[rb][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb][u], negc, z, 0, 0, 0);
         }
 #pragma unroll
         for (int j = 0; j < TPW; ++j) {
@@ -189,7 +197,9 @@ q4_gemvm_kernel(GemvMArgs a) {
                     // 16-wave workgroup fits in 128 VGPRs (the MFMA pipe has room).
 #pragma unroll
                     for (int rb = 0; rb < RB; ++rb) {
-                        const float4_t ns = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb][u], negc, z, 0, 0, 0);
+                        float4_t ns;
+                        if constexpr (HOIST) ns = nsh[rb][u];
+                        else ns = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb][u], negc, z, 0, 0, 0);
                         const float4_t blk =
                             __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb][u], bitcast<half8_t>(bq), ns, 0, 0, 0);
                         if constexpr (GR == 4) {
@@ -311,7 +321,7 @@ static size_t gemvm_lds_bytes(int waves, int tpw) {
     return (size_t)waves * 2 * GM_SLOT + (size_t)tpw * waves * 256 * sizeof(float);
 }
 
-template <int WAVES, int TPW, int RB, int GR>
+template <int WAVES, int TPW, int RB, int GR, bool HOIST>
 static hipError_t launch_gemvm_t(const GemvMArgs &a, int grid, hipStream_t s) {
     const size_t lds = gemvm_lds_bytes(WAVES, TPW);
     static std::atomic<uint64_t> done{0};
@@ -320,13 +330,13 @@ static hipError_t launch_gemvm_t(const GemvMArgs &a, int grid, hipStream_t s) {
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)q4_gemvm_kernel<WAVES, TPW, RB, GR>,
+        e = hipFuncSetAttribute((const void *)q4_gemvm_kernel<WAVES, TPW, RB, GR, HOIST>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
     const int gx = a.tickets ? (grid + 7) / 8 * 8 : grid;
-    hipLaunchKernelGGL((q4_gemvm_kernel<WAVES, TPW, RB, GR>), dim3(gx, a.S), dim3(WAVES * 64), lds, s, a);
+    hipLaunchKernelGGL((q4_gemvm_kernel<WAVES, TPW, RB, GR, HOIST>), dim3(gx, a.S), dim3(WAVES * 64), lds, s, a);
     if (a.S > 1 && !a.tickets) {
         const int64_t n = (int64_t)a.M * 16 * a.ntiles;
         hipLaunchKernelGGL(q4_gemvm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
@@ -334,14 +344,22 @@ static hipError_t launch_gemvm_t(const GemvMArgs &a, int grid, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int WAVES, int RB, int GR = 16>
-static hipError_t launch_gemvm_w(const GemvMArgs &a, int grid, int tpw, hipStream_t s) {
+template <int WAVES, int RB, int GR, bool HOIST>
+static hipError_t launch_gemvm_h(const GemvMArgs &a, int grid, int tpw, hipStream_t s) {
     switch (tpw) {
-        case 1: return launch_gemvm_t<WAVES, 1, RB, GR>(a, grid, s);
-        case 2: return launch_gemvm_t<WAVES, 2, RB, GR>(a, grid, s);
-        case 3: return launch_gemvm_t<WAVES, 3, RB, GR>(a, grid, s);
-        default: return launch_gemvm_t<WAVES, 4, RB, GR>(a, grid, s);
+        case 1: return launch_gemvm_t<WAVES, 1, RB, GR, HOIST>(a, grid, s);
+        case 2: return launch_gemvm_t<WAVES, 2, RB, GR, HOIST>(a, grid, s);
+        case 3: return launch_gemvm_t<WAVES, 3, RB, GR, HOIST>(a, grid, s);
+        default: return launch_gemvm_t<WAVES, 4, RB, GR, HOIST>(a, grid, s);
     }
+}
+
+template <int WAVES, int RB, int GR = 16>
+static hipError_t launch_gemvm_w(const GemvMArgs &a, int grid, int tpw, bool hoist, hipStream_t s) {
+    if constexpr (RB == 1) {
+        if (hoist) return launch_gemvm_h<WAVES, RB, GR, true>(a, grid, tpw, s);
+    }
+    return launch_gemvm_h<WAVES, RB, GR, false>(a, grid, tpw, s);
 }
 
 // 2 <= M <= 32 (two row blocks above 16), 16-byte aligned weights and
@@ -413,11 +431,14 @@ hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
         a.part = (float *)((char *)ws + COUNTER_BYTES);
         if (!opt_is("MCQ4_XCD_LOCAL", '0') && p.S <= 8) a.tickets = (uint64_t *)ws;
     }
-    if (M > 16) return launch_gemvm_w<8, 2>(a, p.grid, p.tpw, s);
+    // One batch per wave at most: the activations and -S once per wave
+    // (MCQ4_GEMVM_HOIST=0 turns it off).
+    const bool hoist = p.bps <= p.waves && !opt_is("MCQ4_GEMVM_HOIST", '0');
+    if (M > 16) return launch_gemvm_w<8, 2>(a, p.grid, p.tpw, hoist, s);
     // M <= 16: 16-wave workgroups (gemvm_plan).
-    if (M <= 4) return launch_gemvm_w<16, 1, 4>(a, p.grid, p.tpw, s);
-    if (M <= 8) return launch_gemvm_w<16, 1, 8>(a, p.grid, p.tpw, s);
-    return launch_gemvm_w<16, 1>(a, p.grid, p.tpw, s);
+    if (M <= 4) return launch_gemvm_w<16, 1, 4>(a, p.grid, p.tpw, hoist, s);
+    if (M <= 8) return launch_gemvm_w<16, 1, 8>(a, p.grid, p.tpw, hoist, s);
+    return launch_gemvm_w<16, 1>(a, p.grid, p.tpw, hoist, s);
 }
 
 }  // namespace mcq4

@@ -225,6 +225,7 @@ PATHS = {
 
     "decode_lds_m1": {"MCQ4_GEMV_PATH": "off"},
     "gemvm": {},
+    "gemvm_nohoist": {"MCQ4_GEMVM_HOIST": "0"},
     "gemvm_split2": {"MCQ4_GEMVM_SPLIT": "2"},
     "gemvm_split8": {"MCQ4_GEMVM_SPLIT": "8"},
     "gemvm_split4": {"MCQ4_GEMVM_SPLIT": "4"},
@@ -260,6 +261,8 @@ PATH_SHAPES = {
     "decode_lds_m1": [(1, 352, 264), (1, 4096, 1032)],
     "gemvm": [(2, 32, 16), (3, 352, 264), (4, 1024, 4104), (5, 11008, 512), (8, 4096, 14336),
               (11, 2048, 1040), (16, 14336, 4096), (16, 352, 8200)],
+    # One batch per wave (the hoisted -S form by default) with it turned off.
+    "gemvm_nohoist": [(16, 14336, 4096), (8, 4096, 14336), (3, 352, 264), (16, 352, 8200)],
     "gemvm_split2": [(2, 352, 264), (9, 4096, 1040), (16, 14336, 4096), (5, 11008, 512)],
     "gemvm_split8": [(16, 2048, 1032), (3, 14336, 512), (12, 512, 200)],
     "gemvm_split4": [(16, 4096, 1040), (6, 11008, 264), (13, 352, 8200)],
@@ -293,7 +296,7 @@ PATH_SHAPES = {
 @pytest.mark.parametrize("path,M,K,N", [(p, *s) for p, shapes in PATH_SHAPES.items() for s in shapes])
 def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM", "MCQ4_GEMV_PATH",
-              "MCQ4_GEMM6_SPLIT", "MCQ4_GEMVM_SPLIT", "MCQ4_XCD_LOCAL"):
+              "MCQ4_GEMM6_SPLIT", "MCQ4_GEMVM_SPLIT", "MCQ4_GEMVM_HOIST", "MCQ4_XCD_LOCAL"):
         monkeypatch.delenv(k, raising=False)
     for k, v in PATHS[path].items():
         monkeypatch.setenv(k, v)
