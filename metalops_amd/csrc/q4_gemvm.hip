@@ -380,8 +380,10 @@ bool gemvm_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M
 // traffic; the fp32 partials are summed in split order by the last split of each
 // workgroup (XCD-local exchange) or, with MCQ4_XCD_LOCAL=0, by a second kernel
 // (M=16 K=14336 N=4096: 15.6 us with the second kernel, was 18.7; M=8: 13.4,
-// was 14.3; at M <= 4 and with several tiles per workgroup it does not pay).
-// MCQ4_GEMVM_SPLIT=1|2|4|8 overrides.
+// was 14.3).  Up to 16 rows the split goes on until every wave has one batch
+// at most, the form with the activations and -S built once per wave (M=4
+// K=14336 N=4096: 11.6 us with four splits against 12.2 with none; M=8: 12.4
+// against 12.5 with two).  MCQ4_GEMVM_SPLIT=1|2|4|8 overrides.
 struct GmPlan {
     int waves, tpw, grid, S, bps;
 };
@@ -391,10 +393,13 @@ static GmPlan gemvm_plan(int64_t M, int64_t K, int64_t N) {
     // Two row blocks: 8-wave workgroups, one per CU (their registers fill the SIMDs).
     if (M > 16) waves = 8;
     const int cap = waves == 8 && M <= 16 ? 512 : 256;
-    int S = M >= 8 && ntiles <= cap && nbt >= 2 * waves ? 2 : 1;
-    // Past 8 rows four splits pay once each still has 12+ batches (M=16
-    // K=14336 N=4096: 13.2 against 14.2 us with two; M=8: 11.0 either way).
-    if (S == 2 && M > 8 && nbt >= 3 * waves) S = 4;
+    int S = 1;
+    if (M <= 16) {
+        if (ntiles <= cap)
+            while (S < 8 && (nbt + S - 1) / S > waves) S *= 2;
+    } else if (ntiles <= cap && nbt >= 2 * waves) {
+        S = 2;
+    }
     if (const char *env = opt("MCQ4_GEMVM_SPLIT")) {
         const int v = atoi(env);
         S = v == 2 || v == 4 || v == 8 ? v : 1;
