@@ -257,7 +257,8 @@ def matmul_ggml_q4_0_grouped(X: torch.Tensor, weights: Sequence[torch.Tensor]) -
     K = num_blocks_per_col * QK4_0
     assert X.shape[1] == K, f"X K dim ({X.shape[1]}) must match weight K ({K})"
     _require_device(X, *weights)
-    if X.dim() != 2 or X.dtype != torch.float16 or X.shape[0] != 1 or N % 16 or len(weights) > 4:
+    if (X.dim() != 2 or X.dtype != torch.float16 or X.shape[0] != 1 or N % 16 or N == 0 or K == 0
+            or len(weights) > 4):
         return [matmul_ggml_q4_0(X, w) for w in weights]
     for w in weights:
         if w.dtype != torch.uint8 or w.shape[2] != BLOCK_Q4_0_SIZE:
@@ -275,8 +276,15 @@ def matmul_ggml_q4_0_grouped(X: torch.Tensor, weights: Sequence[torch.Tensor]) -
     wp = (ctypes.c_void_p * len(ws))(*[w.data_ptr() for w in ws])
     yp = (ctypes.c_void_p * len(Ys))(*[y.data_ptr() for y in Ys])
     stream = _stream(X.device)
-    with torch.cuda.device(x.device):
+    # Shapes the one launch does not cover run per weight inside the library,
+    # with the workspace a single-weight call would get.
+    need = int(_lib.lib.mcq4_matmul_workspace_bytes(1, K, N))
+    ws_buf, ws_ptr, ws_bytes = None, None, 0
+    if need:
+        ws_buf = _workspace.get(x.device, stream, need)
+        ws_ptr, ws_bytes = ws_buf.data_ptr(), ws_buf.numel()
+    with torch.cuda.device(x.device), _workspace.guard(ws_buf, stream):
         _lib.check(_lib.lib.mcq4_matmul_q4_0_f16_grouped(x.data_ptr(), x.stride(0), len(ws), wp, yp, N, 1, K, N,
-                                                         None, 0, stream),
+                                                         ws_ptr, ws_bytes, stream),
                    "mcq4_matmul_q4_0_f16_grouped")
     return Ys

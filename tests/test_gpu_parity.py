@@ -403,3 +403,13 @@ def test_matmul_grouped_other_cases(dev):
     other = torch.from_numpy(ref.quantize_llama_rule(_weights(K, 64, seed=9).numpy())).to(dev)
     with pytest.raises(RuntimeError):
         mo.matmul_ggml_q4_0_grouped(_acts(1, K, seed=3).to(dev), [blocks[0], other])
+    # K above the one-launch kernel's limit: per weight inside the library, same results.
+    K2, N2 = 16416, 64
+    big = [torch.from_numpy(ref.quantize_llama_rule(_weights(K2, N2, seed=20 + g).numpy())).to(dev)
+           for g in range(2)]
+    X2 = _acts(1, K2, seed=4).to(dev)
+    for y, b in zip(mo.matmul_ggml_q4_0_grouped(X2, big), big):
+        assert torch.equal(y.view(torch.int16), mo.matmul_ggml_q4_0(X2, b).view(torch.int16))
+    # N == 0: empty outputs, as for one weight.
+    empty = [torch.zeros((K // 32, 0, 18), dtype=torch.uint8, device=dev) for _ in range(2)]
+    assert [tuple(y.shape) for y in mo.matmul_ggml_q4_0_grouped(_acts(1, K, seed=5).to(dev), empty)] == [(1, 0)] * 2
