@@ -303,7 +303,8 @@ int mcq4_measure_sclk(uint64_t *ticks, int iters, void *stream);
  * Measurement helper; no counterpart in the reference (the benchmark uses it
  * for the read ceiling beside each decode figure: the HBM rate a plain read of
  * the same bytes, in one launch, reaches).  Reads the floor(bytes/16)*16 bytes
- * at `src` (16-byte aligned) with 256-thread workgroups of 16 KiB each and
+ * at `src` (16-byte aligned) with 256-thread workgroups of 16 KiB each
+ * (non-temporal loads, the faster policy for data read once) and
  * writes *sink (a device uint32) only in the unlikely event that the XOR of a
  * workgroup's data equals 0x9E3779B9.
  */
