@@ -390,6 +390,29 @@ def test_matmul_grouped(dev, K, N, count):
         _check_rows(Ys[g].float().cpu().numpy(), mo.matmul_ggml_q4_0(X.to(dev), bd[g]).float().cpu().numpy())
 
 
+def _random_grouped_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        K = 32 * int(rng.integers(1, 200))
+        N = 16 * int(rng.integers(1, 700))
+        cases.append((K, N, int(rng.integers(2, 5))))
+    return cases
+
+
+@pytest.mark.parametrize("K,N,count", _random_grouped_cases(16, 20261203))
+def test_matmul_grouped_random_shapes(dev, K, N, count):
+    """Random grouped shapes (16-column multiples, 2..4 weights): each output within
+    the bar of the oracle."""
+    print(f"random grouped matmul K={K} N={N} count={count}", flush=True)
+    mo = _mo()
+    blocks = [ref.quantize_ref_rule(_weights(K, N, seed=K * 7 + N + g).numpy()) for g in range(count)]
+    X = _acts(1, K, seed=K + N)
+    Ys = mo.matmul_ggml_q4_0_grouped(X.to(dev), [torch.from_numpy(b).to(dev) for b in blocks])
+    for g in range(count):
+        _check_rows(Ys[g].float().cpu().numpy(), ref.matmul_f32(X.numpy(), blocks[g]))
+
+
 def test_matmul_grouped_other_cases(dev):
     """Rows > 1, more than four weights and N % 16 != 0 take the per-weight path
     (the same results bit for bit); mismatched shapes are rejected."""
