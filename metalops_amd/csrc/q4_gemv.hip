@@ -110,16 +110,22 @@ q4_gemv_dma_kernel(GemvArgs a) {
     const int G = (int)gridDim.x, G8 = G & ~7;
     int wg = (int)blockIdx.x;
     if (wg < G8) wg = (wg & 7) * (G8 >> 3) + (wg >> 3);
-    // Tile j of this workgroup: wg + j*G.
-    const int ntl = min(TPW, (a.ntiles - wg + G - 1) / G);         // >= 1 (grid <= ntiles)
+    // Tile j of this workgroup: wg + j*G.  Everything up to the first copy is
+    // on every launch's critical path, so no integer divisions here: the tile
+    // count by compares, the weight of a tile by subtracting tiles_per_w.
+    int ntl = 0;                                                  // >= 1 (grid <= ntiles)
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) ntl += wg + j * G < a.ntiles ? 1 : 0;
     auto tile = [&](int j) { return wg + j * G; };
     // Weight and output bases of tile j (the weight index is uniform: scalar selects).
     const uint8_t *wt[TPW];
     _Float16 *yt[TPW];
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
-        const int t = j < ntl ? tile(j) : 0;
-        const int gi = t / a.tiles_per_w, lt = t - gi * a.tiles_per_w;
+        int lt = j < ntl ? tile(j) : 0, gi = 0;
+#pragma unroll
+        for (int r = 1; r < GV_GROUP_MAX; ++r)
+            if (lt >= a.tiles_per_w) { lt -= a.tiles_per_w; gi = r; }
         const uint8_t *w = gi == 0 ? a.W[0] : gi == 1 ? a.W[1] : gi == 2 ? a.W[2] : a.W[3];
         _Float16 *y = gi == 0 ? a.Y[0] : gi == 1 ? a.Y[1] : gi == 2 ? a.Y[2] : a.Y[3];
         wt[j] = w + (int64_t)lt * ROWB;
