@@ -69,6 +69,7 @@ struct I4Gemv1Args {
     const void *scales, *zeros;
     _Float16 *Y;
     int K, N, nsteps, spg, spw, S;
+    int spg_log2;         // log2(spg) when spg is a power of two, else -1
     int ngr_max;          // scale/zero slots per wave
     int wave_bytes;       // LDS bytes per wave
     int M;                // activation rows (1 .. 16)
@@ -133,8 +134,11 @@ i4_gemv1_kernel(I4Gemv1Args a) {
 
     if (ns > 0) {
         // ---- scale/zero rows of the wave's groups, then its activations ----
-        const int g_first = s_begin / a.spg;
-        const int ngr = (s_begin + ns - 1) / a.spg - g_first + 1;      // <= ngr_max by launch
+        // Group of a step: a shift for the usual power-of-two group sizes (no
+        // integer division ahead of the first copy), else a division.
+        auto group_of = [&](int step) { return a.spg_log2 >= 0 ? step >> a.spg_log2 : step / a.spg; };
+        const int g_first = group_of(s_begin);
+        const int ngr = group_of(s_begin + ns - 1) - g_first + 1;      // <= ngr_max by launch
         {
             // One 16-byte-per-lane copy per group: the scale row's PPR pieces, then
             // the zero row's (slot bytes 0 .. 2*128*ESZ); for 16-bit dtypes lanes
@@ -533,6 +537,9 @@ hipError_t launch_i4_gemv1(const _Float16 *X, int64_t ldx, const uint8_t *P, con
     I4Gemv1Args a;
     a.X = X; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y;
     a.K = K; a.N = N; a.nsteps = K / 32; a.spg = gs / 32; a.spw = c.spw; a.S = c.S;
+    a.spg_log2 = -1;
+    for (int b = 0; b < 30; ++b)
+        if ((1 << b) == a.spg) a.spg_log2 = b;
     a.ngr_max = c.ngr_max;
     a.M = M; a.ldx = ldx; a.ldy = ldy;
     a.wave_bytes = (int)i1_wave_bytes(M, c, wb);

@@ -80,7 +80,11 @@ q4_gemvm_kernel(GemvMArgs a) {
     const int G = (int)gridDim.x, G8 = G & ~7;
     int wg = (int)blockIdx.x;
     if (wg < G8) wg = (wg & 7) * (G8 >> 3) + (wg >> 3);
-    const int ntl = min(TPW, (a.ntiles - wg + G - 1) / G);
+    // Tiles of this workgroup (wg + j G) by compares: no integer division ahead
+    // of the first copy.
+    int ntl = 0;
+#pragma unroll
+    for (int j = 0; j < TPW; ++j) ntl += wg + j * G < a.ntiles ? 1 : 0;
     if (ntl <= 0) return;                         // grid padding (XCD-local exchange)
     // This split's batches [b0, b0 + nbs); wave w owns b0 + w, b0 + w + WAVES, ...
     const int sp = (int)blockIdx.y;
