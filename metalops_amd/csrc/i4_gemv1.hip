@@ -58,7 +58,7 @@ MCQ4_SPLIT_FALLBACK_COUNTER(i4_gemv1_split_fallbacks)
 constexpr int I1_W = 8;          // waves per workgroup
 constexpr int I1_TC = 128;       // tile columns
 constexpr int I1_STEP = 2048;    // 4-bit weight bytes per step and tile (16 byte rows x 128)
-constexpr int I1_R = 3;          // ring slots (steps) per wave
+constexpr int I1_R = 2;          // ring slots (steps) per wave
 constexpr int I1_XB = 1024;      // activation bytes per wave (16 steps)
 constexpr int I1_SMAX = 16;      // K splits at most
 constexpr int I1_NT = 2;         // cache policy of the weight copies: non-temporal (read once)
@@ -445,6 +445,12 @@ static size_t i1_wave_bytes(int64_t M, const I1Cfg &c, int wb) {
                  : (size_t)I1_R * stepw + I1_XB + c.ngr_max * I1_SZSLOT;
 }
 
+// LDS of a workgroup: the waves' rings and slots, and at least the epilogue's
+// wave sums ([I1_W waves][16 rows][128] floats when M > 1), which reuse them.
+static size_t i1_lds_bytes(int64_t M, size_t wave_bytes) {
+    return std::max((size_t)I1_W * wave_bytes, (size_t)I1_W * (M > 1 ? 16 : 1) * I1_TC * sizeof(float));
+}
+
 // 1 <= M <= 32 with 4-bit weights (wb = 4), M <= 16 with int8 (wb = 8), whole 128-column tiles, group size a multiple
 // of 32, 16-byte aligned operands (and activation rows), and a split count
 // within bounds.  MCQ4_I4_GEMV1=0 disables it; =1 limits it to M == 1; =4 to 4-bit
@@ -470,7 +476,7 @@ bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void 
         return false;
     if (M > 1 && (ldx % 8 || ldx < K)) return false;
     const I1Cfg c = i4_gemv1_config(K, N, gs);
-    return c.S <= I1_SMAX && (size_t)I1_W * i1_wave_bytes(M, c, wb) <= 160 * 1024;
+    return c.S <= I1_SMAX && i1_lds_bytes(M, i1_wave_bytes(M, c, wb)) <= 160 * 1024;
 }
 
 size_t i4_gemv1_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs) {
@@ -487,7 +493,7 @@ static bool use_xcd_local(int ntiles, int S) {
 
 template <int SZ, int ACT, bool XL, int RB, int WB>
 static hipError_t launch_i1(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
-    const size_t lds = (size_t)I1_W * a.wave_bytes;
+    const size_t lds = i1_lds_bytes(a.M, a.wave_bytes);
     static std::atomic<uint64_t> done{0};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -549,7 +555,7 @@ hipError_t launch_i4_gemv1(const _Float16 *X, int64_t ldx, const uint8_t *P, con
         a.counters = (uint32_t *)ws;
         a.part = (float *)((char *)ws + COUNTER_BYTES);
     }
-    if ((size_t)I1_W * a.wave_bytes > 160 * 1024) return hipErrorInvalidValue;
+    if (i1_lds_bytes(M, a.wave_bytes) > 160 * 1024) return hipErrorInvalidValue;
     const int ntiles = N / I1_TC;
     if (sz_dt == DT_F32) return launch_i1_wb<DT_F32>(a, ntiles, act, wb, s);
     if (sz_dt == DT_F16) return launch_i1_wb<DT_F16>(a, ntiles, act, wb, s);
