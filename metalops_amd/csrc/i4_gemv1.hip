@@ -454,23 +454,17 @@ static size_t i1_lds_bytes(int64_t M, size_t wave_bytes) {
 // 1 <= M <= 32 with 4-bit weights (wb = 4), M <= 16 with int8 (wb = 8), whole 128-column tiles, group size a multiple
 // of 32, 16-byte aligned operands (and activation rows), and a split count
 // within bounds.  MCQ4_I4_GEMV1=0 disables it; =1 limits it to M == 1; =4 to 4-bit
-// weights; =8 lifts the int8 size rule below.
+// weights (int8 then runs the register-ring GEMV).  With the 2-slot ring this
+// kernel ties the register ring on int8 at M <= 4 within 2% and beats it on
+// 4096x11008 (M = 1: 11.7 against 15.2 us), so int8 comes here at every size.
 bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void *X, int64_t ldx,
                         const void *P, const void *scales, const void *zeros, int wb) {
     int64_t mmax = wb == 4 ? 32 : 16;
-    // Int8 weights at M <= 4 on matrices above 32 Mi weights stay on the
-    // register-ring GEMV, measured faster there (graph replays, M = 1:
-    // 14336x4096 14.7 against 16.0 us, 4096x14336 16.7 against 17.0; M = 4
-    // 4096x14336 17.3 against 18.0); this kernel wins below (4096x4096 7.5
-    // against 8.8 us) and from M = 8 (M = 16 4096x14336 20.5 against 22.4).
-    bool i8_size_rule = wb == 8;
     if (const char *env = opt("MCQ4_I4_GEMV1")) {
         if (env[0] == '0') return false;
         if (env[0] == '1') mmax = 1;
         if (env[0] == '4' && wb != 4) return false;     // 4-bit only
-        if (env[0] == '8') i8_size_rule = false;        // int8 at every size
     }
-    if (i8_size_rule && M <= 4 && K * N > ((int64_t)1 << 25)) return false;
     if (M < 1 || M > mmax || K < 32 || K % 32 || gs % 32 || N % I1_TC || N / I1_TC > COUNTER_SLOTS) return false;
     if (((uintptr_t)X % 16) || ((uintptr_t)P % 16) || ((uintptr_t)scales % 16) || ((uintptr_t)zeros % 16))
         return false;

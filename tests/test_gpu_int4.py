@@ -442,7 +442,6 @@ def test_gemv1_int8(mo, dev, monkeypatch, M, K, N, gs, spw, sz):
         monkeypatch.delenv(k, raising=False)
     if spw is not None:
         monkeypatch.setenv("MCQ4_I4_SPW1", str(spw))
-    monkeypatch.setenv("MCQ4_I4_GEMV1", "8")            # every size, not only where it is the default
     q, s, z = _int8_weights(K, N, gs, sz, M + K + N + gs)
     args = [torch.from_numpy(q).to(dev), torch.from_numpy(s).to(TDT[sz]).to(dev),
             torch.from_numpy(z).to(TDT[sz]).to(dev)]
@@ -457,8 +456,6 @@ def test_gemv1_int8(mo, dev, monkeypatch, M, K, N, gs, spw, sz):
     Xw = torch.zeros(M, K + 64, dtype=torch.float16, device=dev)
     Xw[:, :K] = X
     assert torch.equal(mo.matmul_int8(Xw[:, :K], *args, gs).view(torch.int16), Y.view(torch.int16))
-    monkeypatch.delenv("MCQ4_I4_GEMV1")                 # default routing
-    _check_rows(mo.matmul_int8(X, *args, gs).float().cpu().numpy(), Yref)
     monkeypatch.setenv("MCQ4_I4_GEMV1", "4")            # async-copy GEMV for 4-bit weights only
     _check_rows(mo.matmul_int8(X, *args, gs).float().cpu().numpy(), Yref)
 
@@ -611,17 +608,17 @@ def test_decode_random_shapes(mo, dev, M, K, N, gs):
 
 @pytest.mark.parametrize("M,K,N,gs", _random_decode_shapes(12, 2025))
 def test_decode_random_shapes_int8(mo, dev, monkeypatch, M, K, N, gs):
-    """Seeded random int8 decode shapes on the async-copy GEMV (its size rule
-    lifted) and on the default routing, against the oracle."""
+    """Seeded random int8 decode shapes on the default routing (the async-copy
+    GEMV where it applies) and on the register-ring GEMV, against the oracle."""
     print(f"random int8 decode M={M} K={K} N={N} gs={gs}", flush=True)
     monkeypatch.delenv("MCQ4_I4_SPW1", raising=False)
     q, s, z = _int8_weights(K, N, gs, R.F16, M * 5 + K + N)
     args = [torch.from_numpy(q).to(dev), torch.from_numpy(s).half().to(dev), torch.from_numpy(z).half().to(dev)]
     X = torch.randn(M, K, generator=torch.Generator().manual_seed(K * 3 + M)).half().to(dev)
     Yref = R.matmul_int8_f32(X.float().cpu().numpy(), q, s, z, gs)
-    monkeypatch.setenv("MCQ4_I4_GEMV1", "8")
+    monkeypatch.delenv("MCQ4_I4_GEMV1", raising=False)
     _check_rows(mo.matmul_int8(X, *args, gs).float().cpu().numpy(), Yref)
-    monkeypatch.delenv("MCQ4_I4_GEMV1")
+    monkeypatch.setenv("MCQ4_I4_GEMV1", "4")
     _check_rows(mo.matmul_int8(X, *args, gs).float().cpu().numpy(), Yref)
 
 
