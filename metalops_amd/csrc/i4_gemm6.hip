@@ -306,6 +306,11 @@ i4_gemm6_kernel(I4GemmArgs a) {
         // 1: the other split ran on this XCD (read its partial from the L2);
         // 2: it did not (recompute it here).
         *last_flag = (prev & 0xFF) != 1 ? 0u : (xcd_ticket_local_mask(prev + inc, xcc, 2) & ~a.foreign) == 3u ? 1u : 2u;
+        if ((prev & 0xFF) == 1) {
+            // Both splits have drawn: the slot is free for the next launch now, so
+            // its reset overlaps the sum instead of trailing it.
+            __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         if (*last_flag == 2u) note_split_fallback();
     }
     __syncthreads();
@@ -351,7 +356,6 @@ i4_gemm6_kernel(I4GemmArgs a) {
             }
         }
     }
-    if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Plan: 128-row tiles; K split S = the largest power of two (<= 16, at least 16

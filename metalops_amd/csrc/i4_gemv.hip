@@ -353,7 +353,12 @@ i4_gemv_kernel(I4GemvArgs a) {
             const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const uint32_t local = xcd_ticket_local_mask(prev + inc, xcc, a.S) & ~a.foreign;
             *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u : 0x10000u | local;
-            if ((prev & 0xFF) == (uint64_t)(a.S - 1) && local != (1u << a.S) - 1) note_split_fallback();
+            if ((prev & 0xFF) == (uint64_t)(a.S - 1)) {
+                // Every split has drawn: the slot is free for the next launch now,
+                // so its reset overlaps the sum instead of trailing it.
+                __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (local != (1u << a.S) - 1) note_split_fallback();
+            }
         }
         __syncthreads();
         const uint32_t lf = *last_flag;
@@ -382,7 +387,6 @@ i4_gemv_kernel(I4GemvArgs a) {
             }
             if (col0 + cl < N) a.Y[(int64_t)row * a.ldy + col0 + cl] = (_Float16)activate<ACT>(sum);
         }
-        if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return;
     }
     for (int v = tid; v < M * TC; v += IW * 64) {
@@ -399,6 +403,7 @@ i4_gemv_kernel(I4GemvArgs a) {
         const uint32_t prev =
             __hip_atomic_fetch_add(&a.counters[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *last_flag = prev == (uint32_t)(a.S - 1) ? 1u : 0u;
+        if (prev == (uint32_t)(a.S - 1)) __hip_atomic_store(&a.counters[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!*last_flag) return;
@@ -420,7 +425,6 @@ i4_gemv_kernel(I4GemvArgs a) {
         }
         if (col0 + cl < N) a.Y[(int64_t)row * a.ldy + col0 + cl] = (_Float16)activate<ACT>(sum);
     }
-    if (tid == 0) __hip_atomic_store(&a.counters[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 struct I4GemvCfg {

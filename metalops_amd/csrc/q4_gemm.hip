@@ -208,6 +208,7 @@ q4_gemm_kernel(GemmArgs a) {
     if (tid == 0) {
         const uint32_t prev = atomicAdd(&a.counters[tile_id], 1u);
         last_flag = (prev == (uint32_t)(a.S - 1)) ? 1u : 0u;
+        if (last_flag) __hip_atomic_store(&a.counters[tile_id], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!last_flag) return;
@@ -221,7 +222,6 @@ q4_gemm_kernel(GemmArgs a) {
         const int m = m0 + v / BN, n = n0 + v % BN;
         if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (_Float16)s;
     }
-    if (tid == 0) __hip_atomic_store(&a.counters[tile_id], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- configuration ----------------------------------------------------------

@@ -293,6 +293,11 @@ q4_gemm6_kernel(Gemm6Args a) {
         // 1: the other split ran on this XCD (read its partial from the L2);
         // 2: it did not (recompute it here).
         *last_flag = (prev & 0xFF) != 1 ? 0u : (xcd_ticket_local_mask(prev + inc, xcc, 2) & ~a.foreign) == 3u ? 1u : 2u;
+        if ((prev & 0xFF) == 1) {
+            // Both splits have drawn: the slot is free for the next launch now, so
+            // its reset overlaps the sum instead of trailing it.
+            __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         if (*last_flag == 2u) note_split_fallback();
     }
     __syncthreads();
@@ -332,7 +337,6 @@ q4_gemm6_kernel(Gemm6Args a) {
                 if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (_Float16)v;
             }
         }
-    if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Sums the S fp32 partial tiles of every output tile in split order

@@ -271,7 +271,12 @@ q4_gemvm_kernel(GemvMArgs a) {
         const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const uint32_t local = xcd_ticket_local_mask(prev + inc, xcc, a.S) & ~a.foreign;
         *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u : 0x10000u | local;
-        if ((prev & 0xFF) == (uint64_t)(a.S - 1) && local != (1u << a.S) - 1) note_split_fallback();
+        if ((prev & 0xFF) == (uint64_t)(a.S - 1)) {
+            // Every split has drawn: the slot is free for the next launch now,
+            // so its reset overlaps the sum instead of trailing it.
+            __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (local != (1u << a.S) - 1) note_split_fallback();
+        }
     }
     __syncthreads();
     const uint32_t lf = *last_flag;
@@ -306,7 +311,6 @@ q4_gemvm_kernel(GemvMArgs a) {
             if (q < a.S) t += pv[q];
         a.Y[(int64_t)rr * a.ldy + n] = (_Float16)t;
     }
-    if (tid == 0) __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Sums the S fp32 partials of every output in split order (deterministic) and

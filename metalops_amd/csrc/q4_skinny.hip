@@ -186,6 +186,7 @@ q4_skinny_kernel(SkinnyArgs a) {
     if (tid == 0) {
         const uint32_t prev = atomicAdd(&a.counters[tile], 1u);
         last_flag = (prev == (uint32_t)(a.S - 1)) ? 1u : 0u;
+        if (last_flag) __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!last_flag) return;
@@ -203,7 +204,6 @@ q4_skinny_kernel(SkinnyArgs a) {
         const int n = n0 + t * 16 + (l & 15);
         if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (_Float16)s;
     }
-    if (tid == 0) __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---- launch configuration ---------------------------------------------------
