@@ -84,4 +84,55 @@ __device__ __forceinline__ float activate(float y) {
     }
 }
 
+// RMSNorm of one activation row (native/training_kernels.metal:425-488):
+// rstd = 1 / sqrt(sum(x^2) / K + eps) with the sum in fp32, and
+// x_norm = fp16((x * rstd) * w).  Every kernel that normalises a row sums in the
+// same order, so the fused and the two-kernel paths give identical bits:
+// RMS_WAVES waves; thread t (= 64 wave + lane) adds the squares of the
+// 8-element chunks t, t + 64 RMS_WAVES, ... (elements in order, fmaf), then
+// tail element 8 (K / 8) + t; an xor butterfly over 32, 16, ..., 1 sums each
+// wave's lanes (rms_sumsq_part); the wave totals are added in wave order
+// (rms_sumsq_total).  vec16: x is 16-byte aligned (one 16-byte load per chunk).
+constexpr int RMS_WAVES = 8;
+__device__ __forceinline__ float rms_sumsq_part(const _Float16 *x, int K, int t, bool vec16) {
+    float ss = 0.f;
+    const int nc = K >> 3;
+    for (int ch = t; ch < nc; ch += 64 * RMS_WAVES) {
+        _Float16 v[8];
+        if (vec16) {
+            const half8_t h = *(const half8_t *)(x + 8 * ch);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = h[i];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = x[8 * ch + i];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss = __builtin_fmaf((float)v[i], (float)v[i], ss);
+    }
+    if (8 * nc + t < K) {
+        const float v = (float)x[8 * nc + t];
+        ss = __builtin_fmaf(v, v, ss);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off, 64);
+    return ss;
+}
+__device__ __forceinline__ float rms_sumsq_total(const float *wave_sums) {
+    float ss = wave_sums[0];
+#pragma unroll
+    for (int w = 1; w < RMS_WAVES; ++w) ss += wave_sums[w];
+    return ss;
+}
+__device__ __forceinline__ float rms_rstd(float ss, int K, float eps) {
+    return 1.0f / sqrtf(ss / (float)K + eps);
+}
+// The product is rounded to fp32 and then to fp16, as the reference does.
+// Without the canonicalize (a no-op on a product, no instruction) the backend
+// folds the second multiply and the conversion into v_fma_mixlo_f16, which
+// rounds once, straight to fp16 (1 ulp apart on about 2 elements in 10^4).
+__device__ __forceinline__ _Float16 rms_apply(_Float16 x, float rstd, _Float16 w) {
+    return (_Float16)__builtin_canonicalizef(((float)x * rstd) * (float)w);
+}
+
 }  // namespace mcq4

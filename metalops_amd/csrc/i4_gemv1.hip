@@ -77,6 +77,8 @@ struct I4Gemv1Args {
     float *part;          // [tiles][S][M][128] when S > 1
     uint32_t *counters;   // [tiles]
     uint32_t foreign;     // splits treated as run on another XCD (test switch)
+    const _Float16 *wn;   // NORM: RMSNorm weight [K] (X is the raw row)
+    float eps;            // NORM: RMSNorm epsilon
 };
 
 constexpr int I1_SZSLOT = 1024; // scale/zero bytes per group (one 16-byte-per-lane copy)
@@ -89,10 +91,21 @@ constexpr int I1_XSTEP = 1024;  // MR: a step's activations, 16 rows x 32 halves
 // MFMAs (the B operand is built once for all blocks), and the four output rows
 // 4g..4g+3 of each column are all live.  RB = 2 runs one workgroup per CU (its
 // registers fill the SIMDs).
-template <int SZ, int ACT, bool XL, int RB, int WB>
+//
+// NORM (M == 1, 4-bit weights): the row is RMS-normalised in the kernel
+// (fused_rmsnorm_linear_int4).  Each wave copies the norm weights of its range
+// beside its activations and issues its first R steps; then the workgroup sums
+// the squares of the whole row, an eighth per wave (register loads, after the
+// copies so the weight stream starts as early as without the norm), combines
+// the wave totals through LDS at one barrier (which also waits for every copy
+// issued so far), and each wave normalises its activations in place before
+// its first step.
+template <int SZ, int ACT, bool XL, int RB, int WB, bool NORM = false>
 __global__ void __launch_bounds__(I1_W * 64, RB == 2 ? 1 : 2)
 i4_gemv1_kernel(I4Gemv1Args a) {
     static_assert(WB == 4 || (WB == 8 && RB < 2), "int8 form covers M <= 16");
+    static_assert(!NORM || (RB == 0 && WB == 4 && ACT == ACT_NONE), "the fused norm is the M == 1 INT4 form");
+    static_assert(!NORM || I1_W == RMS_WAVES, "the norm's sum order is per RMS_WAVES-wave workgroup");
     constexpr bool MR = RB > 0;
     constexpr int NB = MR ? RB : 1;              // row blocks
     constexpr int NR = MR ? 4 : 1;               // output rows per lane and block
@@ -118,11 +131,12 @@ i4_gemv1_kernel(I4Gemv1Args a) {
     const int s_begin = (sp * I1_W + wave) * a.spw;
     const int ns = max(0, min(a.spw, a.nsteps - s_begin));
 
-    // [ring R x STEPB][x 1 KiB, M == 1 only][s/z slots]
+    // [ring R x STEPB][x 1 KiB, M == 1 only][norm weights 1 KiB, NORM only][s/z slots]
     uint8_t *const wl = smem + wave * a.wave_bytes;
     uint8_t *const ring = wl;
     uint8_t *const xs = wl + I1_R * STEPB;
-    uint8_t *const szs = xs + (MR ? 0 : I1_XB);
+    uint8_t *const wns = xs + I1_XB;
+    uint8_t *const szs = xs + (MR ? 0 : I1_XB) + (NORM ? I1_XB : 0);
 
     float acc[NB][8][NR];
 #pragma unroll
@@ -132,6 +146,17 @@ i4_gemv1_kernel(I4Gemv1Args a) {
 #pragma unroll
             for (int i = 0; i < NR; ++i) acc[rb][j][i] = 0.f;
 
+    // NORM: this workgroup's share of the row's sum of squares, the wave totals
+    // through LDS behind the waves' areas, one barrier (every wave takes it once,
+    // with or without steps), then rstd in every thread.
+    auto norm_rstd = [&]() -> float {
+        float *part = (float *)(smem + I1_W * a.wave_bytes);
+        const float ss = rms_sumsq_part(a.X, a.K, tid, true);
+        if (lane == 0) part[wave] = ss;
+        __syncthreads();
+        return rms_rstd(rms_sumsq_total(part), a.K, a.eps);
+    };
+    if (NORM && ns == 0) norm_rstd();
     if (ns > 0) {
         // ---- scale/zero rows of the wave's groups, then its activations ----
         // Group of a step: a shift for the usual power-of-two group sizes (no
@@ -157,6 +182,9 @@ i4_gemv1_kernel(I4Gemv1Args a) {
             const int e = min(s_begin * 32 + 8 * lane, a.K - 8);
             __builtin_amdgcn_global_load_lds((void *)(a.X + e),
                                              (__attribute__((address_space(3))) void *)xs, 16, 0, 0);
+            if constexpr (NORM)
+                __builtin_amdgcn_global_load_lds((void *)(a.wn + e),
+                                                 (__attribute__((address_space(3))) void *)wns, 16, 0, 0);
         }
 
         // ---- weight steps ----
@@ -184,7 +212,21 @@ i4_gemv1_kernel(I4Gemv1Args a) {
             }
         };
 #pragma unroll
-        for (int k = 0; k < I1_R - 1; ++k) issue(k);
+        for (int k = 0; k < I1_R - (NORM ? 0 : 1); ++k) issue(k);
+        if constexpr (NORM) {
+            // The loads in norm_rstd are younger than every copy above, so its
+            // barrier's wait covers those too; the first R steps are in flight.
+            const float rstd = norm_rstd();
+            typedef __attribute__((address_space(3))) half8_t lds_h8;
+            lds_h8 *xp = (lds_h8 *)lds_ptr(lds_addr(xs + 16 * lane));
+            const half8_t xv = *xp;
+            const half8_t wv = *(const lds_h8 *)lds_ptr(lds_addr(wns + 16 * lane));
+            half8_t nv;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) nv[i] = rms_apply(xv[i], rstd, wv[i]);
+            *xp = nv;
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
 
         const uint32_t c64 = opaque_vgpr(0x64006400u);
         const uint32_t mlo = opaque_sgpr(0x000F000Fu), mhi = opaque_sgpr(0x00F000F0u);
@@ -247,7 +289,7 @@ i4_gemv1_kernel(I4Gemv1Args a) {
         };
 
         for (int k = 0; k < ns; ++k) {
-            issue(k + I1_R - 1);
+            if (!NORM || k > 0) issue(k + I1_R - 1);
             wait_vmcnt<(I1_R - 1) * NCOPY>();      // step k (and everything older) landed
             // x' for this step: elements 8g..8g+7 of the step (of row 16 rb + c with MR).
             half8_t xq[NB];
@@ -442,11 +484,11 @@ static I1Cfg i4_gemv1_config(int64_t K, int64_t N, int64_t gs) {
     return {(int)spw, (int)S, (int)ngr};
 }
 
-static size_t i1_wave_bytes(int64_t M, const I1Cfg &c, int wb) {
+static size_t i1_wave_bytes(int64_t M, const I1Cfg &c, int wb, bool norm = false) {
     const int rb = M > 16 ? 2 : 1;                // activation blocks per ring slot
     const size_t stepw = (size_t)I1_STEP * (wb / 4);
     return M > 1 ? (size_t)I1_R * (stepw + rb * I1_XSTEP) + c.ngr_max * I1_SZSLOT
-                 : (size_t)I1_R * stepw + I1_XB + c.ngr_max * I1_SZSLOT;
+                 : (size_t)I1_R * stepw + I1_XB * (norm ? 2 : 1) + c.ngr_max * I1_SZSLOT;
 }
 
 // LDS of a workgroup: the waves' rings and slots, and at least the epilogue's
@@ -489,22 +531,23 @@ static bool use_xcd_local(int ntiles, int S) {
     return !opt_is("MCQ4_XCD_LOCAL", '0') && S > 1 && (ntiles + 7) / 8 <= 4096;
 }
 
-template <int SZ, int ACT, bool XL, int RB, int WB>
+template <int SZ, int ACT, bool XL, int RB, int WB, bool NORM = false>
 static hipError_t launch_i1(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
-    const size_t lds = i1_lds_bytes(a.M, a.wave_bytes);
+    const size_t lds = std::max(i1_lds_bytes(a.M, a.wave_bytes),
+                                (size_t)I1_W * a.wave_bytes + (NORM ? RMS_WAVES * sizeof(float) : 0));
     static std::atomic<uint64_t> done{0};
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)i4_gemv1_kernel<SZ, ACT, XL, RB, WB>,
+        e = hipFuncSetAttribute((const void *)i4_gemv1_kernel<SZ, ACT, XL, RB, WB, NORM>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
     const int gx = XL ? (ntiles + 7) / 8 * 8 : ntiles;
-    hipLaunchKernelGGL((i4_gemv1_kernel<SZ, ACT, XL, RB, WB>), dim3(gx, a.S), dim3(I1_W * 64), lds, s, a);
+    hipLaunchKernelGGL((i4_gemv1_kernel<SZ, ACT, XL, RB, WB, NORM>), dim3(gx, a.S), dim3(I1_W * 64), lds, s, a);
     return hipGetLastError();
 }
 
@@ -533,12 +576,11 @@ static hipError_t launch_i1_wb(const I4Gemv1Args &a, int ntiles, int act, int wb
     return wb == 8 ? launch_i1_act<SZ, 8>(a, ntiles, act, s) : launch_i1_act<SZ, 4>(a, ntiles, act, s);
 }
 
-hipError_t launch_i4_gemv1(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
-                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K, int N, int gs,
-                           int act, void *ws, hipStream_t s, int wb) {
-    if (wb != 4 && (wb != 8 || M > 16)) return hipErrorInvalidValue;
+// Arguments and LDS plan shared by the plain and the normalising launches.
+static hipError_t i1_setup(I4Gemv1Args &a, const _Float16 *X, int64_t ldx, const uint8_t *P,
+                           const void *scales, const void *zeros, _Float16 *Y, int64_t ldy, int M,
+                           int K, int N, int gs, void *ws, int wb, bool norm) {
     const I1Cfg c = i4_gemv1_config(K, N, gs);
-    I4Gemv1Args a;
     a.X = X; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y;
     a.K = K; a.N = N; a.nsteps = K / 32; a.spg = gs / 32; a.spw = c.spw; a.S = c.S;
     a.spg_log2 = -1;
@@ -546,18 +588,59 @@ hipError_t launch_i4_gemv1(const _Float16 *X, int64_t ldx, const uint8_t *P, con
         if ((1 << b) == a.spg) a.spg_log2 = b;
     a.ngr_max = c.ngr_max;
     a.M = M; a.ldx = ldx; a.ldy = ldy;
-    a.wave_bytes = (int)i1_wave_bytes(M, c, wb);
+    a.wave_bytes = (int)i1_wave_bytes(M, c, wb, norm);
     a.part = nullptr; a.counters = nullptr; a.foreign = split_foreign_mask();
+    a.wn = nullptr; a.eps = 0.f;
     if (c.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.counters = (uint32_t *)ws;
         a.part = (float *)((char *)ws + COUNTER_BYTES);
     }
     if (i1_lds_bytes(M, a.wave_bytes) > 160 * 1024) return hipErrorInvalidValue;
+    return hipSuccess;
+}
+
+hipError_t launch_i4_gemv1(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
+                           const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K, int N, int gs,
+                           int act, void *ws, hipStream_t s, int wb) {
+    if (wb != 4 && (wb != 8 || M > 16)) return hipErrorInvalidValue;
+    I4Gemv1Args a;
+    if (hipError_t e = i1_setup(a, X, ldx, P, scales, zeros, Y, ldy, M, K, N, gs, ws, wb, false)) return e;
     const int ntiles = N / I1_TC;
     if (sz_dt == DT_F32) return launch_i1_wb<DT_F32>(a, ntiles, act, wb, s);
     if (sz_dt == DT_F16) return launch_i1_wb<DT_F16>(a, ntiles, act, wb, s);
     return launch_i1_wb<DT_BF16>(a, ntiles, act, wb, s);
+}
+
+// fused_rmsnorm_linear_int4 at M == 1 in one launch: the shapes i4_gemv1 takes,
+// a 16-byte aligned norm weight; MCQ4_I4_RMS_FUSE=0 keeps the two-kernel path.
+bool i4_gemv1_rms_supported(int64_t K, int64_t N, int64_t gs, const void *X, const void *wn,
+                            const void *P, const void *scales, const void *zeros) {
+    if (opt_is("MCQ4_I4_RMS_FUSE", '0') || ((uintptr_t)wn % 16)) return false;
+    if (!i4_gemv1_supported(1, K, N, gs, X, K, P, scales, zeros, 4)) return false;
+    const I1Cfg c = i4_gemv1_config(K, N, gs);
+    const size_t wave_bytes = i1_wave_bytes(1, c, 4, true);
+    return std::max(i1_lds_bytes(1, wave_bytes), (size_t)I1_W * wave_bytes + RMS_WAVES * sizeof(float)) <=
+           160 * 1024;
+}
+
+template <int SZ>
+static hipError_t launch_i1_rms(const I4Gemv1Args &a, int ntiles, hipStream_t s) {
+    return use_xcd_local(ntiles, a.S) ? launch_i1<SZ, ACT_NONE, true, 0, 4, true>(a, ntiles, s)
+                                      : launch_i1<SZ, ACT_NONE, false, 0, 4, true>(a, ntiles, s);
+}
+
+hipError_t launch_i4_gemv1_rms(const _Float16 *X, const _Float16 *wn, float eps, const uint8_t *P,
+                               const void *scales, const void *zeros, int sz_dt, _Float16 *Y, int K,
+                               int N, int gs, void *ws, hipStream_t s) {
+    I4Gemv1Args a;
+    if (hipError_t e = i1_setup(a, X, K, P, scales, zeros, Y, N, 1, K, N, gs, ws, 4, true)) return e;
+    a.wn = wn;
+    a.eps = eps;
+    const int ntiles = N / I1_TC;
+    if (sz_dt == DT_F32) return launch_i1_rms<DT_F32>(a, ntiles, s);
+    if (sz_dt == DT_F16) return launch_i1_rms<DT_F16>(a, ntiles, s);
+    return launch_i1_rms<DT_BF16>(a, ntiles, s);
 }
 
 }  // namespace mcq4

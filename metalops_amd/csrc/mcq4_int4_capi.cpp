@@ -46,6 +46,11 @@ hipError_t launch_i4_gemm(const _Float16 *X, int64_t ldx, const uint8_t *P, cons
                           int N, int gs, int act, void *ws, hipStream_t s, int wb);
 hipError_t launch_i4_rmsnorm(const _Float16 *X, int64_t ldx, const _Float16 *w, float eps, int M,
                              int K, _Float16 *out, int64_t ldo, hipStream_t s);
+bool i4_gemv1_rms_supported(int64_t K, int64_t N, int64_t gs, const void *X, const void *wn,
+                            const void *P, const void *scales, const void *zeros);
+hipError_t launch_i4_gemv1_rms(const _Float16 *X, const _Float16 *wn, float eps, const uint8_t *P,
+                               const void *scales, const void *zeros, int sz_dt, _Float16 *Y, int K,
+                               int N, int gs, void *ws, hipStream_t s);
 // Records the message returned by mcq4_last_error (mcq4_capi.cpp); returns code.
 int set_error(int code, const char *msg);
 }  // namespace mcq4
@@ -291,6 +296,20 @@ int mcq4_fused_rmsnorm_linear_int4(const void *X, int64_t ldx, const void *w_nor
         return fail(MCQ4_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
                     workspace ? workspace_bytes : (size_t)0);
     if (!aligned(workspace, 256)) return fail(MCQ4_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
+    // One row on the async-copy GEMV: the kernel normalises its own activations.
+    if (M == 1 && mcq4::i4_gemv1_rms_supported(K, N, group_size, X, w_norm, packed, scales, zeros)) {
+        if (!valid_dt(sz_dtype))
+            return fail(MCQ4_ERR_INVALID_ARG, "sz_dtype must be MCQ4_DTYPE_F32, F16 or BF16");
+        if (ldy < N) return fail(MCQ4_ERR_SHAPE, "ldy (%lld) < N (%lld)", (long long)ldy, (long long)N);
+        if (!aligned(Y, 2)) return fail(MCQ4_ERR_ALIGNMENT, "X and Y must be aligned to their element size");
+        if (!aligned(scales, dt_size(sz_dtype)) || !aligned(zeros, dt_size(sz_dtype)))
+            return fail(MCQ4_ERR_ALIGNMENT, "scales and zeros must be aligned to their element size");
+        return hip_status(mcq4::launch_i4_gemv1_rms((const _Float16 *)X, (const _Float16 *)w_norm, eps,
+                                                     packed, scales, zeros, sz_dtype, (_Float16 *)Y,
+                                                     (int)K, (int)N, (int)group_size, workspace,
+                                                     (hipStream_t)stream),
+                          "fused rmsnorm + int4 launch");
+    }
     _Float16 *xn = (_Float16 *)((char *)workspace + norm_offset(M, K, N, group_size));
     if (int st = hip_status(mcq4::launch_i4_rmsnorm((const _Float16 *)X, ldx,
                                                     (const _Float16 *)w_norm, eps, (int)M, (int)K,

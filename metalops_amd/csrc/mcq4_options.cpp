@@ -26,6 +26,7 @@ const char *const kNames[] = {
     "MCQ4_SPLIT_FOREIGN",   // mask: split-K splits treated as run on another XCD (recompute path)
     // per-group INT4 / INT8 path
     "MCQ4_I4_PATH",         // generic: the general kernel for everything
+    "MCQ4_I4_RMS_FUSE",     // 0: fused RMSNorm + INT4 at M = 1 runs as two kernels
     "MCQ4_I4_GEMV1",        // 0 | 1 | 4: async-copy decode GEMV routing
     "MCQ4_I4_SPW1",         // steps per wave of the async-copy decode GEMV
     "MCQ4_I4_GEMM6",        // 0: the barrier-free prefill kernel

@@ -374,6 +374,38 @@ def test_fused_rmsnorm_linear_int4(mo, dev, M, K, N, gs, sz):
     _check_rows(mo.matmul_int4(X2, packed, s, z, gs).float().cpu().numpy(), _ref(X2, packed, s, z, gs))
 
 
+@pytest.mark.parametrize("K,N,gs,sz", [(4096, 4096, 128, R.F16), (11008, 4096, 128, R.BF16),
+                                       (4096, 1408, 64, R.F32), (512, 256, 32, R.F16),
+                                       (1024, 12288, 128, R.F16)])
+def test_fused_rmsnorm_one_launch_matches_two(mo, dev, monkeypatch, K, N, gs, sz):
+    """M = 1 normalises inside the GEMV; its bits equal the two-kernel path's
+    (norm kernel, then matmul) on the same inputs, with the XCD-local and the
+    agent-scope split exchange, and it stays within tolerance of the oracle."""
+    print(f"fused rmsnorm one launch K={K} N={N} gs={gs} sz={sz}", flush=True)
+    for k in ("MCQ4_I4_RMS_FUSE", "MCQ4_XCD_LOCAL", "MCQ4_I4_GEMV1", "MCQ4_I4_SPW1"):
+        monkeypatch.delenv(k, raising=False)
+    w, packed, s, z = _quant(mo, dev, K, N, gs, sz, seed=K + N)
+    g = torch.Generator().manual_seed(K + gs)
+    X = (torch.randn(1, K, generator=g) * 3).half()
+    wn = (1 + 0.1 * torch.randn(K, generator=g)).half()
+    Xd, wnd = X.to(dev), wn.to(dev)
+    Y1 = mo.fused_rmsnorm_linear_int4(Xd, wnd, packed, s, z, 1e-5, gs)
+    monkeypatch.setenv("MCQ4_I4_RMS_FUSE", "0")
+    Y2 = mo.fused_rmsnorm_linear_int4(Xd, wnd, packed, s, z, 1e-5, gs)
+    assert torch.equal(Y1.view(torch.int16), Y2.view(torch.int16))
+    monkeypatch.delenv("MCQ4_I4_RMS_FUSE")
+    monkeypatch.setenv("MCQ4_XCD_LOCAL", "0")
+    Y3 = mo.fused_rmsnorm_linear_int4(Xd, wnd, packed, s, z, 1e-5, gs)
+    assert torch.equal(Y1.view(torch.int16), Y3.view(torch.int16))
+    monkeypatch.delenv("MCQ4_XCD_LOCAL")
+    xn = R.rmsnorm_f16(X.numpy(), wn.numpy(), 1e-5)
+    Yref = R.matmul_f32(xn.astype(np.float32), packed.cpu().numpy(), s.float().cpu().numpy(),
+                        z.float().cpu().numpy(), gs)
+    _check_rows(Y1.float().cpu().numpy(), Yref)
+    assert torch.equal(mo.fused_rmsnorm_linear_int4(Xd, wnd, packed, s, z, 1e-5, gs).view(torch.int16),
+                       Y1.view(torch.int16))
+
+
 def test_fused_rmsnorm_requires_half(mo, dev):
     w, packed, s, z = _quant(mo, dev, 64, 16, 32)
     with pytest.raises(RuntimeError, match="half precision"):
