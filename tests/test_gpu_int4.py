@@ -406,6 +406,31 @@ def test_fused_rmsnorm_one_launch_matches_two(mo, dev, monkeypatch, K, N, gs, sz
                        Y1.view(torch.int16))
 
 
+@pytest.mark.parametrize("M,K,N,gs", [(1, 4096, 1024, 128), (1, 250, 96, 50), (5, 250, 96, 50),
+                                      (2, 11008, 512, 128)])
+def test_fused_rmsnorm_unaligned_row(mo, dev, M, K, N, gs):
+    """A row that is not 16-byte aligned takes the two-kernel path with scalar
+    loads (and K % 8 != 0 a tail): the same sum order, so the same bits as the
+    aligned call, and within tolerance of the oracle."""
+    print(f"fused rmsnorm unaligned M={M} K={K} N={N} gs={gs}", flush=True)
+    w, packed, s, z = _quant(mo, dev, K, N, gs, R.F16, seed=K + 7)
+    g = torch.Generator().manual_seed(K + M)
+    X = (torch.randn(M, K, generator=g) * 2).half()
+    wn = (1 + 0.1 * torch.randn(K, generator=g)).half()
+    Xa = X.to(dev)
+    big = torch.zeros(M, K + 8, dtype=torch.float16, device=dev)
+    big[:, 1:K + 1] = Xa
+    Xu = big[:, 1:K + 1]
+    assert Xu.data_ptr() % 16 != 0
+    Ya = mo.fused_rmsnorm_linear_int4(Xa, wn.to(dev), packed, s, z, 1e-6, gs)
+    Yu = mo.fused_rmsnorm_linear_int4(Xu, wn.to(dev), packed, s, z, 1e-6, gs)
+    assert torch.equal(Ya.view(torch.int16), Yu.view(torch.int16))
+    xn = R.rmsnorm_f16(X.numpy(), wn.numpy(), 1e-6)
+    Yref = R.matmul_f32(xn.astype(np.float32), packed.cpu().numpy(), s.float().cpu().numpy(),
+                        z.float().cpu().numpy(), gs)
+    _check_rows(Ya.float().cpu().numpy(), Yref)
+
+
 def test_fused_rmsnorm_requires_half(mo, dev):
     w, packed, s, z = _quant(mo, dev, 64, 16, 32)
     with pytest.raises(RuntimeError, match="half precision"):
