@@ -71,7 +71,6 @@ q4_gemm7_kernel(Gemm7Args a) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    const int ntiles = a.tiles_m * a.tiles_n;
     const int bid = blockIdx.x, gx = gridDim.x;
     int tile_id = bid;
     if (gx % 8 == 0) tile_id = (bid % 8) * (gx / 8) + bid / 8;   // consecutive tiles on one XCD
