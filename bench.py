@@ -25,7 +25,9 @@ Metric: q4_0 GEMV GB/s (% HBM peak) at M=1; q4_0 GEMM TFLOP/s
   (``X.float() @ dequant_f32``).
 * ``int4``: the per-group INT4 path (quantization.py:26-239) on the same decode
   layer and prefill shapes, group size 128 with fp16 scales and zeros (an fp16
-  model's weights), with its own roofline and CPU baseline.
+  model's weights), with its own roofline and CPU baseline; ``fused_rmsnorm_m1`` times
+  fused_rmsnorm_linear_int4 (MM:3017-3103) per call on the layer's normalised
+  projections (qkv, gate, up) beside plain matmul_int4 on the same weights.
 
 Inputs are synthetic: seeded N(0, 0.02) fp32 weights quantized on the GPU with
 the llama.cpp q4_0 rule, N(0, 1) fp16 activations.
@@ -407,6 +409,42 @@ def i4_decode_bench(mo, torch, dev, args):
             "launches_step": len(DECODE_LAYER), "copies": R}
 
 
+I4_NORMED = ("qkv", "gate", "up")   # the projections that follow an RMSNorm in a Llama layer
+
+
+def i4_rmsnorm_bench(mo, torch, dev, args):
+    """fused_rmsnorm_linear_int4 at M=1 on the decode layer's normalised projections
+    (qkv after input_layernorm, gate and up after post_attention_layernorm), against
+    plain matmul_int4 on the same weights: one graph of R rotated weight copies each."""
+    R = max(1, args.copies)
+    shapes = [(K, N) for name, K, N in DECODE_LAYER if name in I4_NORMED]
+    layers = [[make_i4_weights(mo, torch, K, N, 9000 + 1000 * r + i, dev) for i, (K, N) in enumerate(shapes)]
+              for r in range(R)]
+    g = torch.Generator(device=dev).manual_seed(4)
+    x = torch.randn(1, 4096, generator=g, device=dev).half()
+    wn = (1 + 0.1 * torch.randn(4096, generator=g, device=dev)).half()
+    stream = torch.cuda.Stream(dev)
+    out = {}
+    for name, fn in (("fused", lambda w: mo.fused_rmsnorm_linear_int4(x, wn, *w, 1e-5, I4_GROUP)),
+                     ("plain", lambda w: mo.matmul_int4(x, *w, I4_GROUP))):
+        with torch.cuda.stream(stream):
+            for w in layers[0]:
+                fn(w)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for r in range(R):
+                for w in layers[r]:
+                    fn(w)
+        reps = max(1, args.steps // R)
+        secs, _ = time_region(torch, stream, lambda i: graph.replay(), reps, max(1, args.warmup // R))
+        out[name] = secs / (reps * R * len(shapes))
+        del graph
+    del layers
+    torch.cuda.empty_cache()
+    return out
+
+
 def i4_prefill_bench(mo, torch, dev, iters=30, warmup=10):
     out = []
     stream = torch.cuda.Stream(dev)
@@ -568,6 +606,7 @@ def main():
     i4_t = i4_dec["seconds"] / i4_dec["steps"]
     i4_gbs = i4_dec["bytes_step"] / i4_t / 1e9
     i4_pre = i4_prefill_bench(mo, torch, dev)
+    i4_rms = i4_rmsnorm_bench(mo, torch, dev, args)
 
     cpu = i4_cpu = pre_cpu = None
     if not args.no_cpu:
@@ -663,6 +702,11 @@ def main():
                 "algorithmic_bytes_per_launch": i4_dec["bytes_step"] // i4_dec["launches_step"],
                 "kernel": "i4_gemv1_kernel (decode GEMV, M=1)",
                 "avg_launch_us": round(i4_t / i4_dec["launches_step"] * 1e6, 3),
+            },
+            "fused_rmsnorm_m1": {
+                "projections": list(I4_NORMED),
+                "us_per_call": round(i4_rms["fused"] * 1e6, 3),
+                "plain_matmul_us_per_call": round(i4_rms["plain"] * 1e6, 3),
             },
             "prefill": {
                 "configs": [{k: (round(v, 3) if isinstance(v, float) else v) for k, v in p.items()}
