@@ -277,9 +277,12 @@ size_t mcq4_fused_rmsnorm_linear_int4_workspace_bytes(int64_t M, int64_t K, int6
  * fused_rmsnorm_linear_int4 (native/core_mps.mm:3017-3103): Y = matmul_int4(
  * rmsnorm(X, w_norm, eps), packed, scales, zeros) with X [M][ldx] fp16, w_norm
  * [K] fp16, Y [M][ldy] fp16.  RMSNorm as native/training_kernels.metal:425-488:
- * rstd = 1/sqrt(sum(x^2)/K + eps) in fp32, X_norm = fp16(x * rstd * w_norm),
+ * rstd = 1/sqrt(sum(x^2)/K + eps) in fp32, X_norm = fp16(x * rstd * w_norm).
+ * M == 1 with X and w_norm 16-byte aligned, on the shapes the async-copy INT4
+ * GEMV takes: one launch that normalises inside the GEMV.  Otherwise X_norm is
  * written to the workspace behind the matmul's share (workspace 256-byte
- * aligned), then the INT4 matmul on the same stream.
+ * aligned), then the INT4 matmul runs on the same stream.  Both forms give the
+ * same bits.
  */
 int mcq4_fused_rmsnorm_linear_int4(const void *X, int64_t ldx, const void *w_norm, float eps,
                                    const uint8_t *packed, const void *scales, const void *zeros,
