@@ -69,3 +69,16 @@ def test_q4_0_grouped_graph_replay(mo, dev):
     refs = [y.float().cpu().numpy() for y in mo.matmul_ggml_q4_0_grouped(X, blocks)]
     ref = np.concatenate(refs, axis=1)
     _replay_check(dev, lambda: torch.cat(mo.matmul_ggml_q4_0_grouped(X, blocks), dim=1), ref)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (1, 11008, 4096), (4, 4096, 1024)])
+def test_fused_rmsnorm_graph_replay(mo, dev, M, K, N):
+    """The fused RMSNorm + INT4 linear (one launch at M = 1, two kernels above),
+    captured: every replay equals the eager call."""
+    g = torch.Generator(device=dev).manual_seed(M + K)
+    W = (torch.randn(K, N, generator=g, device=dev) * 0.02).half()
+    packed, s, z = mo.quantize_int4(W, 128)
+    X = (torch.randn(M, K, generator=g, device=dev) * 2).half()
+    wn = (1 + 0.1 * torch.randn(K, generator=g, device=dev)).half()
+    ref = mo.fused_rmsnorm_linear_int4(X, wn, packed, s, z, 1e-5, 128).float().cpu().numpy()
+    _replay_check(dev, lambda: mo.fused_rmsnorm_linear_int4(X, wn, packed, s, z, 1e-5, 128), ref)
