@@ -214,9 +214,12 @@ i4_gemv1_kernel(I4Gemv1Args a) {
 #pragma unroll
         for (int k = 0; k < I1_R - (NORM ? 0 : 1); ++k) issue(k);
         if constexpr (NORM) {
-            // The loads in norm_rstd are younger than every copy above, so its
-            // barrier's wait covers those too; the first R steps are in flight.
+            // The first R steps stay in flight while the row is summed; the
+            // activations and norm weights have to have landed before they are
+            // normalised (nothing left to wait for in practice: the loads in
+            // norm_rstd are younger than every copy above).
             const float rstd = norm_rstd();
+            wait_vmcnt<0>();
             typedef __attribute__((address_space(3))) half8_t lds_h8;
             lds_h8 *xp = (lds_h8 *)lds_ptr(lds_addr(xs + 16 * lane));
             const half8_t xv = *xp;
