@@ -28,17 +28,20 @@
 //   * Activations: lane (c = l%16, g = l/16) reads elements 8g..8g+7 of each of
 //     the batch's B K blocks from the wave's LDS copy (all 16 lanes of a group
 //     read the same 16 bytes) and rearranges them to
-//     x' = [x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16] (4 v_perm, 2 v_pk_mul).
+//     x' = [x0, x4, x1, x5, x2, x6, x3, x7] (4 v_perm).
 //   * Weights: for each 16-column group of the tile, lane (c, g) reads the qs
-//     dword w of elements 8g..8g+7 of column c of the group.  Four v_and_or_b32 build the fp16 operand
-//     [1024+q0, 1024+q4, 1024+16q1, 1024+16q5, 1024+q2, 1024+q6, 1024+16q3,
-//     1024+16q7] (low nibbles as is, high nibbles in place = times 16, which x'
-//     divides out).  Against the constant operand C = [1032, 1032, 1152, 1152,
-//     1032, 1032, 1152, 1152] the same x' gives S = 1024 sum(x') + 8 sum(x), so
-//     one MFMA per K block and batch, mfma(x', -C), yields -S; it is the
-//     accumulator input of the per-item MFMA:
+//     dword w of elements 8g..8g+7 of column c of the group.  Four v_and_or_b32
+//     build the fp16 operand [1024+q0, 1024+q4, 64+q1, 64+q5, 1024+q2, 1024+q6,
+//     64+q3, 64+q7]: a low nibble under the exponent of 1024 is 1024 + q, a high
+//     nibble left in place (bits 4..7 of the half) under the exponent of 64 is
+//     64 * (1 + 16q/1024) = 64 + q.  Against the constant operand
+//     C = [1032, 1032, 72, 72, 1032, 1032, 72, 72] the same x' gives the block
+//     sum S, so one MFMA per K block and batch, mfma(x', -C), yields -S; it is
+//     the accumulator input of the per-row MFMA:
 //     mfma(x', B, -S)[0] = sum x*(q - 8), exact products, fp32 sums.
-//   * acc_tile += d * that, in fp32.
+//   * Per item, the LDS reads of all eight rows (K block x 16-column group) are
+//     issued first, then the unpacks and MFMAs, then acc += d * that in fp32, so
+//     the wave that finishes last is not serialised on LDS and MFMA latency.
 //   * Epilogue: partials of the waves per column summed through LDS in wave
 //     order (deterministic), stored as fp16.
 #include <algorithm>
@@ -84,7 +87,7 @@ __device__ __forceinline__ void gv_wait(int pending) {
     wait_vmcnt<0>();
 }
 
-template <int R, int TPW, int NW, int TW>
+template <int R, int TPW, int NW, int TW, bool GROUP>
 __global__ void __launch_bounds__(NW * 64)
 q4_gemv_dma_kernel(GemvArgs a) {
     static_assert(R >= 1 && R <= 3 && TPW >= 1 && TPW <= GV_TPW_MAX, "config");
@@ -92,46 +95,58 @@ q4_gemv_dma_kernel(GemvArgs a) {
     constexpr int B = GV_ITEM / ROWB;        // K blocks per item
     constexpr int CPR = ROWB / 16;           // 16-byte chunks per strip row
     constexpr int NG = TW / 16;              // 16-column MFMA groups per tile
-    static_assert(B * ROWB == GV_ITEM && NG * 16 == TW, "tile width");
+    // 16-column tiles keep the wave partials in an LDS area of their own (one
+    // barrier in the epilogue); 64-column tiles put them in the ring slots once
+    // every wave is done (a second barrier) to stay at three workgroups per CU.
+    constexpr bool SEPRED = TW == 16;
+    static_assert(B * ROWB == GV_ITEM && NG * 16 == TW && B * NG == 8, "tile width");
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    // Every kernel argument the prologue needs, loaded in one scalar round trip
+    // (the uses below sit behind branches, which would otherwise split the loads).
+    const int G = (int)gridDim.x, ntiles = a.ntiles, tpwt = a.tiles_per_w, nb = a.nb, nbt = a.nbt, xw = a.xw;
+    const uint32_t grow = (uint32_t)a.N * BLOCK_BYTES;
+    const _Float16 *X = a.X;
+    const uint8_t *W0 = a.W[0];
+    _Float16 *Y0 = a.Y[0];
+    asm volatile("" ::"s"(ntiles), "s"(tpwt), "s"(nb), "s"(nbt), "s"(xw), "s"(grow), "s"(X), "s"(W0), "s"(Y0));
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 15, g = lane >> 4;
-    const uint32_t grow = (uint32_t)a.N * BLOCK_BYTES;
 
-    // LDS: [NW waves x activations][NW waves x R slots]; the partials (TPW x NW
-    // waves x TW floats) reuse the slots once every wave is done with them, which
-    // keeps a 64-column 8-wave workgroup at 46 KiB (three per CU).
-    uint8_t *xs = smem + wave * a.xw;
-    uint8_t *ring = smem + NW * a.xw + wave * (R * GV_SLOT);
-    float *red = (float *)(smem + NW * a.xw);
+    // LDS: [NW waves x activations][NW waves x R slots][partials when SEPRED]
+    uint8_t *xs = smem + wave * xw;
+    uint8_t *ring = smem + NW * xw + wave * (R * GV_SLOT);
+    float *red = (float *)(smem + NW * xw + (SEPRED ? NW * R * GV_SLOT : 0));
 
-    const int G = (int)gridDim.x, G8 = G & ~7;
+    const int G8 = G & ~7;
     int wg = (int)blockIdx.x;
-    if (wg < G8) wg = (wg & 7) * (G8 >> 3) + (wg >> 3);
+    {
+        const int r = (wg & 7) * (G8 >> 3) + (wg >> 3);
+        wg = wg < G8 ? r : wg;
+    }
     // Tile j of this workgroup: wg + j*G.  Everything up to the first copy is
     // on every launch's critical path, so no integer divisions here: the tile
     // count by compares, the weight of a tile by subtracting tiles_per_w.
     int ntl = 0;                                                  // >= 1 (grid <= ntiles)
 #pragma unroll
-    for (int j = 0; j < TPW; ++j) ntl += wg + j * G < a.ntiles ? 1 : 0;
-    auto tile = [&](int j) { return wg + j * G; };
-    // Weight and output bases of tile j (the weight index is uniform: scalar selects).
+    for (int j = 0; j < TPW; ++j) ntl += wg + j * G < ntiles ? 1 : 0;
     const uint8_t *wt[TPW];
     _Float16 *yt[TPW];
 #pragma unroll
     for (int j = 0; j < TPW; ++j) {
-        int lt = j < ntl ? tile(j) : 0, gi = 0;
+        int lt = j < ntl ? wg + j * G : 0, gi = 0;
+        if (GROUP) {
 #pragma unroll
-        for (int r = 1; r < GV_GROUP_MAX; ++r)
-            if (lt >= a.tiles_per_w) { lt -= a.tiles_per_w; gi = r; }
-        const uint8_t *w = gi == 0 ? a.W[0] : gi == 1 ? a.W[1] : gi == 2 ? a.W[2] : a.W[3];
-        _Float16 *y = gi == 0 ? a.Y[0] : gi == 1 ? a.Y[1] : gi == 2 ? a.Y[2] : a.Y[3];
+            for (int r = 1; r < GV_GROUP_MAX; ++r)
+                if (lt >= tpwt) { lt -= tpwt; gi = r; }
+        }
+        const uint8_t *w = !GROUP || gi == 0 ? W0 : gi == 1 ? a.W[1] : gi == 2 ? a.W[2] : a.W[3];
+        _Float16 *y = !GROUP || gi == 0 ? Y0 : gi == 1 ? a.Y[1] : gi == 2 ? a.Y[2] : a.Y[3];
         wt[j] = w + (int64_t)lt * ROWB;
         yt[j] = y + lt * TW;
     }
-    const int nbm = a.nbt > wave ? (a.nbt - wave + NW - 1) / NW : 0;  // my batches
+    const int nbm = nbt > wave ? (nbt - wave + NW - 1) / NW : 0;  // my batches
     const int nmine = nbm * ntl;
 
     // Copy geometry per lane and copy i: strip chunk q = lane + 64 i of an item
@@ -147,7 +162,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
     // Item (batch index m of this wave, tile j) into ring slot `slot`.
     auto issue = [&](int m, int j, int slot) {
         const int row0 = (wave + NW * m) * B;
-        const int rows = min(B, a.nb - row0);
+        const int rows = min(B, nb - row0);
         const uint8_t *wb = wt[j] + (int64_t)row0 * grow;
 #pragma unroll
         for (int i = 0; i < GV_LOADS; ++i) {
@@ -172,10 +187,10 @@ q4_gemv_dma_kernel(GemvArgs a) {
     // row lane/4, piece lane%4; rows past K clamp to the last row), so they are
     // older than every weight copy and land before the first item does.
     for (int m = 0; m < nbm; ++m) {
-        const int r = min((wave + NW * m) * B + (lane >> 2), a.nb - 1);
+        const int r = min((wave + NW * m) * B + (lane >> 2), nb - 1);
         if (lane < 4 * B)
             __builtin_amdgcn_global_load_lds(
-                (void *)((const uint8_t *)a.X + (int64_t)r * (QK * 2) + 16 * (lane & 3)),
+                (void *)((const uint8_t *)X + (int64_t)r * (QK * 2) + 16 * (lane & 3)),
                 (__attribute__((address_space(3))) void *)(xs + m * (B * 64)), 16, 0, 0);
     }
     // R-1 items ahead; each iteration issues one more before it waits, into the
@@ -186,13 +201,14 @@ q4_gemv_dma_kernel(GemvArgs a) {
     const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
     const uint32_t qal = (uint32_t)(qoff & ~3), qsh = (uint32_t)(qoff & 3) * 8;
     const uint32_t doff = (uint32_t)(c * BLOCK_BYTES);
-    const uint32_t c64 = opaque_vgpr(0x64006400u);
+    // fp16 exponent words: 1024 + q for a low nibble (bits 0..3 of a half),
+    // 64 + q for a high nibble left in place (bits 4..7: 64 * (1 + 16q/1024)).
+    const uint32_t e1024 = opaque_vgpr(0x64006400u), e64 = opaque_vgpr(0x54005400u);
     const uint32_t mlo = opaque_sgpr(0x000F000Fu), mhi = opaque_sgpr(0x00F000F0u);
-    // -C as the fp16 operand: (-1032, -1032) and (-1152, -1152) pairs.
-    const uint32_t nlo = 0xE408E408u, nhi = 0xE480E480u;
+    // -C as the fp16 operand: (-1032, -1032) and (-72, -72) pairs.
+    const uint32_t nlo = 0xE408E408u, nhi = 0xD480D480u;
     const half8_t negc = bitcast<half8_t>(uint4_t{nlo, nhi, nlo, nhi});
     const float4_t z = {0.f, 0.f, 0.f, 0.f};
-    const half2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
 
     float acc[TPW][NG];
 #pragma unroll
@@ -202,7 +218,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
 
     int k = 0, slot = 0;
     for (int m = 0; m < nbm; ++m) {
-        const int rows = min(B, a.nb - (wave + NW * m) * B);
+        const int rows = min(B, nb - (wave + NW * m) * B);
         half8_t xq[B];
         float4_t negs[B];
 #pragma unroll
@@ -218,44 +234,54 @@ q4_gemv_dma_kernel(GemvArgs a) {
 #pragma unroll
                     for (int u = 0; u < B; ++u) {
                         const uint4_t x = bitcast<uint4_t>(*(const lds_half8 *)(lds_ptr(xa) + u * 64));
-                        const uint32_t h15 = __builtin_amdgcn_perm(x[2], x[0], 0x07060302u);   // x1, x5
-                        const uint32_t h37 = __builtin_amdgcn_perm(x[3], x[1], 0x07060302u);   // x3, x7
-                        const uint4_t v = {__builtin_amdgcn_perm(x[2], x[0], 0x05040100u),     // x0, x4
-                                           bitcast<uint32_t>(bitcast<half2_t>(h15) * s16),
-                                           __builtin_amdgcn_perm(x[3], x[1], 0x05040100u),     // x2, x6
-                                           bitcast<uint32_t>(bitcast<half2_t>(h37) * s16)};
+                        const uint4_t v = {__builtin_amdgcn_perm(x[2], x[0], 0x05040100u),   // x0, x4
+                                           __builtin_amdgcn_perm(x[2], x[0], 0x07060302u),   // x1, x5
+                                           __builtin_amdgcn_perm(x[3], x[1], 0x05040100u),   // x2, x6
+                                           __builtin_amdgcn_perm(x[3], x[1], 0x07060302u)};  // x3, x7
                         xq[u] = bitcast<half8_t>(v);
                         negs[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], negc, z, 0, 0, 0);
                     }
                 }
                 gv_wait<R>(min(R - 1, nmine - 1 - k));
+                // All eight (K block, column group) rows of the item: LDS reads
+                // first, then the unpack and MFMAs, then the scaled sums, so a wave
+                // that runs alone at the end of the launch is not serialised on
+                // LDS and MFMA latencies row by row.
                 const uint32_t base = lds_addr(ring + slot * GV_SLOT);
+                uint32_t q0[B][NG], q1[B][NG];
+                _Float16 dh[B][NG];
 #pragma unroll
-                for (int grp = 0; grp < NG; ++grp) {
-                    const uint32_t qa = base + grp * 288 + qal, da = base + grp * 288 + doff;
-                    auto row = [&](int u) {
-                        const lds_u32 *qp = (const lds_u32 *)(lds_ptr(qa) + u * ROWB);
-                        const uint32_t q0 = qp[0], q1 = qp[1];
-                        const uint32_t w = __builtin_amdgcn_alignbit(q1, q0, qsh);
-                        const uint32_t w8 = __builtin_amdgcn_alignbit(q1, q0, qsh + 8);
-                        const float d = (float)bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(da) + u * ROWB));
-                        const uint4_t bq = {and_or(w, mlo, c64), and_or(w, mhi, c64),
-                                            and_or(w8, mlo, c64), and_or(w8, mhi, c64)};
-                        const float4_t blk =
-                            __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], bitcast<half8_t>(bq), negs[u], 0, 0, 0);
-                        return d * blk[0];
-                    };
-                    if (rows == B) {
-                        float part[B];
+                for (int u = 0; u < B; ++u)
 #pragma unroll
-                        for (int u = 0; u < B; ++u) part[u] = row(u);
-#pragma unroll
-                        for (int u = 0; u < B; ++u) acc[j][grp] += part[u];
-                    } else {
-#pragma unroll
-                        for (int u = 0; u < B; ++u)
-                            if (u < rows) acc[j][grp] += row(u);
+                    for (int grp = 0; grp < NG; ++grp) {
+                        const lds_u32 *qp = (const lds_u32 *)(lds_ptr(base + qal) + u * ROWB + grp * 288);
+                        q0[u][grp] = qp[0];
+                        q1[u][grp] = qp[1];
+                        dh[u][grp] = bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(base + doff) + u * ROWB + grp * 288));
                     }
+                float4_t r[B][NG];
+#pragma unroll
+                for (int u = 0; u < B; ++u)
+#pragma unroll
+                    for (int grp = 0; grp < NG; ++grp) {
+                        const uint32_t w = __builtin_amdgcn_alignbit(q1[u][grp], q0[u][grp], qsh);
+                        const uint32_t w8 = __builtin_amdgcn_alignbit(q1[u][grp], q0[u][grp], qsh + 8);
+                        const uint4_t bq = {and_or(w, mlo, e1024), and_or(w, mhi, e64), and_or(w8, mlo, e1024),
+                                            and_or(w8, mhi, e64)};
+                        r[u][grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], bitcast<half8_t>(bq), negs[u],
+                                                                           0, 0, 0);
+                    }
+                if (rows == B) {
+#pragma unroll
+                    for (int u = 0; u < B; ++u)
+#pragma unroll
+                        for (int grp = 0; grp < NG; ++grp) acc[j][grp] += (float)dh[u][grp] * r[u][grp][0];
+                } else {
+#pragma unroll
+                    for (int u = 0; u < B; ++u)
+#pragma unroll
+                        for (int grp = 0; grp < NG; ++grp)
+                            if (u < rows) acc[j][grp] += (float)dh[u][grp] * r[u][grp][0];
                 }
                 // All reads of this slot are done before the next iteration refills it.
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -266,7 +292,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
     }
 
     // Partials (lanes 0..15 hold column 16 grp + lane), then the ordered wave sum.
-    __syncthreads();                              // every wave's last slot is read
+    if (!SEPRED) __syncthreads();                 // every wave's last slot is read
     if (lane < 16) {
 #pragma unroll
         for (int j = 0; j < TPW; ++j)
@@ -275,7 +301,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
                 for (int grp = 0; grp < NG; ++grp)
                     red[(j * NW + wave) * TW + grp * 16 + lane] = nbm > 0 ? acc[j][grp] : 0.f;
     }
-    __syncthreads();
+    lds_barrier();
     for (int v = tid; v < ntl * TW; v += NW * 64) {
         const int j = v / TW, col = v % TW;
         float s = 0.f;
@@ -286,11 +312,12 @@ q4_gemv_dma_kernel(GemvArgs a) {
 }
 
 static size_t gemv_lds_bytes(int R, int tpw, int xw, int nw, int tw) {
-    return (size_t)nw * xw + std::max((size_t)nw * R * GV_SLOT, (size_t)tpw * nw * tw * sizeof(float));
+    const size_t ring = (size_t)nw * R * GV_SLOT, red = (size_t)tpw * nw * tw * sizeof(float);
+    return (size_t)nw * xw + (tw == 16 ? ring + red : std::max(ring, red));
 }
 
-template <int R, int TPW, int NW, int TW>
-static hipError_t launch_gemv_t(const GemvArgs &a, int grid, hipStream_t s) {
+template <int R, int TPW, int NW, int TW, bool GROUP>
+static hipError_t launch_gemv_g(const GemvArgs &a, int grid, hipStream_t s) {
     const size_t lds = gemv_lds_bytes(R, TPW, a.xw, NW, TW);
     if (lds > 160 * 1024) return hipErrorInvalidValue;
     static std::atomic<uint64_t> done{0};
@@ -299,13 +326,20 @@ static hipError_t launch_gemv_t(const GemvArgs &a, int grid, hipStream_t s) {
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)q4_gemv_dma_kernel<R, TPW, NW, TW>,
+        e = hipFuncSetAttribute((const void *)q4_gemv_dma_kernel<R, TPW, NW, TW, GROUP>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL((q4_gemv_dma_kernel<R, TPW, NW, TW>), dim3(grid), dim3(NW * 64), lds, s, a);
+    hipLaunchKernelGGL((q4_gemv_dma_kernel<R, TPW, NW, TW, GROUP>), dim3(grid), dim3(NW * 64), lds, s, a);
     return hipGetLastError();
+}
+
+// One weight (the drop-in call) or up to GV_GROUP_MAX weights sharing X.
+template <int R, int TPW, int NW, int TW>
+static hipError_t launch_gemv_t(const GemvArgs &a, int grid, hipStream_t s) {
+    return a.ntiles > a.tiles_per_w ? launch_gemv_g<R, TPW, NW, TW, true>(a, grid, s)
+                                    : launch_gemv_g<R, TPW, NW, TW, false>(a, grid, s);
 }
 
 template <int R, int NW>
