@@ -91,9 +91,12 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     p.add_argument("--part", choices=["all", "decode", "prefill", "configs", "copy", "int4-decode",
-                                      "int4-prefill"], default="all",
+                                      "int4-prefill", "probes"], default="all",
                    help="run one part only (for profiler passes); 'copy' runs a plain 256 MiB "
-                        "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters")
+                        "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters; "
+                        "'probes' runs the machine probes of libmcq4_bench.so (launch floor, "
+                        "read patterns of the q4_0 layout, atomic and store-to-load latency, "
+                        "shader clock)")
     return p.parse_args()
 
 
@@ -199,18 +202,48 @@ def config_points(mo, torch, dev):
     return out
 
 
+_BENCH_LIB = None
+
+
+def bench_lib():
+    """libmcq4_bench.so: the measurement probes (metalops_amd/csrc/bench/mcq4_bench.h),
+    built beside libmcq4.so and kept out of the drop-in library."""
+    global _BENCH_LIB
+    if _BENCH_LIB is None:
+        import ctypes
+        path = os.path.join(ROOT, "metalops_amd", "_lib", "libmcq4_bench.so")
+        if not os.path.exists(path):
+            raise ImportError(f"{path} is not built; run __graft_entry__.build()")
+        lib = ctypes.CDLL(path)
+        p, i, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
+        sigs = {"mcqb_read_probe": [p, sz, p, p], "mcqb_read_tiles": [p, i64, i64, i, i, i, p, p],
+                "mcqb_empty": [i, i, p], "mcqb_measure_sclk": [p, i, p],
+                "mcqb_atomic_chain": [p, i, i, p, p], "mcqb_exchange": [p, p, i, i, i, i, p]}
+        for name, args in sigs.items():
+            fn = getattr(lib, name)
+            fn.restype = i
+            fn.argtypes = args
+        _BENCH_LIB = lib
+    return _BENCH_LIB
+
+
+def bench_check(status, name):
+    if status != 0:
+        raise RuntimeError(f"{name} failed with status {status}")
+
+
 def read_ceiling(torch, stream, weights, reps):
-    """Seconds per pass of plain reads (mcq4_read_probe, one launch per weight) over
+    """Seconds per pass of plain reads (mcqb_read_probe, one launch per weight) over
     `weights` in order, captured in one HIP graph -- the HBM read rate the same
     bytes reach with launches of the same sizes and nothing else to do."""
-    from metalops_amd import _lib
+    lib = bench_lib()
     sink = torch.zeros(4, dtype=torch.int32, device=weights[0].device)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         cs = torch.cuda.current_stream().cuda_stream
         for w in weights:
-            _lib.check(_lib.lib.mcq4_read_probe(w.data_ptr(), w.numel() * w.element_size(),
-                                                sink.data_ptr(), cs), "mcq4_read_probe")
+            bench_check(lib.mcqb_read_probe(w.data_ptr(), w.numel() * w.element_size(), sink.data_ptr(), cs),
+                        "mcqb_read_probe")
     secs, _ = time_region(torch, stream, lambda i: graph.replay(), reps, 3)
     del graph
     return secs / reps
@@ -246,6 +279,7 @@ def decode_bench(mo, torch, dev, args):
         secs, wall = time_region(torch, stream, fn, calls, args.warmup, stats=st)
         steps = calls
         median_step_s = st["median_call_s"]
+        replays, check_s = 0, None
     else:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
@@ -269,6 +303,14 @@ def decode_bench(mo, torch, dev, args):
         secs, wall = time_region(torch, stream, fn, full + rem, max(1, args.warmup // R), stats=st)
         steps = args.steps
         median_step_s = st["median_call_s"] / R if full else secs / steps
+        replays = full + rem
+        # A short timed region (the driver's --steps 20 is two replays) is checked
+        # against one of at least 50 ms of replays, reported beside it.
+        check_s = None
+        if secs < 0.05:
+            n = max(1, int(0.05 / (secs / max(1, full + rem) * (R if not full else 1))) + 1)
+            csecs, _ = time_region(torch, stream, lambda i: graph.replay(), n, 3)
+            check_s = csecs / (n * R)
     bytes_step = sum(wbytes(K, N) for _, K, N in DECODE_LAYER)
     xy_step = sum(2 * K + 2 * N for _, K, N in DECODE_LAYER)
     read_s = read_ceiling(torch, stream, [w for layer in layers for w in layer], 20) / R
@@ -292,6 +334,7 @@ def decode_bench(mo, torch, dev, args):
     del ggraph
     return {
         "read_ceiling_s": read_s,
+        "graph_replays": replays, "check_step_s": check_s,
         "grouped_step_s": gsecs / (reps * R),
         "seconds": secs, "steps": steps, "wall": wall, "median_step_s": median_step_s,
         "bytes_step": bytes_step, "xy_step": xy_step,
@@ -539,6 +582,119 @@ def cpu_baseline(seconds_budget):
     }
 
 
+def probes(torch, dev):
+    """Machine probes (libmcq4_bench.so) that the decode figures are read against:
+    the per-launch floor of a graph, the HBM read rate of the q4_0 layout's access
+    patterns at the decode layer's sizes, the round trip of a returning atomic, the
+    store-to-load visibility between workgroups, and the shader clock under MFMA load."""
+    lib = bench_lib()
+    stream = torch.cuda.Stream(dev)
+    out = {"part": "probes"}
+
+    def graph_time(launch, n, reps=20):
+        with torch.cuda.stream(stream):
+            launch(0)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(n):
+                launch(i)
+        secs, _ = time_region(torch, stream, lambda i: graph.replay(), reps, 3)
+        del graph
+        return secs / (reps * n)
+
+    # 1. Per-launch floor: back-to-back empty kernels in one graph.
+    floor = {}
+    for grid, block in ((1, 64), (256, 256), (256, 1024)):
+        t = graph_time(lambda i: bench_check(lib.mcqb_empty(grid, block, torch.cuda.current_stream().cuda_stream),
+                                             "mcqb_empty"), 50)
+        floor[f"{grid}x{block}"] = round(t * 1e6, 3)
+    out["empty_kernel_us_per_launch"] = floor
+
+    # 2. Read patterns of a q4_0 weight [K/32][N][18] at the layer's shapes, over
+    #    copies rotated through >= 1.1 GB (reads from HBM): contiguous, 16-column
+    #    strips (one workgroup per strip, the M = 1 kernel's pattern) and 64-column
+    #    tiles split four ways along K.
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    pats = []
+    for _, K, N in DECODE_LAYER[:2] + DECODE_LAYER[2:3] + DECODE_LAYER[4:]:
+        nbytes = wbytes(K, N)
+        copies = max(2, -(-int(1.1e9) // nbytes))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(0, 256) for _ in range(copies)]
+        rec = {"K": K, "N": N, "bytes": nbytes}
+        cs = lambda: torch.cuda.current_stream().cuda_stream
+        kinds = {
+            "contiguous": lambda i: bench_check(lib.mcqb_read_probe(bufs[i].data_ptr(), nbytes, sink.data_ptr(), cs()),
+                                                "mcqb_read_probe"),
+            "strip16": lambda i: bench_check(lib.mcqb_read_tiles(bufs[i].data_ptr(), K, N, 16, 1, 16, sink.data_ptr(),
+                                                                 cs()), "mcqb_read_tiles"),
+            "tile64_k4": lambda i: bench_check(lib.mcqb_read_tiles(bufs[i].data_ptr(), K, N, 64, 4, 16,
+                                                                   sink.data_ptr(), cs()), "mcqb_read_tiles"),
+        }
+        for name, fn in kinds.items():
+            t = graph_time(fn, copies)
+            rec[name] = {"us": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1)}
+        pats.append(rec)
+        del bufs
+    torch.cuda.empty_cache()
+    out["read_patterns"] = pats
+
+    # 3. Returning 64-bit atomic add, a dependent chain per workgroup.
+    words = torch.zeros(256 * 64, dtype=torch.int64, device=dev)
+    ticks = torch.zeros(256, dtype=torch.int64, device=dev)
+    at = {}
+    for grid in (1, 256):
+        bench_check(lib.mcqb_atomic_chain(words.data_ptr(), 200, grid, ticks.data_ptr(), None), "mcqb_atomic_chain")
+        torch.cuda.synchronize()
+        bench_check(lib.mcqb_atomic_chain(words.data_ptr(), 200, grid, ticks.data_ptr(), None), "mcqb_atomic_chain")
+        torch.cuda.synchronize()
+        at[f"grid{grid}"] = round(float(ticks[:grid].double().mean()) * 10.0 / 200, 1)
+    out["atomic_rtt_ns"] = at
+
+    # 4. Store -> poll visibility between workgroups (pair stride 8: same XCD under
+    #    round-robin placement; stride 1: neighbouring XCDs).
+    slots = torch.zeros(4096, dtype=torch.int64, device=dev)
+    res = torch.zeros(1024, dtype=torch.int64, device=dev)
+    ex = []
+    for sm, sname in ((0, "plain"), (1, "agent_atomic"), (2, "nontemporal")):
+        for lm, lname in ((0, "sc0_buffer_load"), (1, "agent_atomic_load")):
+            for d in (8, 1):
+                slots.zero_()
+                torch.cuda.synchronize()
+                bench_check(lib.mcqb_exchange(slots.data_ptr(), res.data_ptr(), d, sm, lm, 20000, None),
+                            "mcqb_exchange")
+                torch.cuda.synchronize()
+                h = res.view(256, 4).cpu().tolist()
+                same, cross, fail_same, fail_cross = [], [], 0, 0
+                for wg in range(256):
+                    if (wg // d) % 2 == 0:
+                        continue
+                    pw = wg - d
+                    sx = h[wg][0] == h[pw][0]
+                    if not h[wg][3]:
+                        if sx:
+                            fail_same += 1
+                        else:
+                            fail_cross += 1
+                        continue
+                    (same if sx else cross).append((h[wg][2] - h[pw][1]) * 10.0)
+                rec = {"store": sname, "load": lname, "pair_stride": d}
+                for nm, v, f in (("same_xcd", same, fail_same), ("cross_xcd", cross, fail_cross)):
+                    if v or f:
+                        rec[nm] = {"pairs": len(v) + f, "never_seen": f,
+                                   "p50_ns": round(statistics.median(v), 0) if v else None}
+                ex.append(rec)
+    out["store_to_load"] = ex
+
+    # 5. Shader clock under a dense MFMA load.
+    tk = torch.zeros(4096, dtype=torch.int64, device=dev)
+    bench_check(lib.mcqb_measure_sclk(tk.data_ptr(), 20000, None), "mcqb_measure_sclk")
+    torch.cuda.synchronize()
+    t2 = tk.view(-1, 2).double()
+    out["sclk_mfma_mhz"] = round(float((100.0 * t2[:, 0] / t2[:, 1]).median()), 0)
+    return out
+
+
 def run_part(mo, torch, dev, args):
     """One part of the benchmark, printing its own JSON line (profiler passes)."""
     if args.part == "copy":
@@ -565,6 +721,8 @@ def run_part(mo, torch, dev, args):
               flush=True)
     elif args.part == "configs":
         print(json.dumps({"part": "configs", "configs": config_points(mo, torch, dev)}), flush=True)
+    elif args.part == "probes":
+        print(json.dumps(probes(torch, dev)), flush=True)
     elif args.part == "int4-prefill":
         print(json.dumps({"part": "int4-prefill", "configs": i4_prefill_bench(mo, torch, dev)}),
               flush=True)
@@ -623,6 +781,16 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(t_step * 1e3, 5),
         "median_ms_per_step": round(dec["median_step_s"] * 1e3, 5),
+        # What ms_per_step rests on: the timed region, its graph replays (each of
+        # `weight_copies_rotated` steps) and, when the region is under 50 ms, the
+        # per-step time over at least 50 ms of replays of the same graph.
+        "timing": {
+            "timed_region_ms": round(dec["seconds"] * 1e3, 4),
+            "graph_replays": dec["graph_replays"],
+            "steps_per_replay": dec["copies"],
+            "check_ms_per_step_50ms": (round(dec["check_step_s"] * 1e3, 5)
+                                       if dec["check_step_s"] is not None else None),
+        },
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -644,7 +812,7 @@ def main():
         "read_ceiling": {
             "GB/s": round(dec["bytes_step"] / dec["read_ceiling_s"] / 1e9, 1),
             "pct_hbm_peak": round(100 * dec["bytes_step"] / dec["read_ceiling_s"] / 1e9 / HBM_PEAK_GBS, 2),
-            "kernel": "read_probe_kernel (mcq4_read_probe: 16 KiB per 256-thread workgroup)",
+            "kernel": "read_probe_kernel (mcqb_read_probe: 16 KiB per 256-thread workgroup)",
             "value_over_ceiling": round(dec["read_ceiling_s"] / t_step, 4),
         },
         # The layer with gate and up in one launch (matmul_ggml_q4_0_grouped, no

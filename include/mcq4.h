@@ -290,29 +290,6 @@ int mcq4_fused_rmsnorm_linear_int4(const void *X, int64_t ldx, const void *w_nor
                                    int64_t N, int64_t group_size, void *workspace,
                                    size_t workspace_bytes, void *stream);
 
-/*
- * Measurement helper; no counterpart in the reference (it measures the shader
- * clock the power limit leaves under a dense MFMA load).  Runs 512 workgroups of 4
- * waves, each `iters` rounds of four v_mfma_f32_32x32x16_f16 chains on fresh
- * pseudo-random fp16 operands, and writes
- * per wave w the shader-clock ticks (s_memtime) and 100 MHz real-time ticks
- * (s_memrealtime) of the loop to ticks[2w] and ticks[2w+1]: ticks is a device
- * buffer of 4096 uint64 owned by the caller.  sclk = 100 MHz * ticks[2w] /
- * ticks[2w+1].
- */
-int mcq4_measure_sclk(uint64_t *ticks, int iters, void *stream);
-
-/*
- * Measurement helper; no counterpart in the reference (the benchmark uses it
- * for the read ceiling beside each decode figure: the HBM rate a plain read of
- * the same bytes, in one launch, reaches).  Reads the floor(bytes/16)*16 bytes
- * at `src` (16-byte aligned) with 256-thread workgroups of 16 KiB each
- * (non-temporal loads, the faster policy for data read once) and
- * writes *sink (a device uint32) only in the unlikely event that the XOR of a
- * workgroup's data equals 0x9E3779B9.
- */
-int mcq4_read_probe(const void *src, size_t bytes, uint32_t *sink, void *stream);
-
 #ifdef __cplusplus
 }
 #endif

@@ -56,8 +56,6 @@ SIGNATURES = {
     "mcq4_fused_rmsnorm_linear_int4_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "mcq4_fused_rmsnorm_linear_int4": (_int, [_p, _i64, _p, ctypes.c_float, _p, _p, _p, _int, _p,
                                               _i64, _i64, _i64, _i64, _i64, _p, _sz, _p]),
-    "mcq4_measure_sclk": (_int, [_p, _int, _p]),
-    "mcq4_read_probe": (_int, [_p, _sz, _p, _p]),
 }
 
 

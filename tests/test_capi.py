@@ -167,22 +167,6 @@ def test_int8_and_fused_validation_codes():
     assert f(X, 64, W, 1e-6, P, S, Z, F16, Y, 8, 4, 64, 8, 32, 0x70080, need, None) == _lib.MCQ4_ERR_ALIGNMENT  # 128-, not 256-aligned
 
 
-def test_measure_sclk_validation():
-    """Argument checks need no GPU: a null buffer or a non-positive count is rejected."""
-    assert _lib.lib.mcq4_measure_sclk(None, 10, None) == _lib.MCQ4_ERR_INVALID_ARG
-    assert _lib.lib.mcq4_measure_sclk(ctypes.c_void_p(256), 0, None) == _lib.MCQ4_ERR_INVALID_ARG
-
-
-def test_read_probe_validation():
-    """Argument checks need no GPU: null pointers, fewer than 16 bytes and a source
-    that is not 16-byte aligned are rejected."""
-    f = _lib.lib.mcq4_read_probe
-    assert f(None, 1024, ctypes.c_void_p(256), None) == _lib.MCQ4_ERR_INVALID_ARG
-    assert f(ctypes.c_void_p(256), 1024, None, None) == _lib.MCQ4_ERR_INVALID_ARG
-    assert f(ctypes.c_void_p(256), 8, ctypes.c_void_p(512), None) == _lib.MCQ4_ERR_INVALID_ARG
-    assert f(ctypes.c_void_p(264), 1024, ctypes.c_void_p(512), None) == _lib.MCQ4_ERR_INVALID_ARG
-
-
 def test_grouped_validation():
     """The grouped entry point's argument checks need no GPU: no weights, a null
     weight or output pointer, and ldy < N are rejected on either path."""
@@ -199,30 +183,3 @@ def test_grouped_validation():
         assert b"ldy" in _lib.lib.mcq4_last_error()
 
 
-@pytest.mark.gpu
-def test_read_probe_leaves_sink():
-    """The probe reads and, for data whose workgroup XOR is not the magic value, leaves
-    the sink untouched."""
-    import torch
-    src = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
-    sink = torch.full((4,), 7, dtype=torch.int32, device="cuda")
-    s = torch.cuda.current_stream()
-    _lib.check(_lib.lib.mcq4_read_probe(src.data_ptr(), src.numel() + 5, sink.data_ptr(), s.cuda_stream),
-               "mcq4_read_probe")
-    torch.cuda.synchronize()
-    assert sink.tolist() == [7, 7, 7, 7]
-
-
-@pytest.mark.gpu
-def test_measure_sclk_plausible():
-    """Every wave reports shader-clock and 100 MHz real-time ticks; the implied clock
-    lies between 300 MHz and 3 GHz (MI355X peaks at 2.4 GHz)."""
-    import torch
-    ticks = torch.zeros(4096, dtype=torch.int64, device="cuda")
-    s = torch.cuda.current_stream()
-    _lib.check(_lib.lib.mcq4_measure_sclk(ticks.data_ptr(), 2000, s.cuda_stream), "mcq4_measure_sclk")
-    torch.cuda.synchronize()
-    t = ticks.view(-1, 2).double().cpu()
-    assert (t[:, 1] > 0).all() and (t[:, 0] > 0).all()
-    mhz = 100.0 * t[:, 0] / t[:, 1]
-    assert 300.0 < float(mhz.median()) < 3000.0
