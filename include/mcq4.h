@@ -108,7 +108,8 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y,
  * arguments minus the workspace: the split-K workspace is the library's own
  * device array (one per GPU, held until the process ends) of
  * mcq4_matmul_noalloc_max_workspace_bytes() bytes (256 KiB of counters +
- * 64 MiB); a shape whose mcq4_matmul_workspace_bytes exceeds it returns
+ * 16 MiB: every decode plan, prefill split-K plans up to M = 64 at
+ * K = 14336); a shape whose mcq4_matmul_workspace_bytes exceeds it returns
  * MCQ4_ERR_WORKSPACE.  Calls allocate nothing (no hipMalloc / hipFree, no
  * allocating library routine).  Every call on a GPU shares that GPU's array:
  * calls that overlap on one GPU (two streams, two threads) race and give wrong

@@ -55,17 +55,23 @@ __device__ __forceinline__ void store_dt(void *p, int64_t i, float v, int dt) {
 // int8 [K][N]) product over K rows [k0, k1): sum of x[k] * (q - z) * s in fp32.
 // The split-K recompute path of the XCD-local exchange (q4_common.h): slow,
 // taken only when a split ran on another XCD.
-template <int WB>
+__device__ __forceinline__ _Float16 rms_apply(_Float16 x, float rstd, _Float16 w);
+
+// With NORM the row is the raw activation row of a fused RMSNorm: each element
+// is normalised as the kernel normalised it (rms_apply with the row's rstd and
+// the norm weight wn) before the product.
+template <int WB, bool NORM = false>
 __device__ __forceinline__ float i4_dot_range(const _Float16 *xrow, const uint8_t *P, const void *scales,
                                            const void *zeros, int sz_dt, int N, int gs, int n, int k0,
-                                           int k1) {
+                                           int k1, const _Float16 *wn = nullptr, float rstd = 0.f) {
     float acc = 0.f;
     for (int k = k0; k < k1; ++k) {
         float q;
         if constexpr (WB == 4) q = (float)((P[(int64_t)(k >> 1) * N + n] >> (4 * (k & 1))) & 0xF);
         else q = (float)(int8_t)P[(int64_t)k * N + n];
         const int64_t gi = (int64_t)(k / gs) * N + n;
-        acc += (float)xrow[k] * ((q - load_dt(zeros, gi, sz_dt)) * load_dt(scales, gi, sz_dt));
+        const _Float16 x = NORM ? rms_apply(xrow[k], rstd, wn[k]) : xrow[k];
+        acc += (float)x * ((q - load_dt(zeros, gi, sz_dt)) * load_dt(scales, gi, sz_dt));
     }
     return acc;
 }

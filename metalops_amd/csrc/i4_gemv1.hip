@@ -156,7 +156,10 @@ i4_gemv1_kernel(I4Gemv1Args a) {
         __syncthreads();
         return rms_rstd(rms_sumsq_total(part), a.K, a.eps);
     };
-    if (NORM && ns == 0) norm_rstd();
+    // rstd of the row, kept for the split-K recompute path (which rebuilds the
+    // normalised activations of a split that ran on another XCD).
+    float rstd_row = 0.f;
+    if (NORM && ns == 0) rstd_row = norm_rstd();
     if (ns > 0) {
         // ---- scale/zero rows of the wave's groups, then its activations ----
         // Group of a step: a shift for the usual power-of-two group sizes (no
@@ -219,6 +222,7 @@ i4_gemv1_kernel(I4Gemv1Args a) {
             // normalised (nothing left to wait for in practice: the loads in
             // norm_rstd are younger than every copy above).
             const float rstd = norm_rstd();
+            rstd_row = rstd;
             wait_vmcnt<0>();
             typedef __attribute__((address_space(3))) half8_t lds_h8;
             lds_h8 *xp = (lds_h8 *)lds_ptr(lds_addr(xs + 16 * lane));
@@ -424,10 +428,11 @@ i4_gemv1_kernel(I4Gemv1Args a) {
 #pragma unroll
                     for (int i = 0; i < 8; ++i)
                         if (q0 + i < a.S && !((local >> (q0 + i)) & 1))
-                            pv[i] = i4_dot_range<WB>(a.X + (int64_t)(v / I1_TC) * a.ldx, a.P, a.scales, a.zeros,
-                                                     SZ, N, a.spg * KS, col0 + v % I1_TC,
-                                                     min((q0 + i) * I1_W * a.spw, a.nsteps) * KS,
-                                                     min((q0 + i + 1) * I1_W * a.spw, a.nsteps) * KS);
+                            pv[i] = i4_dot_range<WB, NORM>(a.X + (int64_t)(v / I1_TC) * a.ldx, a.P, a.scales,
+                                                           a.zeros, SZ, N, a.spg * KS, col0 + v % I1_TC,
+                                                           min((q0 + i) * I1_W * a.spw, a.nsteps) * KS,
+                                                           min((q0 + i + 1) * I1_W * a.spw, a.nsteps) * KS,
+                                                           a.wn, rstd_row);
                 }
 #pragma unroll
                 for (int i = 0; i < 8; ++i)

@@ -119,8 +119,12 @@ int check_kn(int64_t K, int64_t N) {
 // Scratch of the allocation-free matmul entry point: one split-K workspace per
 // GPU in the library's own device memory (zero at load; every completed call
 // leaves its counter area zero again).  Host code uses only the per-device
-// address from hipGetSymbolAddress, never the array's name.
-constexpr size_t kNoAllocScratchBytes = mcq4::COUNTER_BYTES + ((size_t)64 << 20);
+// address from hipGetSymbolAddress, never the array's name.  16 MiB of partials
+// hold every decode shape's split-K plan (1.25 MiB at M = 16..32, K = 14336) and
+// prefill plans up to M = 64 at K = 14336; larger split-K plans are rejected.
+// The array is part of the library image, so every GPU the library is loaded on
+// holds it (16.25 MiB) whether or not the entry point is called.
+constexpr size_t kNoAllocScratchBytes = mcq4::COUNTER_BYTES + ((size_t)16 << 20);
 static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 constexpr int kMaxDevices = 64;
 std::atomic<void *> g_scratch[kMaxDevices];
@@ -377,7 +381,9 @@ int mcq4_matmul_q4_0_f16_noalloc(const void *X, int64_t ldx, const uint8_t *W, v
         g_scratch_dirty[dev].store(false, std::memory_order_release);
     }
     const int st = mcq4_matmul_q4_0_f16(X, ldx, W, Y, ldy, M, K, N, ws, kNoAllocScratchBytes, stream);
-    if (st == MCQ4_ERR_HIP) g_scratch_dirty[dev].store(true, std::memory_order_release);
+    // Any failure may follow a launch that drew split-K tickets: the next call
+    // zeroes the counter area first.
+    if (st != MCQ4_OK) g_scratch_dirty[dev].store(true, std::memory_order_release);
     return st;
 }
 

@@ -6,6 +6,7 @@
 // RuntimeError (TORCH_CHECK), work enqueued on the current stream without a
 // synchronisation.  The split-K workspace is kept per (device, stream),
 // zero-filled once (every call leaves its counters zero).
+#include <string>
 #include <torch/extension.h>
 #include <c10/hip/HIPStream.h>
 #include <c10/core/DeviceGuard.h>
@@ -56,7 +57,14 @@ torch::Tensor matmul_ggml_q4_0(torch::Tensor X, torch::Tensor W_blocks) {
     const int st = mcq4_matmul_q4_0_f16(x.data_ptr(), K, w.data_ptr<uint8_t>(), Y.data_ptr(), N, M, K, N,
                                         need ? ws.data_ptr() : nullptr, need ? (size_t)ws.numel() : 0,
                                         stream);
-    TORCH_CHECK(st == MCQ4_OK, "matmul_ggml_q4_0: ", mcq4_status_string(st), ": ", mcq4_last_error());
+    if (st != MCQ4_OK) {
+        // A call that failed after some split-K workgroups drew tickets would leave
+        // the per-stream workspace's counter area non-zero for the next call: zero
+        // it again (a fill kernel on the same stream) before reporting the error.
+        const std::string msg = mcq4_last_error();
+        if (need) (void)mcq4_reset_workspace(ws.data_ptr(), (size_t)ws.numel(), stream);
+        TORCH_CHECK(false, "matmul_ggml_q4_0: ", mcq4_status_string(st), ": ", msg);
+    }
     return Y;
 }
 

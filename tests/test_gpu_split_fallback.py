@@ -54,6 +54,22 @@ def _i4_case(dev, M, K, N, gs, wb):
     return (lambda: mo.matmul_int8(X, *args, gs)), Yref
 
 
+def _rms_case(dev, M, K, N, gs):
+    """fused_rmsnorm_linear_int4: the one-launch M == 1 kernel normalises the row
+    inside the GEMV, so its recompute path must rebuild the normalised row."""
+    import metalops_amd as mo
+    g = torch.Generator().manual_seed(M + K + N + 1)
+    X = torch.randn(M, K, generator=g).half()
+    wn = (torch.rand(K, generator=g) + 0.5).half()
+    W = (torch.randn(K, N, generator=g) * 0.02).half().to(dev)
+    p, s, z = mo.quantize_int4(W, gs)
+    Xn = R4.rmsnorm_f16(X.numpy(), wn.numpy(), 1e-5)
+    Yref = R4.matmul_f32(Xn.astype(np.float32), p.cpu().numpy(), s.float().cpu().numpy(),
+                         z.float().cpu().numpy(), gs)
+    Xd, wnd = X.to(dev), wn.to(dev)
+    return (lambda: mo.fused_rmsnorm_linear_int4(Xd, wnd, p, s, z, 1e-5, gs)), Yref
+
+
 CASES = [
     # (name, environment, case builder args)
     ("q4_gemvm_s2", {"MCQ4_GEMVM_SPLIT": "2"}, ("q4", 16, 14336, 4096)),
@@ -63,6 +79,7 @@ CASES = [
     ("q4_gemm6_s2", {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "2"}, ("q4", 300, 4096, 640)),
     ("i4_gemv1", {}, ("i4", 1, 4096, 4096, 128, 4)),
     ("i4_gemv1_mr", {}, ("i4", 8, 11008, 4096, 128, 4)),
+    ("i4_gemv1_rmsnorm", {}, ("rms", 1, 4096, 4096, 128)),
     ("i4_gemv", {"MCQ4_I4_GEMV1": "0"}, ("i4", 4, 4096, 1040, 64, 4)),
     ("i8_gemv", {"MCQ4_I4_GEMV1": "0"}, ("i4", 8, 4096, 1024, 128, 8)),
     ("i4_gemm6_s2", {"MCQ4_I4_GEMM7": "0"}, ("i4", 2048, 14336, 4096, 128, 4)),
@@ -78,7 +95,8 @@ def test_split_recompute_path(dev, monkeypatch, name, env, case):
         monkeypatch.delenv(k, raising=False)
     for k, v in env.items():
         monkeypatch.setenv(k, v)
-    fn, Yref = _q4_case(dev, *case[1:]) if case[0] == "q4" else _i4_case(dev, *case[1:])
+    build = {"q4": _q4_case, "i4": _i4_case, "rms": _rms_case}[case[0]]
+    fn, Yref = build(dev, *case[1:])
     Y = fn()
     torch.cuda.synchronize()
     base = _lib.split_fallback_count(reset=True)

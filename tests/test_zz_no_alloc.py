@@ -35,9 +35,9 @@ def _run_pair(dev, M, K, N, seed):
 
 
 @pytest.mark.parametrize("first,second", [
-    ((2048, 14336, 4096), (16, 14336, 4096)),     # prefill split-K (64 MiB) then decode split-K
+    ((200, 11008, 1024), (16, 14336, 4096)),      # prefill split-K (16 MiB) then decode split-K
     ((16, 14336, 4096), (8, 4096, 1040)),         # decode split-K then a smaller decode
-    ((512, 11008, 4096), (130, 1024, 384)),       # 4-way split-K reduce then a small prefill
+    ((128, 11008, 1024), (130, 1024, 384)),       # prefill split-K then a small prefill
 ])
 def test_noalloc_matches_workspace_entry(dev, monkeypatch, first, second):
     from metalops_amd import _lib
@@ -55,7 +55,14 @@ def test_noalloc_rejects_oversized_and_bad_args(dev):
     from metalops_amd import _lib
     L = _lib.lib
     cap = int(L.mcq4_matmul_noalloc_max_workspace_bytes())
-    assert cap == 256 * 1024 + 64 * 1024 * 1024
+    assert cap == 256 * 1024 + 16 * 1024 * 1024
+    # a plan whose split-K workspace exceeds the scratch is refused with a clear error
+    big = (2048, 14336, 4096)
+    assert int(L.mcq4_matmul_workspace_bytes(*big)) > cap
+    xb = torch.zeros(1, 16, dtype=torch.float16, device=dev)
+    assert L.mcq4_matmul_q4_0_f16_noalloc(xb.data_ptr(), 14336, xb.data_ptr(), xb.data_ptr(), 4096,
+                                          *big, None) == _lib.MCQ4_ERR_WORKSPACE
+    assert b"allocation-free" in L.mcq4_last_error()
     # argument errors are reported as by the workspace entry point
     assert L.mcq4_matmul_q4_0_f16_noalloc(None, 32, None, None, 8, 1, 32, 8, None) == _lib.MCQ4_ERR_INVALID_ARG
     x = torch.zeros(1, 48, dtype=torch.float16, device=dev)
