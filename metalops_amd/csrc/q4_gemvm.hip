@@ -18,11 +18,13 @@
 //     the batch's 8 K blocks, loaded from global memory into registers right
 //     before the batch's first weight copy is issued (so the in-order vmcnt never
 //     makes a weight wait stall behind them), then rearranged to
-//     x' = [x0, x4, x1/16, x5/16, x2, x6, x3/16, x7/16].
-//   * Per K block row: B = [1024+q0, 1024+q4, 1024+16q1, ...] from four
-//     v_and_or_b32, and mfma(x', B, -S) with -S = mfma(x', -C) of that row
-//     (C = [1032, 1032, 1152, 1152, ...]) gives sum x*(q-8) for the lane's four
-//     output rows 4g..4g+3 of column r; acc += d * that in fp32.
+//     x' = [x0, x4, x1, x5, x2, x6, x3, x7].
+//   * Per K block row: B = [1024+q0, 1024+q4, 64+q1, 64+q5, ...] from four
+//     v_and_or_b32 (a high nibble left in place under the exponent of 64 is
+//     64 + q), and mfma(x', B, -S) with -S = mfma(x', -C) of that row
+//     (C = [1032, 1032, 72, 72, ...]) gives sum x*(q-8) for the lane's four
+//     output rows 4g..4g+3 of column r; acc += d * that in fp32, four rows at a
+//     time after their LDS reads and MFMAs.
 //   * Epilogue: per-wave partials through LDS, summed over waves in order
 //     (deterministic), stored as fp16 for rows < M.
 #include <algorithm>
@@ -40,6 +42,11 @@ constexpr int GM_WCH = GM_B * 18;            // 144 strip chunks per item
 constexpr int GM_SLOT = GM_WCH * 16 + 64;    // + read overhang
 constexpr int GM_TPW_MAX = 4;
 constexpr int GM_NT = 2;                     // cache policy of the weight copies: non-temporal
+#ifndef GM_GU_SET
+constexpr int GM_GU = 4;                     // K-block rows unpacked per group
+#else
+constexpr int GM_GU = GM_GU_SET;
+#endif
 
 struct GemvMArgs {
     const _Float16 *X;
@@ -144,12 +151,13 @@ q4_gemvm_kernel(GemvMArgs a) {
     const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
     const uint32_t qal = (uint32_t)(qoff & ~3), qsh = (uint32_t)(qoff & 3) * 8;
     const uint32_t doff = (uint32_t)(c * BLOCK_BYTES);
-    const uint32_t c64 = opaque_vgpr(0x64006400u);
+    // fp16 exponent words: 1024 + q for a low nibble, 64 + q for a high nibble
+    // left in place (bits 4..7 of the half: 64 * (1 + 16q/1024)).
+    const uint32_t e1024 = opaque_vgpr(0x64006400u), e64 = opaque_vgpr(0x54005400u);
     const uint32_t mlo = opaque_sgpr(0x000F000Fu), mhi = opaque_sgpr(0x00F000F0u);
-    const uint32_t nlo = 0xE408E408u, nhi = 0xE480E480u;     // -1032, -1152 pairs
+    const uint32_t nlo = 0xE408E408u, nhi = 0xD480D480u;     // -1032, -72 pairs
     const half8_t negc = bitcast<half8_t>(uint4_t{nlo, nhi, nlo, nhi});
     const float4_t z = {0.f, 0.f, 0.f, 0.f};
-    const half2_t s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
 
     float4_t acc[RB][TPW];
 #pragma unroll
@@ -167,12 +175,10 @@ q4_gemvm_kernel(GemvMArgs a) {
 #pragma unroll
         for (int u = 0; u < GM_B; ++u) {
             const uint4_t x = xr[rb][u];
-            const uint32_t h15 = __builtin_amdgcn_perm(x[2], x[0], 0x07060302u);   // x1, x5
-            const uint32_t h37 = __builtin_amdgcn_perm(x[3], x[1], 0x07060302u);   // x3, x7
             const uint4_t v = {__builtin_amdgcn_perm(x[2], x[0], 0x05040100u),     // x0, x4
-                               bitcast<uint32_t>(bitcast<half2_t>(h15) * s16),
+                               __builtin_amdgcn_perm(x[2], x[0], 0x07060302u),     // x1, x5
                                __builtin_amdgcn_perm(x[3], x[1], 0x05040100u),     // x2, x6
-                               bitcast<uint32_t>(bitcast<half2_t>(h37) * s16)};
+                               __builtin_amdgcn_perm(x[3], x[1], 0x07060302u)};    // x3, x7
             xq[rb][u] = bitcast<half8_t>(v);
             if constexpr (HOIST) nsh[rb][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb][u], negc, z, 0, 0, 0);
         }
@@ -189,40 +195,63 @@ q4_gemvm_kernel(GemvMArgs a) {
                 else wait_vmcnt<3>();
                 const uint32_t base = lds_addr(ring + slot * GM_SLOT);
                 const uint32_t qa = base + qal, da = base + doff;
-                auto row = [&](int u) {
-                    const lds_u32 *qp = (const lds_u32 *)(lds_ptr(qa) + u * GM_ROW);
-                    const uint32_t q0 = qp[0], q1 = qp[1];
-                    const uint32_t w = __builtin_amdgcn_alignbit(q1, q0, qsh);
-                    const uint32_t w8 = __builtin_amdgcn_alignbit(q1, q0, qsh + 8);
-                    const float d = (float)bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(da) + u * GM_ROW));
-                    const uint4_t bq = {and_or(w, mlo, c64), and_or(w, mhi, c64),
-                                        and_or(w8, mlo, c64), and_or(w8, mhi, c64)};
-                    // -S of this row, recomputed per item: keeps 32 VGPRs free so a
-                    // 16-wave workgroup fits in 128 VGPRs (the MFMA pipe has room).
+                // GU K-block rows at a time: their LDS reads first, then the
+                // unpacks and MFMAs, then the scaled sums, so a wave is not
+                // serialised on LDS and MFMA latency row by row.
+                constexpr int GU = GM_GU;
+                auto rows4 = [&](int u0, int nrows) {
+                    uint32_t q0[GU], q1[GU];
+                    float d[GU];
 #pragma unroll
-                    for (int rb = 0; rb < RB; ++rb) {
-                        float4_t ns;
-                        if constexpr (HOIST) ns = nsh[rb][u];
-                        else ns = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb][u], negc, z, 0, 0, 0);
-                        const float4_t blk =
-                            __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb][u], bitcast<half8_t>(bq), ns, 0, 0, 0);
-                        if constexpr (GR == 4) {
-                            acc[rb][j][0] += d * blk[0];
-                        } else if constexpr (GR == 8) {
-                            acc[rb][j][0] += d * blk[0];
-                            acc[rb][j][2] += d * blk[2];
-                        } else {
-                            acc[rb][j] += d * blk;
+                    for (int v = 0; v < GU; ++v) {
+                        const lds_u32 *qp = (const lds_u32 *)(lds_ptr(qa) + (u0 + v) * GM_ROW);
+                        q0[v] = qp[0];
+                        q1[v] = qp[1];
+                        d[v] = (float)bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(da) + (u0 + v) * GM_ROW));
+                    }
+                    float4_t blk[RB][GU];
+#pragma unroll
+                    for (int v = 0; v < GU; ++v) {
+                        const int u = u0 + v;
+                        const uint32_t w = __builtin_amdgcn_alignbit(q1[v], q0[v], qsh);
+                        const uint32_t w8 = __builtin_amdgcn_alignbit(q1[v], q0[v], qsh + 8);
+                        const uint4_t bq = {and_or(w, mlo, e1024), and_or(w, mhi, e64),
+                                            and_or(w8, mlo, e1024), and_or(w8, mhi, e64)};
+#pragma unroll
+                        for (int rb = 0; rb < RB; ++rb) {
+                            // -S of this row, recomputed per item unless hoisted: keeps 32
+                            // VGPRs free so a 16-wave workgroup fits in 128 VGPRs.
+                            float4_t ns;
+                            if constexpr (HOIST) ns = nsh[rb][u];
+                            else ns = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb][u], negc, z, 0, 0, 0);
+                            blk[rb][v] =
+                                __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[rb][u], bitcast<half8_t>(bq), ns, 0, 0, 0);
+                        }
+                    }
+#pragma unroll
+                    for (int v = 0; v < GU; ++v) {
+                        if (v >= nrows) break;
+#pragma unroll
+                        for (int rb = 0; rb < RB; ++rb) {
+                            if constexpr (GR == 4) {
+                                acc[rb][j][0] += d[v] * blk[rb][v][0];
+                            } else if constexpr (GR == 8) {
+                                acc[rb][j][0] += d[v] * blk[rb][v][0];
+                                acc[rb][j][2] += d[v] * blk[rb][v][2];
+                            } else {
+                                acc[rb][j] += d[v] * blk[rb][v];
+                            }
                         }
                     }
                 };
                 if (rows == GM_B) {
 #pragma unroll
-                    for (int u = 0; u < GM_B; ++u) row(u);
+                    for (int u0 = 0; u0 < GM_B; u0 += GU) rows4(u0, GU);
                 } else {
+                    // Rows past K hold a copy of row 0 (valid data, never summed).
 #pragma unroll
-                    for (int u = 0; u < GM_B; ++u)
-                        if (u < rows) row(u);
+                    for (int u0 = 0; u0 < GM_B; u0 += GU)
+                        if (u0 < rows) rows4(u0, min(rows - u0, GU));
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
                 slot ^= 1;
@@ -413,8 +442,11 @@ static GmPlan gemvm_plan(int64_t M, int64_t K, int64_t N) {
         S = v == 2 || v == 4 || v == 8 ? v : 1;
     }
     S = std::max(1, std::min(S, nbt));
-    const int tpw = S > 1 ? std::min(GM_TPW_MAX, S) : std::min(GM_TPW_MAX, (ntiles + cap - 1) / cap);
-    const int grid = (ntiles + tpw - 1) / tpw;
+    // Without a split: every CU gets a workgroup (tiles wg, wg + grid, ...: three
+    // or four each at N = 14336) rather than ceil(ntiles / 4) full ones.
+    const int grid0 = S > 1 ? 0 : std::min(ntiles, cap);
+    const int tpw = S > 1 ? std::min(GM_TPW_MAX, S) : std::min(GM_TPW_MAX, (ntiles + grid0 - 1) / grid0);
+    const int grid = S > 1 ? (ntiles + tpw - 1) / tpw : std::max(grid0, (ntiles + tpw - 1) / tpw);
     const int bps = (nbt + S - 1) / S;
     return {waves, tpw, grid, (nbt + bps - 1) / bps, bps};
 }
