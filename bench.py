@@ -51,7 +51,7 @@ FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
 # workloads (bench.py --part decode|prefill), each counter scaled by what it reads
 # for a plain 256 MiB device copy (FETCH_SIZE x 2, WRITE_SIZE x 1).  Figures and
 # commands: profiles/gemv_dma_llama7b_m1.md, profiles/q4_gemm7_llama7b_m2048.md.
-DECODE_TRAFFIC_BYTES = 22999449       # average over the five projections
+DECODE_TRAFFIC_BYTES = 23294795       # average over the five projections (23.28 MB read + 0.017 MB written)
 DECODE_KERNEL = "q4_gemv_dma_kernel (decode GEMV, M=1)"
 PREFILL_KERNEL = "q4_gemm7_kernel (M=2048 K=4096 N=14336)"
 PREFILL_UP_TRAFFIC_BYTES = 361849343  # 302.7 MB read + 59.2 MB written
