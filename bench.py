@@ -686,7 +686,42 @@ def probes(torch, dev):
                 ex.append(rec)
     out["store_to_load"] = ex
 
-    # 5. Shader clock under a dense MFMA load.
+    # 5. Prefill tile time against the number of tiles in flight: the 256 x 256-tile
+    #    GEMM (forced with MCQ4_GEMM_PATH=7, no K split: MCQ4_GEMM6_SPLIT=1) on M = 256,
+    #    K = 4096, N = 256 n -- n tiles, one workgroup per CU up to 256, then rounds --
+    #    with random operands and with all-zero operands.
+    import metalops_amd as mo
+    from metalops_amd import _lib as mlib
+    saved = {k: os.environ.get(k) for k in ("MCQ4_GEMM_PATH", "MCQ4_GEMM6_SPLIT")}
+    os.environ["MCQ4_GEMM_PATH"] = "7"
+    os.environ["MCQ4_GEMM6_SPLIT"] = "1"
+    mlib.reload_options()
+    tiles = []
+    try:
+        for n in (1, 8, 64, 128, 192, 256, 448, 512):
+            rec = {"tiles": n}
+            w = make_weights(mo, torch, 4096, 256 * n, 5, dev)
+            g = torch.Generator(device=dev).manual_seed(6)
+            x = torch.randn(256, 4096, generator=g, device=dev).half()
+            for kind in ("random", "zero"):
+                if kind == "zero":
+                    w.zero_()
+                    x.zero_()
+                t = graph_time(lambda i: mo.matmul_ggml_q4_0(x, w), 4, reps=10)
+                rec[kind + "_us"] = round(t * 1e6, 2)
+            rec["tflops_random"] = round(2.0 * 256 * 4096 * 256 * n / (rec["random_us"] * 1e-6) / 1e12, 1)
+            tiles.append(rec)
+            del w, x
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        mlib.reload_options()
+    out["prefill_tile_scaling"] = tiles
+
+    # 6. Shader clock under a dense MFMA load.
     tk = torch.zeros(4096, dtype=torch.int64, device=dev)
     bench_check(lib.mcqb_measure_sclk(tk.data_ptr(), 20000, None), "mcqb_measure_sclk")
     torch.cuda.synchronize()
