@@ -61,7 +61,11 @@ constexpr int GV_WIDE = 64;                  // tile width of the large-N plan
 constexpr int GV_WIDE_MIN_TILES = 1024;      // 64-column tiles from N = 65536 on
 constexpr int GV_TPW_MAX = 4;                // tiles per workgroup
 constexpr int GV_K_MAX = 16384;
+#ifndef GV_RING_SET
 constexpr int GV_RING = 2;                   // items in flight per wave (1 and 3 measured slower)
+#else
+constexpr int GV_RING = GV_RING_SET;
+#endif
 constexpr int GV_NT = 2;                     // cache policy of the weight copies: non-temporal
 
 constexpr int GV_GROUP_MAX = 4;              // weights sharing X in one launch
@@ -367,9 +371,18 @@ bool gemv_dma_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t 
 // 16-column tiles (64-column tiles when N % 64 == 0 and the weights hold 1024 or
 // more of them); *n_done returns the number of leading columns of each weight
 // covered.
+bool gemv_span_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t N);
+hipError_t launch_gemv_span(const _Float16 *X, const uint8_t *W, _Float16 *Y, int K, int N, hipStream_t s);
+
 hipError_t launch_gemv_dma_group(const _Float16 *X, const uint8_t *const *W, _Float16 *const *Y, int count,
                                  int K, int N, int *n_done, hipStream_t s) {
     if (count < 1 || count > GV_GROUP_MAX || (count > 1 && N % 16)) return hipErrorInvalidValue;
+    // One weight with 4096 < N <= 12288 at K <= 4096: contiguous spans of 1..3
+    // 16-column groups per workgroup (q4_gemv_span.hip).
+    if (count == 1 && gemv_span_supported(X, W[0], K, N)) {
+        *n_done = N;
+        return launch_gemv_span(X, W[0], Y[0], K, N, s);
+    }
     GemvArgs a;
     a.X = X;
     for (int g = 0; g < GV_GROUP_MAX; ++g) {
@@ -398,7 +411,11 @@ hipError_t launch_gemv_dma_group(const _Float16 *X, const uint8_t *const *W, _Fl
     // (more than 1024 tiles) runs 8-wave workgroups of GV_TPW_MAX tiles, two per
     // CU, backfilled as they finish (16-column tiles at N = 128256: 56 vs 66 us
     // with 16 waves; 16 waves stay faster on the layer shapes).
+#ifndef GV_NW_SET
     const int nw = a.ntiles > 256 * GV_TPW_MAX ? 8 : 16;
+#else
+    const int nw = GV_NW_SET;
+#endif
     const int per_round = nw == 16 ? 256 : 512;
     int grid = std::min(a.ntiles, per_round);
     if (a.ntiles > per_round * GV_TPW_MAX) grid = (a.ntiles + GV_TPW_MAX - 1) / GV_TPW_MAX;

@@ -250,6 +250,8 @@ PATHS = {
     "gemm7": {"MCQ4_GEMM_PATH": "7"},
     "gemm7_split2": {"MCQ4_GEMM_PATH": "7", "MCQ4_GEMM6_SPLIT": "2"},
     "gemm7_split3": {"MCQ4_GEMM_PATH": "7", "MCQ4_GEMM6_SPLIT": "3"},
+    "gemv_span": {},
+    "gemv_span_off": {"MCQ4_GEMV_SPAN": "0"},
 }
 PATH_SHAPES = {
     "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
@@ -258,6 +260,12 @@ PATH_SHAPES = {
     # (a last item of one row) and waves without batches.
     "gemv_dma_wide": [(1, 32, 65536), (1, 352, 65536), (1, 2080, 65600), (1, 4096, 70016)],
 
+    # Contiguous spans of 16-column groups (M = 1, 4096 < N <= 12288, K <= 4096):
+    # one to three groups per workgroup, one K block, a partial last batch, the
+    # largest K and N, ragged group counts (257, 513, 767 groups).
+    "gemv_span": [(1, 32, 4112), (1, 352, 8208), (1, 4096, 12288), (1, 4064, 12272), (1, 2080, 6144),
+                  (1, 96, 4128), (1, 4096, 8192)],
+    "gemv_span_off": [(1, 4096, 12288), (1, 352, 8208)],
     "decode_lds_m1": [(1, 352, 264), (1, 4096, 1032)],
     "gemvm": [(2, 32, 16), (3, 352, 264), (4, 1024, 4104), (5, 11008, 512), (8, 4096, 14336),
               (11, 2048, 1040), (16, 14336, 4096), (16, 352, 8200)],
@@ -296,7 +304,8 @@ PATH_SHAPES = {
 @pytest.mark.parametrize("path,M,K,N", [(p, *s) for p, shapes in PATH_SHAPES.items() for s in shapes])
 def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM", "MCQ4_GEMV_PATH",
-              "MCQ4_GEMM6_SPLIT", "MCQ4_GEMVM_SPLIT", "MCQ4_GEMVM_HOIST", "MCQ4_XCD_LOCAL"):
+              "MCQ4_GEMM6_SPLIT", "MCQ4_GEMVM_SPLIT", "MCQ4_GEMVM_HOIST", "MCQ4_XCD_LOCAL",
+              "MCQ4_GEMV_SPAN"):
         monkeypatch.delenv(k, raising=False)
     for k, v in PATHS[path].items():
         monkeypatch.setenv(k, v)
