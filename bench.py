@@ -51,8 +51,8 @@ FP16_PEAK_TFLOPS = 2500.0    # MI355X dense fp16 MFMA
 # workloads (bench.py --part decode|prefill), each counter scaled by what it reads
 # for a plain 256 MiB device copy (FETCH_SIZE x 2, WRITE_SIZE x 1).  Figures and
 # commands: profiles/gemv_dma_llama7b_m1.md, profiles/q4_gemm7_llama7b_m2048.md.
-DECODE_TRAFFIC_BYTES = 23294795       # average over the five projections (23.28 MB read + 0.017 MB written)
-DECODE_KERNEL = "q4_gemv_dma_kernel (decode GEMV, M=1)"
+DECODE_TRAFFIC_BYTES = 23335567       # average over the five projections (23.32 MB read + 0.017 MB written)
+DECODE_KERNEL = "q4_gemv_span_kernel (qkv, gate, up) + q4_gemv_dma_kernel (o, down): decode GEMV, M=1"
 PREFILL_KERNEL = "q4_gemm7_kernel (M=2048 K=4096 N=14336)"
 PREFILL_UP_TRAFFIC_BYTES = 361849343  # 302.7 MB read + 59.2 MB written
 
@@ -613,8 +613,9 @@ def probes(torch, dev):
 
     # 2. Read patterns of a q4_0 weight [K/32][N][18] at the layer's shapes, over
     #    copies rotated through >= 1.1 GB (reads from HBM): contiguous, 16-column
-    #    strips (one workgroup per strip, the M = 1 kernel's pattern) and 64-column
-    #    tiles split four ways along K.
+    #    strips (one workgroup per strip, the M = 1 strip kernel's pattern), 64-column
+    #    tiles split four ways along K and, at N > 4096, spans of 2-3 16-column groups
+    #    (one workgroup per span, near the M = 1 span kernel's 256 spans).
     sink = torch.zeros(4, dtype=torch.int32, device=dev)
     pats = []
     for _, K, N in DECODE_LAYER[:2] + DECODE_LAYER[2:3] + DECODE_LAYER[4:]:
@@ -631,6 +632,13 @@ def probes(torch, dev):
             "tile64_k4": lambda i: bench_check(lib.mcqb_read_tiles(bufs[i].data_ptr(), K, N, 64, 4, 16,
                                                                    sink.data_ptr(), cs()), "mcqb_read_tiles"),
         }
+        if N > 4096:
+            g = -(-N // (16 * 256))
+            while N % (16 * g):
+                g -= 1
+            rec["span_cols"] = 16 * g
+            kinds["span"] = lambda i, c=16 * g: bench_check(
+                lib.mcqb_read_tiles(bufs[i].data_ptr(), K, N, c, 1, 16, sink.data_ptr(), cs()), "mcqb_read_tiles")
         for name, fn in kinds.items():
             t = graph_time(fn, copies)
             rec[name] = {"us": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1)}
