@@ -371,17 +371,18 @@ bool gemv_dma_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t 
 // 16-column tiles (64-column tiles when N % 64 == 0 and the weights hold 1024 or
 // more of them); *n_done returns the number of leading columns of each weight
 // covered.
-bool gemv_span_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t N);
-hipError_t launch_gemv_span(const _Float16 *X, const uint8_t *W, _Float16 *Y, int K, int N, hipStream_t s);
+bool gemv_span_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N);
+hipError_t launch_gemv_span(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y, int64_t ldy, int M,
+                            int K, int N, hipStream_t s);
 
 hipError_t launch_gemv_dma_group(const _Float16 *X, const uint8_t *const *W, _Float16 *const *Y, int count,
                                  int K, int N, int *n_done, hipStream_t s) {
     if (count < 1 || count > GV_GROUP_MAX || (count > 1 && N % 16)) return hipErrorInvalidValue;
-    // One weight with 4096 < N <= 12288 at K <= 4096: contiguous spans of 1..3
+    // One weight with 4096 < N <= 16384 at K <= 4096: contiguous spans of 1..4
     // 16-column groups per workgroup (q4_gemv_span.hip).
-    if (count == 1 && gemv_span_supported(X, W[0], K, N)) {
+    if (count == 1 && gemv_span_supported(X, K, W[0], 1, K, N)) {
         *n_done = N;
-        return launch_gemv_span(X, W[0], Y[0], K, N, s);
+        return launch_gemv_span(X, K, W[0], Y[0], N, 1, K, N, s);
     }
     GemvArgs a;
     a.X = X;

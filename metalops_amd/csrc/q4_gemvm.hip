@@ -458,8 +458,18 @@ size_t gemvm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     return p.S > 1 ? COUNTER_BYTES + (size_t)p.S * M * (N / 16) * 16 * sizeof(float) : 0;
 }
 
+bool gemv_span_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N);
+hipError_t launch_gemv_span(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y, int64_t ldy, int M,
+                            int K, int N, hipStream_t s);
+
 hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, void *ws, int *n_done, hipStream_t s) {
+    // 9 <= M <= 16 with 4096 < N <= 16384 at K <= 4096: contiguous spans of
+    // 16-column groups per workgroup (q4_gemv_span.hip), no K split and no workspace.
+    if (gemv_span_supported(X, ldx, W, M, K, N)) {
+        *n_done = N;
+        return launch_gemv_span(X, ldx, W, Y, ldy, M, K, N, s);
+    }
     GemvMArgs a;
     a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
     a.M = M; a.nb = K / QK; a.N = N;

@@ -260,12 +260,16 @@ PATH_SHAPES = {
     # (a last item of one row) and waves without batches.
     "gemv_dma_wide": [(1, 32, 65536), (1, 352, 65536), (1, 2080, 65600), (1, 4096, 70016)],
 
-    # Contiguous spans of 16-column groups (M = 1, 4096 < N <= 12288, K <= 4096):
-    # one to three groups per workgroup, one K block, a partial last batch, the
+    # Contiguous spans of 16-column groups (M = 1 and 9..16, 4096 < N <= 16384,
+    # K <= 4096; M = 2..8 of the same shapes take the strip kernel): one to four
+    # groups per workgroup, one K block, a partial last batch, the
     # largest K and N, ragged group counts (257, 513, 767 groups).
     "gemv_span": [(1, 32, 4112), (1, 352, 8208), (1, 4096, 12288), (1, 4064, 12272), (1, 2080, 6144),
-                  (1, 96, 4128), (1, 4096, 8192)],
-    "gemv_span_off": [(1, 4096, 12288), (1, 352, 8208)],
+                  (1, 96, 4128), (1, 4096, 8192), (1, 4096, 16384), (1, 1024, 14336),
+                  # M = 9..16 (16 rows per MFMA A operand); M = 2..8 pass to the strip kernel.
+                  (2, 352, 8208), (3, 4096, 14336), (4, 4096, 14336), (5, 32, 4112), (8, 2080, 16384),
+                  (9, 4096, 12288), (12, 96, 16368), (16, 4096, 14336), (16, 4064, 6144)],
+    "gemv_span_off": [(1, 4096, 12288), (1, 352, 8208), (4, 4096, 14336), (16, 352, 8208)],
     "decode_lds_m1": [(1, 352, 264), (1, 4096, 1032)],
     "gemvm": [(2, 32, 16), (3, 352, 264), (4, 1024, 4104), (5, 11008, 512), (8, 4096, 14336),
               (11, 2048, 1040), (16, 14336, 4096), (16, 352, 8200)],
@@ -365,7 +369,14 @@ def _random_cases(n, seed):
     return cases
 
 
-@pytest.mark.parametrize("M,K,N,pad", _random_cases(48, 20261202))
+# The span kernel's region (M = 1 and 9..16, 4096 < N <= 16384, K <= 4096) and the
+# strip kernel's shapes next to it (M = 3, 6) with row strides
+# past K, which the random draw above never reaches.
+SPAN_STRIDE_CASES = [(1, 2048, 8208, 8), (3, 4096, 8192, 40), (6, 352, 16384, 40), (16, 1024, 12288, 8),
+                     (11, 4096, 14336, 40)]
+
+
+@pytest.mark.parametrize("M,K,N,pad", _random_cases(48, 20261202) + SPAN_STRIDE_CASES)
 def test_matmul_random_shapes(dev, M, K, N, pad):
     """Random shapes and strides against the oracle's fp32 product, with the
     reference-rule quantizer; the row stride of X is K + pad."""
