@@ -17,7 +17,7 @@
 //   * Barrier between the two steps of a stage; stage s+3's copies go out
 //     during the second step, one per two MFMAs.
 //   * Split K (grid.z): fp32 partial tiles in the caller's workspace, summed in
-//     split order by q4_gemm6_reduce_kernel; with two splits the second
+//     split order by q4_gemm6_reduce_kernel<S>; with two splits the second
 //     workgroup of a tile to finish adds the first's partial itself, read from
 //     their shared XCD's L2 (see xcd_ticket_inc), and stores Y.
 //
@@ -340,24 +340,68 @@ q4_gemm6_kernel(Gemm6Args a) {
 }
 
 // Sums the S fp32 partial tiles of every output tile in split order
-// (deterministic) and stores fp16; four consecutive columns per thread.
+// (deterministic) and stores fp16.  Thread t of block b owns float4 v = 256 b +
+// t + 256 u of the [tiles][128 x 256] output for u < G6_RV; with S a template
+// argument every split's loads of all its float4 go out before the first add
+// (SC == 0: S read at run time, one split's loads at a time).
+constexpr int G6_RV = 2;
+template <int SC>
 __global__ void __launch_bounds__(256)
 q4_gemm6_reduce_kernel(Gemm6Args a) {
     constexpr int TILE = G6_BM * G6_BN;
-    const int64_t v4 = (int64_t)blockIdx.x * 256 + threadIdx.x;     // float4 index
-    const int64_t ntiles = (int64_t)a.tiles_m * a.tiles_n;
-    if (v4 >= ntiles * (TILE / 4)) return;
-    const int64_t tile = v4 / (TILE / 4);
-    const int e = (int)(v4 % (TILE / 4)) * 4;
-    const int tm = (int)(tile % a.tiles_m), tn = (int)(tile / a.tiles_m);
-    const float4_t *p = (const float4_t *)(a.partials + tile * a.S * TILE + e);
-    float4_t sum = p[0];
-    for (int sp = 1; sp < a.S; ++sp) sum += p[(int64_t)sp * (TILE / 4)];
-    const int m = tm * G6_BM + e / G6_BN, n = tn * G6_BN + e % G6_BN;
-    if (m >= a.M) return;
+    const int S = SC ? SC : a.S;
+    const int64_t n4 = (int64_t)a.tiles_m * a.tiles_n * (TILE / 4);
+    const int64_t base = (int64_t)blockIdx.x * (256 * G6_RV) + threadIdx.x;
+    const float4_t *p[G6_RV];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-        if (n + c < a.N) a.Y[(int64_t)m * a.ldy + n + c] = (_Float16)sum[c];
+    for (int u = 0; u < G6_RV; ++u) {
+        const int64_t v4 = min(base + 256 * u, n4 - 1);
+        const int64_t tile = v4 / (TILE / 4);
+        p[u] = (const float4_t *)(a.partials + tile * S * TILE) + v4 % (TILE / 4);
+    }
+    float4_t sum[G6_RV];
+    if constexpr (SC > 0) {
+        float4_t v[G6_RV][SC];
+#pragma unroll
+        for (int sp = 0; sp < SC; ++sp)
+#pragma unroll
+            for (int u = 0; u < G6_RV; ++u) v[u][sp] = __builtin_nontemporal_load(p[u] + (int64_t)sp * (TILE / 4));
+#pragma unroll
+        for (int u = 0; u < G6_RV; ++u) {
+            sum[u] = v[u][0];
+#pragma unroll
+            for (int sp = 1; sp < SC; ++sp) sum[u] += v[u][sp];
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < G6_RV; ++u) sum[u] = __builtin_nontemporal_load(p[u]);
+        for (int sp = 1; sp < S; ++sp) {
+            float4_t v[G6_RV];
+#pragma unroll
+            for (int u = 0; u < G6_RV; ++u) v[u] = __builtin_nontemporal_load(p[u] + (int64_t)sp * (TILE / 4));
+#pragma unroll
+            for (int u = 0; u < G6_RV; ++u) sum[u] += v[u];
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < G6_RV; ++u) {
+        const int64_t v4 = base + 256 * u;
+        if (v4 >= n4) break;
+        const int64_t tile = v4 / (TILE / 4);
+        const int e = (int)(v4 % (TILE / 4)) * 4;
+        const int tm = (int)(tile % a.tiles_m), tn = (int)(tile / a.tiles_m);
+        const int m = tm * G6_BM + e / G6_BN, n = tn * G6_BN + e % G6_BN;
+        if (m >= a.M) continue;
+        _Float16 *y = a.Y + (int64_t)m * a.ldy + n;
+        if (n + 3 < a.N && ((uintptr_t)y & 7) == 0) {
+            const half4_t h = {(_Float16)sum[u][0], (_Float16)sum[u][1], (_Float16)sum[u][2], (_Float16)sum[u][3]};
+            *(half4_t *)y = h;
+        } else {
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                if (n + c < a.N) y[c] = (_Float16)sum[u][c];
+        }
+    }
 }
 
 // Plan: 128-row tiles; K split S = the largest power of two (<= 16, at least
@@ -425,7 +469,13 @@ hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
     hipLaunchKernelGGL(q4_gemm6_kernel, dim3(gx, 1, a.S), dim3(256), G6_LDS, s, a);
     if (a.S > 1 && !a.tickets) {
         const int64_t n4 = (int64_t)ntiles * (G6_BM * G6_BN / 4);
-        hipLaunchKernelGGL(q4_gemm6_reduce_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, a);
+        const dim3 grid((unsigned)((n4 + 256 * G6_RV - 1) / (256 * G6_RV)));
+        switch (a.S) {
+            case 2: hipLaunchKernelGGL(q4_gemm6_reduce_kernel<2>, grid, dim3(256), 0, s, a); break;
+            case 4: hipLaunchKernelGGL(q4_gemm6_reduce_kernel<4>, grid, dim3(256), 0, s, a); break;
+            case 8: hipLaunchKernelGGL(q4_gemm6_reduce_kernel<8>, grid, dim3(256), 0, s, a); break;
+            default: hipLaunchKernelGGL(q4_gemm6_reduce_kernel<0>, grid, dim3(256), 0, s, a); break;
+        }
     }
     return hipGetLastError();
 }
