@@ -217,6 +217,7 @@ def bench_lib():
         lib = ctypes.CDLL(path)
         p, i, i64, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_size_t
         sigs = {"mcqb_read_probe": [p, sz, p, p], "mcqb_read_tiles": [p, i64, i64, i, i, i, p, p],
+                "mcqb_read_rows": [p, i64, i64, i64, i, i, p, p],
                 "mcqb_empty": [i, i, p], "mcqb_measure_sclk": [p, i, p],
                 "mcqb_atomic_chain": [p, i, i, p, p], "mcqb_exchange": [p, p, i, i, i, i, p]}
         for name, args in sigs.items():
@@ -646,6 +647,31 @@ def probes(torch, dev):
         del bufs
     torch.cuda.empty_cache()
     out["read_patterns"] = pats
+
+    # 2b. Per-group INT4 weights [K/2][N] (one byte per column per two K rows): pieces
+    #     of 64 and 128 columns (bytes), each piece column split along K so the grid
+    #     stays near 256 workgroups of 8 waves (the INT4 decode kernel's tile is 128).
+    ipats = []
+    for _, K, N in DECODE_LAYER[:2] + DECODE_LAYER[2:3] + DECODE_LAYER[4:]:
+        nbytes = (K // 2) * N
+        copies = max(2, -(-int(1.1e9) // nbytes))
+        bufs = [torch.empty(nbytes, dtype=torch.uint8, device=dev).random_(0, 256) for _ in range(copies)]
+        rec = {"K": K, "N": N, "bytes": nbytes}
+        cs = lambda: torch.cuda.current_stream().cuda_stream
+        kinds = {"contiguous": lambda i: bench_check(
+            lib.mcqb_read_probe(bufs[i].data_ptr(), nbytes, sink.data_ptr(), cs()), "mcqb_read_probe")}
+        for piece in (64, 128):
+            ks = max(1, 256 // (N // piece))
+            rec[f"piece{piece}_ksplit"] = ks
+            kinds[f"piece{piece}"] = lambda i, pc=piece, k=ks: bench_check(
+                lib.mcqb_read_rows(bufs[i].data_ptr(), K // 2, N, pc, k, 8, sink.data_ptr(), cs()), "mcqb_read_rows")
+        for name, fn in kinds.items():
+            t = graph_time(fn, copies)
+            rec[name] = {"us": round(t * 1e6, 3), "GB/s": round(nbytes / t / 1e9, 1)}
+        ipats.append(rec)
+        del bufs
+    torch.cuda.empty_cache()
+    out["int4_read_patterns"] = ipats
 
     # 3. Returning 64-bit atomic add, a dependent chain per workgroup.
     words = torch.zeros(256 * 64, dtype=torch.int64, device=dev)

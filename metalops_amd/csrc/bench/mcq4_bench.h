@@ -28,6 +28,13 @@ int mcqb_read_probe(const void *src, size_t bytes, uint32_t *sink, void *stream)
 int mcqb_read_tiles(const void *W, int64_t K, int64_t N, int tile_cols, int ksplit, int waves,
                     uint32_t *sink, void *stream);
 
+/* Any row-piece pattern: rows of row_bytes bytes (a multiple of 16) split into
+ * pieces of piece_bytes (a multiple of 16 that divides row_bytes) and ksplit row
+ * ranges; workgroup (t, s) reads rows [s*rows/ksplit, (s+1)*rows/ksplit) of piece
+ * column t.  The per-group INT4 weight [K/2][N] is rows = K/2, row_bytes = N. */
+int mcqb_read_rows(const void *W, int64_t rows, int64_t row_bytes, int64_t piece_bytes, int ksplit, int waves,
+                   uint32_t *sink, void *stream);
+
 /* An empty kernel of grid x block threads (the per-launch floor). */
 int mcqb_empty(int grid, int block, void *stream);
 

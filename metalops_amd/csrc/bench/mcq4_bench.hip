@@ -160,15 +160,18 @@ extern "C" int mcqb_read_probe(const void *src, size_t bytes, uint32_t *sink, vo
     return hip_status();
 }
 
-extern "C" int mcqb_read_tiles(const void *W, int64_t K, int64_t N, int tile_cols, int ksplit, int waves,
-                               uint32_t *sink, void *stream) {
-    if (!W || !sink || ((uintptr_t)W & 15) || K < 32 || K % 32 || N < 1 || tile_cols < 1 || ksplit < 1 ||
-        ksplit > K / 32 || (tile_cols * 18) % 16 || N % tile_cols || (N / tile_cols) * ksplit > 0x7fffffff)
+// Row pieces of piece_bytes of `rows` rows of row_bytes each, ksplit row ranges per
+// piece column: the shared body of mcqb_read_tiles and mcqb_read_rows.
+static int read_pieces(const void *W, int64_t rows, int64_t row_bytes, int64_t piece_bytes, int ksplit, int waves,
+                       uint32_t *sink, void *stream) {
+    if (!W || !sink || ((uintptr_t)W & 15) || rows < 1 || rows > 0x7fffffff || row_bytes < 16 || row_bytes % 16 ||
+        piece_bytes < 16 || piece_bytes % 16 || row_bytes % piece_bytes || ksplit < 1 || ksplit > rows ||
+        (row_bytes / piece_bytes) * ksplit > 0x7fffffff || rows * row_bytes / 16 > 0x7fffffff)
         return kInvalid;
-    const int ntile = (int)(N / tile_cols), grid = ntile * ksplit, cpr = tile_cols * 18 / 16;
+    const int ntile = (int)(row_bytes / piece_bytes), grid = ntile * ksplit, cpr = (int)(piece_bytes / 16);
     const hipStream_t s = (hipStream_t)stream;
-    const int nb = (int)(K / 32);
-    const int64_t grow = N * 18;
+    const int nb = (int)rows;
+    const int64_t grow = row_bytes;
     switch (waves) {
         case 4: hipLaunchKernelGGL(read_tiles_kernel<4>, dim3(grid), dim3(256), 0, s, (const uint8_t *)W, nb, grow, cpr, ksplit, ntile, sink); break;
         case 8: hipLaunchKernelGGL(read_tiles_kernel<8>, dim3(grid), dim3(512), 0, s, (const uint8_t *)W, nb, grow, cpr, ksplit, ntile, sink); break;
@@ -176,6 +179,18 @@ extern "C" int mcqb_read_tiles(const void *W, int64_t K, int64_t N, int tile_col
         default: return kInvalid;
     }
     return hip_status();
+}
+
+extern "C" int mcqb_read_tiles(const void *W, int64_t K, int64_t N, int tile_cols, int ksplit, int waves,
+                               uint32_t *sink, void *stream) {
+    if (K < 32 || K % 32 || N < 1 || tile_cols < 1 || (tile_cols * 18) % 16 || N % tile_cols || ksplit > K / 32)
+        return kInvalid;
+    return read_pieces(W, K / 32, N * 18, (int64_t)tile_cols * 18, ksplit, waves, sink, stream);
+}
+
+extern "C" int mcqb_read_rows(const void *W, int64_t rows, int64_t row_bytes, int64_t piece_bytes, int ksplit,
+                              int waves, uint32_t *sink, void *stream) {
+    return read_pieces(W, rows, row_bytes, piece_bytes, ksplit, waves, sink, stream);
 }
 
 extern "C" int mcqb_empty(int grid, int block, void *stream) {

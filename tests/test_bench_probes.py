@@ -23,7 +23,7 @@ def _bench():
 
 def test_bench_library_exports_header():
     names = re.findall(r"^int (mcqb_\w+)\(", open(HEADER).read(), re.M)
-    assert len(names) == 6
+    assert len(names) == 7
     lib = ctypes.CDLL(BENCH_SO)
     for n in names:
         assert hasattr(lib, n), n
@@ -44,6 +44,9 @@ def test_probe_argument_checks():
     assert lib.mcqb_read_tiles(v(256), 4096, 4096, 16, 1, 12, v(512), None) == 1   # waves
     assert lib.mcqb_read_tiles(v(256), 4096, 4096, 24, 1, 16, v(512), None) == 1   # N % tile
     assert lib.mcqb_read_tiles(v(256), 4096, 4096, 16, 129, 16, v(512), None) == 1  # ksplit > K/32
+    assert lib.mcqb_read_rows(v(256), 2048, 4096, 96, 1, 8, v(512), None) == 1    # row % piece
+    assert lib.mcqb_read_rows(v(256), 2048, 4096, 72, 1, 8, v(512), None) == 1    # piece % 16
+    assert lib.mcqb_read_rows(v(256), 2048, 4096, 128, 2049, 8, v(512), None) == 1  # ksplit > rows
     assert lib.mcqb_empty(0, 64, None) == 1
     assert lib.mcqb_empty(1, 2048, None) == 1
     assert lib.mcqb_measure_sclk(None, 10, None) == 1
@@ -64,6 +67,8 @@ def test_read_probes_leave_sink():
     assert lib.mcqb_read_probe(src.data_ptr(), src.numel() + 5, sink.data_ptr(), s) == 0
     for tc, ks, nw in ((16, 1, 16), (64, 4, 8), (256, 16, 4)):
         assert lib.mcqb_read_tiles(src.data_ptr(), 4096, 4096, tc, ks, nw, sink.data_ptr(), s) == 0
+    for pc, ks in ((64, 4), (128, 8)):
+        assert lib.mcqb_read_rows(src.data_ptr(), 2048, 4096, pc, ks, 8, sink.data_ptr(), s) == 0
     assert lib.mcqb_empty(256, 256, s) == 0
     torch.cuda.synchronize()
     assert sink.tolist() == [7, 7, 7, 7]
