@@ -156,68 +156,68 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
         }
         // The activations (the oldest loads) first.
         wait_vmcnt<NC>();
-            half8_t xq[GS_B];
-            float4_t negs[HOIST ? GS_B : 1];
-            const uint32_t xa = lds_addr(xs + 16 * g);
-    #pragma unroll
-            for (int u = 0; u < GS_B; ++u) {
-                uint4_t x;
-                if constexpr (GR == 1) x = bitcast<uint4_t>(*(const lds_half8 *)(lds_ptr(xa) + u * 64));
-                else x = xr[u];
-                const uint4_t v = {__builtin_amdgcn_perm(x[2], x[0], 0x05040100u),   // x0, x4
-                                   __builtin_amdgcn_perm(x[2], x[0], 0x07060302u),   // x1, x5
-                                   __builtin_amdgcn_perm(x[3], x[1], 0x05040100u),   // x2, x6
-                                   __builtin_amdgcn_perm(x[3], x[1], 0x07060302u)};  // x3, x7
-                xq[u] = bitcast<half8_t>(v);
-                if constexpr (HOIST) negs[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], negc, z, 0, 0, 0);
-            }
-            const uint32_t base = lds_addr(slot);
-            // GS_RP K rows (all groups of the span) at a time, each set as soon as the
-            // copies holding it have landed (the copies cover the item in row-major
-            // order, so rows up to RP (h + 1) - 1 need the first gs_need(ng, h)).
-            auto pair = [&](auto NGc, int h) {
-                constexpr int NG = decltype(NGc)::value;
-                constexpr uint32_t rowb = 288u * NG;
-                uint32_t q0[GS_RP][NG], q1[GS_RP][NG];
-                _Float16 dh[GS_RP][NG];
-    #pragma unroll
-                for (int v = 0; v < GS_RP; ++v)
-    #pragma unroll
-                    for (int grp = 0; grp < NG; ++grp) {
-                        const uint32_t ra = base + (GS_RP * h + v) * rowb + grp * 288;
-                        const lds_u32 *qp = (const lds_u32 *)lds_ptr(ra + qal);
-                        q0[v][grp] = qp[0];
-                        q1[v][grp] = qp[1];
-                        dh[v][grp] = bitcast<_Float16>(*(const lds_u16 *)lds_ptr(ra + doff));
-                    }
-                float4_t ns[GS_RP];
-    #pragma unroll
-                for (int v = 0; v < GS_RP; ++v) {
-                    if constexpr (HOIST) ns[v] = negs[GS_RP * h + v];
-                    else ns[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[GS_RP * h + v], negc, z, 0, 0, 0);
+        half8_t xq[GS_B];
+        float4_t negs[HOIST ? GS_B : 1];
+        const uint32_t xa = lds_addr(xs + 16 * g);
+#pragma unroll
+        for (int u = 0; u < GS_B; ++u) {
+            uint4_t x;
+            if constexpr (GR == 1) x = bitcast<uint4_t>(*(const lds_half8 *)(lds_ptr(xa) + u * 64));
+            else x = xr[u];
+            const uint4_t v = {__builtin_amdgcn_perm(x[2], x[0], 0x05040100u),   // x0, x4
+                               __builtin_amdgcn_perm(x[2], x[0], 0x07060302u),   // x1, x5
+                               __builtin_amdgcn_perm(x[3], x[1], 0x05040100u),   // x2, x6
+                               __builtin_amdgcn_perm(x[3], x[1], 0x07060302u)};  // x3, x7
+            xq[u] = bitcast<half8_t>(v);
+            if constexpr (HOIST) negs[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], negc, z, 0, 0, 0);
+        }
+        const uint32_t base = lds_addr(slot);
+        // GS_RP K rows (all groups of the span) at a time, each set as soon as the
+        // copies holding it have landed (the copies cover the item in row-major
+        // order, so rows up to RP (h + 1) - 1 need the first gs_need(ng, h)).
+        auto pair = [&](auto NGc, int h) {
+            constexpr int NG = decltype(NGc)::value;
+            constexpr uint32_t rowb = 288u * NG;
+            uint32_t q0[GS_RP][NG], q1[GS_RP][NG];
+            _Float16 dh[GS_RP][NG];
+#pragma unroll
+            for (int v = 0; v < GS_RP; ++v)
+#pragma unroll
+                for (int grp = 0; grp < NG; ++grp) {
+                    const uint32_t ra = base + (GS_RP * h + v) * rowb + grp * 288;
+                    const lds_u32 *qp = (const lds_u32 *)lds_ptr(ra + qal);
+                    q0[v][grp] = qp[0];
+                    q1[v][grp] = qp[1];
+                    dh[v][grp] = bitcast<_Float16>(*(const lds_u16 *)lds_ptr(ra + doff));
                 }
-                float4_t r[GS_RP][NG];
-    #pragma unroll
-                for (int v = 0; v < GS_RP; ++v)
-    #pragma unroll
-                    for (int grp = 0; grp < NG; ++grp) {
-                        const uint32_t w = __builtin_amdgcn_alignbit(q1[v][grp], q0[v][grp], qsh);
-                        const uint32_t w8 = __builtin_amdgcn_alignbit(q1[v][grp], q0[v][grp], qsh + 8);
-                        const uint4_t bq = {and_or(w, mlo, e1024), and_or(w, mhi, e64), and_or(w8, mlo, e1024),
-                                            and_or(w8, mhi, e64)};
-                        r[v][grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[GS_RP * h + v], bitcast<half8_t>(bq),
-                                                                           ns[v], 0, 0, 0);
-                    }
-    #pragma unroll
-                for (int v = 0; v < GS_RP; ++v)
-                    if (GS_RP * h + v < rows) {
-    #pragma unroll
-                        for (int grp = 0; grp < NG; ++grp)
-    #pragma unroll
-                            for (int i = 0; i < NA; ++i)
-                                acc[grp][i] += (float)dh[v][grp] * r[v][grp][i];
-                    }
-            };
+            float4_t ns[GS_RP];
+#pragma unroll
+            for (int v = 0; v < GS_RP; ++v) {
+                if constexpr (HOIST) ns[v] = negs[GS_RP * h + v];
+                else ns[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[GS_RP * h + v], negc, z, 0, 0, 0);
+            }
+            float4_t r[GS_RP][NG];
+#pragma unroll
+            for (int v = 0; v < GS_RP; ++v)
+#pragma unroll
+                for (int grp = 0; grp < NG; ++grp) {
+                    const uint32_t w = __builtin_amdgcn_alignbit(q1[v][grp], q0[v][grp], qsh);
+                    const uint32_t w8 = __builtin_amdgcn_alignbit(q1[v][grp], q0[v][grp], qsh + 8);
+                    const uint4_t bq = {and_or(w, mlo, e1024), and_or(w, mhi, e64), and_or(w8, mlo, e1024),
+                                        and_or(w8, mhi, e64)};
+                    r[v][grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[GS_RP * h + v], bitcast<half8_t>(bq),
+                                                                       ns[v], 0, 0, 0);
+                }
+#pragma unroll
+            for (int v = 0; v < GS_RP; ++v)
+                if (GS_RP * h + v < rows) {
+#pragma unroll
+                    for (int grp = 0; grp < NG; ++grp)
+#pragma unroll
+                        for (int i = 0; i < NA; ++i)
+                            acc[grp][i] += (float)dh[v][grp] * r[v][grp][i];
+                }
+        };
         constexpr int NH = GS_B / GS_RP;
         static_for<NH>([&](auto H) {
             constexpr int h = decltype(H)::value;
