@@ -43,6 +43,7 @@ hipError_t q4_gemm6_split_fallbacks(uint64_t *count, bool reset);
 hipError_t i4_gemv_split_fallbacks(uint64_t *count, bool reset);
 hipError_t i4_gemv1_split_fallbacks(uint64_t *count, bool reset);
 hipError_t i4_gemm6_split_fallbacks(uint64_t *count, bool reset);
+hipError_t q4_gemv_span_split_fallbacks(uint64_t *count, bool reset);
 hipError_t launch_q4_xact(const void *X, int x_dt, int64_t ldx, const uint8_t *W, void *Y,
                           int64_t ldy, int64_t M, int64_t K, int64_t N, hipStream_t s);
 bool gemv_dma_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t N);
@@ -353,7 +354,7 @@ int mcq4_split_fallback_count(uint64_t *count, int reset) {
     *count = 0;
     hipError_t (*const readers[])(uint64_t *, bool) = {
         mcq4::q4_gemvm_split_fallbacks, mcq4::q4_gemm6_split_fallbacks, mcq4::i4_gemv_split_fallbacks,
-        mcq4::i4_gemv1_split_fallbacks, mcq4::i4_gemm6_split_fallbacks};
+        mcq4::i4_gemv1_split_fallbacks, mcq4::i4_gemm6_split_fallbacks, mcq4::q4_gemv_span_split_fallbacks};
     for (auto rd : readers)
         if (int st = hip_status(rd(count, reset != 0), "split fallback counter")) return st;
     return MCQ4_OK;

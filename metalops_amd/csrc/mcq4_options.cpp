@@ -19,7 +19,7 @@ const char *const kNames[] = {
     "MCQ4_GEMM_PATH",       // sync | async | 6 | 7: force one prefill kernel
     "MCQ4_GEMM6_SPLIT",     // K splits of the prefill GEMM
     "MCQ4_GEMV_PATH",       // off: M == 1 through the batched decode kernels
-    "MCQ4_GEMV_SPAN",       // 0: M == 1, 9..16 at 4096 < N <= 16384 through the strip kernels
+    "MCQ4_GEMV_SPAN",       // 0: no span kernels (strip kernels instead); 1: the split form wherever it fits
     "MCQ4_GEMVM_SPLIT",     // 1 | 2 | 4 | 8: K splits of the batched decode GEMV
     "MCQ4_GEMVM_HOIST",     // 0: batched decode GEMV rebuilds -S per item even with one batch per wave
     "MCQ4_DECODE_PATH",     // direct: the register-load decode kernel

@@ -1,5 +1,6 @@
 // q4_0 GEMV for M == 1 and 9 <= M <= 16 rows at 4096 < N <= 16384 columns and
-// K <= 4096: one workgroup per CU owning a contiguous span of 16-column groups.
+// K <= 4096: one workgroup per CU owning a contiguous span of 16-column groups;
+// and, split along K, for 2 <= M <= 16 at N <= 4096 with long K.
 //
 // The strip kernels (q4_gemv.hip at M == 1, q4_gemvm.hip at M = 2..32) give each
 // workgroup tiles wg, wg + G, ... and copy 16-column items (288-byte pieces of each
@@ -31,6 +32,14 @@
 //   * Epilogue: each wave's partials per output row and column go to its own
 //     (drained) LDS slot; after one barrier they are summed in wave order and
 //     stored as fp16.
+//
+// Split form (SPLIT, 2 <= M <= 16 at N <= 4096, where the groups would give one
+// 288-byte strip per workgroup): workgroup (tile, split) owns 64 neighbouring
+// columns (1152-byte row pieces, the pattern a plain read serves ~20% faster than
+// strips) and one K range of up to 128 K blocks, the same one item per wave.  The
+// K splits of a tile share blockIdx.x and run on one XCD; their fp32 partials meet
+// in that XCD's L2 and the last to take the tile's ticket sums them in split
+// order (a split recorded on another XCD is recomputed from the inputs).
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
@@ -38,6 +47,8 @@
 #include "q4_common.h"
 
 namespace mcq4 {
+
+MCQ4_SPLIT_FALLBACK_COUNTER(q4_gemv_span_split_fallbacks)
 
 constexpr int GS_GRID = 256;                 // workgroups: one per CU
 constexpr int GS_NW = 16;                    // waves per workgroup
@@ -74,13 +85,20 @@ struct GemvSpanArgs {
     int64_t ldx, ldy;                        // row strides of X and Y (elements)
     int M, nb, groups;                       // rows; K blocks; 16-column groups of N
     uint32_t grow;                           // bytes per K row (18 N)
+    // Split form: 64-column tiles (blockIdx.x, XCD-renumbered, grid.x a multiple of
+    // 8) and K splits (blockIdx.y) of bps K blocks each.
+    int S = 1, bps = 0;
+    float *part = nullptr;                   // [S][M][N] fp32 partials
+    uint64_t *tickets = nullptr;             // 64-bit tickets [8][4096] by blockIdx.x mod 8
+    uint32_t foreign = 0;                    // splits treated as run on another XCD (test switch)
 };
 
-template <int GR>
+template <int GR, bool SPLIT>
 __global__ void __launch_bounds__(GS_NW * 64)
 q4_gemv_span_kernel(GemvSpanArgs a) {
-    static_assert(GR == 1 || GR == 16, "row groups");
-    constexpr int NA = GR == 1 ? 1 : 4;          // accumulators per group
+    static_assert(GR == 1 || GR == 4 || GR == 8 || GR == 16, "row groups");
+    constexpr int NA = GR <= 4 ? 1 : GR / 4;     // accumulators per group
+    constexpr int IS = GR == 1 ? 0 : 16 / GR;    // accumulator i is MFMA result element i * IS
     constexpr bool HOIST = GR == 1;              // -S for all 8 rows up front (else per row pair)
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int nb = a.nb, ngt = a.groups, M = a.M;
@@ -98,14 +116,28 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
     uint8_t *xs = smem + wave * (GS_B * 64);
     uint8_t *slot = smem + XS + wave * GS_SLOT;
 
-    // XCD renumbering of the GS_GRID workgroups; span bounds by a shift (the grid
-    // is fixed, groups <= 1024, so wg * groups fits 32 bits).
-    const int wg = ((int)blockIdx.x & 7) * (GS_GRID / 8) + ((int)blockIdx.x >> 3);
-    const int g0 = (wg * ngt) >> 8, g1 = ((wg + 1) * ngt) >> 8;
-    static_assert(GS_GRID == 256, "span bounds by a shift of 8");
-    const int ng = g1 - g0;                                        // 1..GS_NGMAX
-    const int row0 = wave * GS_B;
-    const int rows = max(0, min(GS_B, nb - row0));                 // 0: no item for this wave
+    int g0, ng, kb0 = 0, kbe = nb;
+    if constexpr (SPLIT) {
+        // Tile t (64 columns) of the XCD-renumbered grid.x; split blockIdx.y owns
+        // K blocks [sp bps, (sp + 1) bps).  Every split of a tile has the same
+        // blockIdx.x, so the same linear id mod 8 (grid.x a multiple of 8): one XCD.
+        const int gx = (int)gridDim.x;
+        const int t = ((int)blockIdx.x & 7) * (gx >> 3) + ((int)blockIdx.x >> 3);
+        if (t >= (ngt >> 2)) return;                               // grid padding
+        g0 = 4 * t;
+        ng = 4;
+        kb0 = (int)blockIdx.y * a.bps;
+        kbe = min(kb0 + a.bps, nb);
+    } else {
+        // XCD renumbering of the GS_GRID workgroups; span bounds by a shift (the
+        // grid is fixed, groups <= 1024, so wg * groups fits 32 bits).
+        const int wg = ((int)blockIdx.x & 7) * (GS_GRID / 8) + ((int)blockIdx.x >> 3);
+        g0 = (wg * ngt) >> 8;
+        ng = (((wg + 1) * ngt) >> 8) - g0;                         // 1..GS_NGMAX
+        static_assert(GS_GRID == 256, "span bounds by a shift of 8");
+    }
+    const int row0 = kb0 + wave * GS_B;
+    const int rows = max(0, min(GS_B, kbe - row0));                // 0: no item for this wave
     const uint8_t *wb = W + (int64_t)g0 * 288 + (int64_t)row0 * grow;
 
     const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
@@ -138,9 +170,9 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
                                                  (__attribute__((address_space(3))) void *)xs, 16, 0, 0);
             }
         } else {
-            // Lane (c, g): activation row min(c, M - 1), elements 8g..8g+7 of each K
-            // block of the batch (blocks past K clamp to the last one).
-            const uint8_t *xrow = (const uint8_t *)X + (int64_t)min(c, M - 1) * ldx * 2 + 16 * g;
+            // Lane (c, g): activation row min(c / (16 / GR), M - 1), elements 8g..8g+7
+            // of each K block of the batch (blocks past K clamp to the last one).
+            const uint8_t *xrow = (const uint8_t *)X + (int64_t)min(c / (16 / GR), M - 1) * ldx * 2 + 16 * g;
 #pragma unroll
             for (int u = 0; u < GS_B; ++u) xr[u] = *(const uint4_t *)(xrow + (int64_t)min(row0 + u, nb - 1) * 64);
         }
@@ -215,7 +247,7 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
                     for (int grp = 0; grp < NG; ++grp)
 #pragma unroll
                         for (int i = 0; i < NA; ++i)
-                            acc[grp][i] += (float)dh[v][grp] * r[v][grp][i];
+                            acc[grp][i] += (float)dh[v][grp] * r[v][grp][i * IS];
                 }
         };
         constexpr int NH = GS_B / GS_RP;
@@ -227,34 +259,78 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
         });
     };
     if (rows > 0) {
-        switch (ng) {
-            case 1: item(std::integral_constant<int, 1>{}); break;
-            case 2: item(std::integral_constant<int, 2>{}); break;
-            case 3: item(std::integral_constant<int, 3>{}); break;
-            default: item(std::integral_constant<int, GS_NGMAX>{}); break;
+        if constexpr (SPLIT) {
+            item(std::integral_constant<int, 4>{});
+        } else {
+            switch (ng) {
+                case 1: item(std::integral_constant<int, 1>{}); break;
+                case 2: item(std::integral_constant<int, 2>{}); break;
+                case 3: item(std::integral_constant<int, 3>{}); break;
+                default: item(std::integral_constant<int, GS_NGMAX>{}); break;
+            }
         }
         // Every LDS read of the slot has returned before it holds the partials.
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     // Partials into this wave's slot: [output row][64 columns] floats.  Accumulator
-    // i of lane (c, g) is output row 4g + i (row 0 for every lane at M == 1).
+    // i of lane (c, g) is output row g GR/4 + i (row 0 for every lane at M == 1).
     float *mine = (float *)slot;
     if (GR > 1 || lane < 16) {
 #pragma unroll
         for (int i = 0; i < NA; ++i)
 #pragma unroll
             for (int grp = 0; grp < GS_NGMAX; ++grp)
-                mine[(GR == 1 ? 0 : 4 * g + i) * 64 + grp * 16 + c] = acc[grp][i];
+                mine[(GR == 1 ? 0 : g * (GR / 4) + i) * 64 + grp * 16 + c] = acc[grp][i];
     }
     lds_barrier();
     // Thread (row, col) = (tid / 64, tid % 64): 16 rows x 64 columns = the workgroup.
     const int row = tid >> 6, col = tid & 63;
-    if (col < 16 * ng && row < (GR == 1 ? 1 : M)) {
+    const bool live = col < 16 * ng && row < (GR == 1 ? 1 : M);
+    const int n = 16 * g0 + col;
+    float s = 0.f;
+    if (live) {
         const float *p = (const float *)(smem + XS) + row * 64 + col;
-        float s = 0.f;
 #pragma unroll
         for (int w = 0; w < GS_NW; ++w) s += p[w * (GS_SLOT / 4)];
-        Y[(int64_t)row * ldy + 16 * g0 + col] = (_Float16)s;
+        if constexpr (!SPLIT) Y[(int64_t)row * ldy + n] = (_Float16)s;
+    }
+    if constexpr (SPLIT) {
+        // This split's partial stays in the XCD's L2 (plain stores); once it is
+        // stored, one lane takes the tile's ticket and the workgroup that draws
+        // the last sums the S partials in split order -- its own from registers,
+        // the others through the L2, and any split that ran on another XCD
+        // (recorded in the ticket) recomputed from the inputs.
+        const int N = ngt * 16, sp = (int)blockIdx.y, S = a.S;
+        if (live) a.part[((int64_t)sp * M + row) * N + n] = s;
+        wait_vmcnt<0>();
+        __syncthreads();
+        uint32_t *last_flag = (uint32_t *)smem;                    // the slots are idle from here
+        uint64_t *cnt = a.tickets + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
+        if (tid == 0) {
+            const uint32_t xcc = xcc_id();
+            const uint64_t inc = xcd_ticket_inc(xcc, sp);
+            const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const uint32_t local = xcd_ticket_local_mask(prev + inc, xcc, S) & ~a.foreign;
+            *last_flag = (prev & 0xFF) != (uint64_t)(S - 1) ? 0u : 0x10000u | local;
+            if ((prev & 0xFF) == (uint64_t)(S - 1)) {
+                // Every split has drawn: the slot is free for the next launch.
+                __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (local != (1u << S) - 1) note_split_fallback();
+            }
+        }
+        __syncthreads();
+        const uint32_t lf = *last_flag;
+        if (!lf || !live) return;
+        const uint32_t local = lf & 0xFFFF;
+        float tot = 0.f;
+        for (int q = 0; q < S; ++q) {
+            float pv;
+            if (q == sp && ((local >> q) & 1)) pv = s;
+            else if ((local >> q) & 1) pv = load_l2_f32(a.part, (int)((((int64_t)q * M + row) * N + n) * 4));
+            else pv = q4_dot_range(X + (int64_t)row * ldx, W, N, n, min(q * a.bps, nb), min((q + 1) * a.bps, nb));
+            tot += pv;
+        }
+        Y[(int64_t)row * ldy + n] = (_Float16)tot;
     }
 }
 
@@ -270,8 +346,8 @@ bool gemv_span_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64
            (M == 1 || ldx % 8 == 0) && N * 18 * 8 < ((int64_t)1 << 31);
 }
 
-template <int GR>
-static hipError_t launch_span_gr(const GemvSpanArgs &a, hipStream_t s) {
+template <int GR, bool SPLIT>
+static hipError_t launch_span_gr(const GemvSpanArgs &a, dim3 grid, hipStream_t s) {
     const size_t lds = (GR == 1 ? GS_XS : 0) + (size_t)GS_NW * GS_SLOT + GS_PAD;
     static std::atomic<uint64_t> done{0};
     int dev = 0;
@@ -279,12 +355,12 @@ static hipError_t launch_span_gr(const GemvSpanArgs &a, hipStream_t s) {
     if (e != hipSuccess) return e;
     const uint64_t bit = 1ull << (dev & 63);
     if (!(done.load(std::memory_order_acquire) & bit)) {
-        e = hipFuncSetAttribute((const void *)q4_gemv_span_kernel<GR>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                160 * 1024);
+        e = hipFuncSetAttribute((const void *)q4_gemv_span_kernel<GR, SPLIT>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    hipLaunchKernelGGL(q4_gemv_span_kernel<GR>, dim3(GS_GRID), dim3(GS_NW * 64), lds, s, a);
+    hipLaunchKernelGGL((q4_gemv_span_kernel<GR, SPLIT>), grid, dim3(GS_NW * 64), lds, s, a);
     return hipGetLastError();
 }
 
@@ -297,7 +373,72 @@ hipError_t launch_gemv_span(const _Float16 *X, int64_t ldx, const uint8_t *W, _F
     a.nb = K / QK;
     a.groups = N / 16;
     a.grow = (uint32_t)N * BLOCK_BYTES;
-    return M == 1 ? launch_span_gr<1>(a, s) : launch_span_gr<16>(a, s);
+    const dim3 grid(GS_GRID);
+    return M == 1 ? launch_span_gr<1, false>(a, grid, s) : launch_span_gr<16, false>(a, grid, s);
+}
+
+// Split form, 2 <= M <= 16 at N <= 4096: 64-column tiles (N % 64 == 0) and S K
+// splits, S the largest power of two (<= 8) with tiles x S <= 256, then bps = K
+// blocks per split rounded up to whole batches of 8 (<= 128: one item per wave)
+// and S recounted from it.
+struct SpanSplitPlan {
+    int S, bps, gx;
+};
+static SpanSplitPlan span_split_plan(int64_t K, int64_t N) {
+    const int64_t ntiles = N / 64, nb = K / QK;
+    int S = 1;
+    while (S < 8 && ntiles * S * 2 <= 256) S *= 2;
+    int bps = (int)((nb + S - 1) / S);
+    bps = (bps + GS_B - 1) / GS_B * GS_B;
+    S = (int)((nb + bps - 1) / bps);
+    return {S, bps, (int)((ntiles + 7) / 8 * 8)};
+}
+
+// True when the split form takes the whole of W: 2 <= M <= 16, N % 64 == 0 with
+// N <= 4096, at least two K splits of at most 128 K blocks each, 16-byte aligned
+// weights and activation rows -- and, unless MCQ4_GEMV_SPAN=1 forces it, at least
+// 64 K blocks (8 busy waves) per split.  Shorter splits leave most of a workgroup
+// idle and pay an exchange the strip kernel does not need there (M = 4 at
+// 4096 x 4096: 6.8 against 5.0 us); at K = 14336, N = 4096 the split form is 5-8%
+// faster at M = 2..16.  It sums the splits through the XCD's L2 only, so
+// MCQ4_XCD_LOCAL=0 (and a forced MCQ4_GEMVM_SPLIT) leave these shapes to the strip
+// kernel.
+bool gemv_span_split_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N) {
+    if (opt_is("MCQ4_GEMV_SPAN", '0') || opt_is("MCQ4_XCD_LOCAL", '0') || opt("MCQ4_GEMVM_SPLIT")) return false;
+    if (M < 2 || M > 16 || N % 64 || N < 64 || N > 4096 || K < QK || ldx % 8 || ((uintptr_t)W % 16) ||
+        ((uintptr_t)X % 16))
+        return false;
+    const SpanSplitPlan p = span_split_plan(K, N);
+    if (p.S < 2 || p.bps > GS_NW * GS_B) return false;
+    return opt_is("MCQ4_GEMV_SPAN", '1') || K / QK >= (int64_t)64 * p.S;
+}
+
+size_t gemv_span_split_workspace_bytes(int64_t M, int64_t K, int64_t N) {
+    if (M < 2 || M > 16 || N % 64 || N < 64 || N > 4096 || K < QK) return 0;
+    const SpanSplitPlan p = span_split_plan(K, N);
+    return COUNTER_BYTES + (size_t)p.S * M * N * sizeof(float);
+}
+
+hipError_t launch_gemv_span_split(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y, int64_t ldy,
+                                  int M, int K, int N, void *ws, hipStream_t s) {
+    if (!ws) return hipErrorInvalidValue;
+    const SpanSplitPlan p = span_split_plan(K, N);
+    GemvSpanArgs a;
+    a.X = X; a.W = W; a.Y = Y;
+    a.ldx = ldx; a.ldy = ldy;
+    a.M = M;
+    a.nb = K / QK;
+    a.groups = N / 16;
+    a.grow = (uint32_t)N * BLOCK_BYTES;
+    a.S = p.S;
+    a.bps = p.bps;
+    a.tickets = (uint64_t *)ws;
+    a.part = (float *)((char *)ws + COUNTER_BYTES);
+    a.foreign = split_foreign_mask();
+    const dim3 grid(p.gx, p.S);
+    if (M <= 4) return launch_span_gr<4, true>(a, grid, s);
+    if (M <= 8) return launch_span_gr<8, true>(a, grid, s);
+    return launch_span_gr<16, true>(a, grid, s);
 }
 
 }  // namespace mcq4

@@ -451,16 +451,22 @@ static GmPlan gemvm_plan(int64_t M, int64_t K, int64_t N) {
     return {waves, tpw, grid, (nbt + bps - 1) / bps, bps};
 }
 
+size_t gemv_span_split_workspace_bytes(int64_t M, int64_t K, int64_t N);
+
 size_t gemvm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M < 2 || M > 32 || N < 16 || K < QK) return 0;
     const GmPlan p = gemvm_plan(M, K, N);
     // Partials follow the workspace's counter area, which other kernels rely on staying zero.
-    return p.S > 1 ? COUNTER_BYTES + (size_t)p.S * M * (N / 16) * 16 * sizeof(float) : 0;
+    const size_t own = p.S > 1 ? COUNTER_BYTES + (size_t)p.S * M * (N / 16) * 16 * sizeof(float) : 0;
+    return std::max(own, gemv_span_split_workspace_bytes(M, K, N));
 }
 
 bool gemv_span_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N);
 hipError_t launch_gemv_span(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y, int64_t ldy, int M,
                             int K, int N, hipStream_t s);
+bool gemv_span_split_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N);
+hipError_t launch_gemv_span_split(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y, int64_t ldy,
+                                  int M, int K, int N, void *ws, hipStream_t s);
 
 hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, void *ws, int *n_done, hipStream_t s) {
@@ -469,6 +475,12 @@ hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
     if (gemv_span_supported(X, ldx, W, M, K, N)) {
         *n_done = N;
         return launch_gemv_span(X, ldx, W, Y, ldy, M, K, N, s);
+    }
+    // 2 <= M <= 16 at N <= 4096: 64-column spans over K splits, summed through the
+    // XCD's L2 (q4_gemv_span.hip).
+    if (ws && gemv_span_split_supported(X, ldx, W, M, K, N)) {
+        *n_done = N;
+        return launch_gemv_span_split(X, ldx, W, Y, ldy, M, K, N, ws, s);
     }
     GemvMArgs a;
     a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;

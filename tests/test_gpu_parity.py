@@ -251,6 +251,8 @@ PATHS = {
     "gemm7_split2": {"MCQ4_GEMM_PATH": "7", "MCQ4_GEMM6_SPLIT": "2"},
     "gemm7_split3": {"MCQ4_GEMM_PATH": "7", "MCQ4_GEMM6_SPLIT": "3"},
     "gemv_span": {},
+    "gemv_span_split": {"MCQ4_GEMV_SPAN": "1"},
+    "gemv_span_split_off": {"MCQ4_GEMV_SPAN": "0"},
     "gemv_span_off": {"MCQ4_GEMV_SPAN": "0"},
 }
 PATH_SHAPES = {
@@ -270,6 +272,14 @@ PATH_SHAPES = {
                   (2, 352, 8208), (3, 4096, 14336), (4, 4096, 14336), (5, 32, 4112), (8, 2080, 16384),
                   (9, 4096, 12288), (12, 96, 16368), (16, 4096, 14336), (16, 4064, 6144)],
     "gemv_span_off": [(1, 4096, 12288), (1, 352, 8208), (4, 4096, 14336), (16, 352, 8208)],
+    # 64-column spans over K splits (2 <= M <= 16, N % 64 == 0, N <= 4096; forced,
+    # since by default only splits of 64+ K blocks take it): 4, 8, 16 distinct rows
+    # per MFMA; 2 to 8 splits; a last split shorter than the others, waves without
+    # an item, partial last batches, grid padding.
+    "gemv_span_split": [(2, 14336, 4096), (4, 14336, 4096), (8, 14336, 4096), (16, 14336, 4096),
+                        (3, 11008, 4096), (7, 4096, 4096), (12, 4096, 2048), (16, 16384, 4096),
+                        (5, 352, 1024), (9, 2080, 2048), (13, 1024, 64), (6, 4128, 3008)],
+    "gemv_span_split_off": [(4, 14336, 4096), (16, 4096, 4096)],
     "decode_lds_m1": [(1, 352, 264), (1, 4096, 1032)],
     "gemvm": [(2, 32, 16), (3, 352, 264), (4, 1024, 4104), (5, 11008, 512), (8, 4096, 14336),
               (11, 2048, 1040), (16, 14336, 4096), (16, 352, 8200)],
