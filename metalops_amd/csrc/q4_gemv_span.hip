@@ -1,5 +1,5 @@
-// q4_0 GEMV for M == 1 and 9 <= M <= 16 rows at 4096 < N <= 16384 columns and
-// K <= 4096: one workgroup per CU owning a contiguous span of 16-column groups;
+// q4_0 GEMV for 1 <= M <= 16 rows at 4096 < N <= 16384 columns and K <= 4096:
+// one workgroup per CU owning a contiguous span of 16-column groups;
 // and, split along K, for 2 <= M <= 16 at N <= 4096 with long K.
 //
 // The strip kernels (q4_gemv.hip at M == 1, q4_gemvm.hip at M = 2..32) give each
@@ -20,11 +20,12 @@
 //     hold the next two rows before their math, so the math of the first rows
 //     overlaps the rest of the item's copies.
 //   * Activations, issued before the item: at M == 1 (GR = 1) the batch's row is
-//     copied into LDS ahead of the item; at M >= 9 (GR = 16) lane (c, g) loads
-//     activation row min(c, M - 1) straight into registers as its MFMA A row, so
-//     accumulator i of the lane is output row 4g + i (four fp32 updates per K-block
-//     row).  At M = 2..8 the strip kernel (q4_gemvm.hip) measured as fast or
-//     faster (M = 4: 10.1 against 10.3-10.5 us at 4096 x 14336), so it keeps them.
+//     copied into LDS ahead of the item; at M >= 2 each lane loads its MFMA A row
+//     straight into registers.  With GR distinct rows per 16-row A operand (GR = 4
+//     for M <= 4, 8 for M <= 8, else 16), A row r holds activation row
+//     min(r / (16 / GR), M - 1), so accumulator i of lane (c, g) is output row
+//     (4g + i (16 / GR)) GR / 16: one fp32 update per K-block row at M <= 4, two
+//     at M <= 8, four above.
 //   * Per 16-column group of the span: LDS reads of two rows first, then four
 //     v_and_or_b32 per row into fp16 1024 + q (low nibbles) and 64 + q (high
 //     nibbles in place), mfma(x', B, -S) with x' = [x0, x4, x1, x5, x2, x6, x3, x7]
@@ -334,14 +335,14 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
     }
 }
 
-// True when the span kernel takes the whole of W for M rows: M == 1 or 9 <= M <= 16,
+// True when the span kernel takes the whole of W for M rows: 1 <= M <= 16,
 // N % 16 == 0 with 256 < N/16 <= 1024 groups (one span of 1..4 groups per
 // workgroup on 256 workgroups), at most 16 batches of 8 K blocks (K <= 4096, one
 // item per wave), 16-byte aligned weights and activation rows.
 bool gemv_span_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N) {
     if (opt_is("MCQ4_GEMV_SPAN", '0')) return false;
     const int64_t groups = N / 16, nb = K / QK;
-    return (M == 1 || (M >= 9 && M <= 16)) && N % 16 == 0 && groups > GS_GRID && groups <= GS_GRID * GS_NGMAX && nb >= 1 &&
+    return M >= 1 && M <= 16 && N % 16 == 0 && groups > GS_GRID && groups <= GS_GRID * GS_NGMAX && nb >= 1 &&
            nb <= GS_NW * GS_B && ((uintptr_t)W % 16) == 0 && ((uintptr_t)X % 16) == 0 &&
            (M == 1 || ldx % 8 == 0) && N * 18 * 8 < ((int64_t)1 << 31);
 }
@@ -374,7 +375,10 @@ hipError_t launch_gemv_span(const _Float16 *X, int64_t ldx, const uint8_t *W, _F
     a.groups = N / 16;
     a.grow = (uint32_t)N * BLOCK_BYTES;
     const dim3 grid(GS_GRID);
-    return M == 1 ? launch_span_gr<1, false>(a, grid, s) : launch_span_gr<16, false>(a, grid, s);
+    if (M == 1) return launch_span_gr<1, false>(a, grid, s);
+    if (M <= 4) return launch_span_gr<4, false>(a, grid, s);
+    if (M <= 8) return launch_span_gr<8, false>(a, grid, s);
+    return launch_span_gr<16, false>(a, grid, s);
 }
 
 // Split form, 2 <= M <= 16 at N <= 4096: 64-column tiles (N % 64 == 0) and S K

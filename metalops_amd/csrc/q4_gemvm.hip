@@ -470,8 +470,8 @@ hipError_t launch_gemv_span_split(const _Float16 *X, int64_t ldx, const uint8_t 
 
 hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, void *ws, int *n_done, hipStream_t s) {
-    // 9 <= M <= 16 with 4096 < N <= 16384 at K <= 4096: contiguous spans of
-    // 16-column groups per workgroup (q4_gemv_span.hip), no K split and no workspace.
+    // M <= 16 with 4096 < N <= 16384 at K <= 4096: contiguous spans of 16-column
+    // groups per workgroup (q4_gemv_span.hip), no K split and no workspace.
     if (gemv_span_supported(X, ldx, W, M, K, N)) {
         *n_done = N;
         return launch_gemv_span(X, ldx, W, Y, ldy, M, K, N, s);

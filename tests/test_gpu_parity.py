@@ -262,13 +262,12 @@ PATH_SHAPES = {
     # (a last item of one row) and waves without batches.
     "gemv_dma_wide": [(1, 32, 65536), (1, 352, 65536), (1, 2080, 65600), (1, 4096, 70016)],
 
-    # Contiguous spans of 16-column groups (M = 1 and 9..16, 4096 < N <= 16384,
-    # K <= 4096; M = 2..8 of the same shapes take the strip kernel): one to four
-    # groups per workgroup, one K block, a partial last batch, the
+    # Contiguous spans of 16-column groups (M <= 16, 4096 < N <= 16384, K <= 4096):
+    # one to four groups per workgroup, one K block, a partial last batch, the
     # largest K and N, ragged group counts (257, 513, 767 groups).
     "gemv_span": [(1, 32, 4112), (1, 352, 8208), (1, 4096, 12288), (1, 4064, 12272), (1, 2080, 6144),
                   (1, 96, 4128), (1, 4096, 8192), (1, 4096, 16384), (1, 1024, 14336),
-                  # M = 9..16 (16 rows per MFMA A operand); M = 2..8 pass to the strip kernel.
+                  # M = 2..16: 4, 8 and 16 distinct rows per MFMA A operand.
                   (2, 352, 8208), (3, 4096, 14336), (4, 4096, 14336), (5, 32, 4112), (8, 2080, 16384),
                   (9, 4096, 12288), (12, 96, 16368), (16, 4096, 14336), (16, 4064, 6144)],
     "gemv_span_off": [(1, 4096, 12288), (1, 352, 8208), (4, 4096, 14336), (16, 352, 8208)],
@@ -379,8 +378,7 @@ def _random_cases(n, seed):
     return cases
 
 
-# The span kernel's region (M = 1 and 9..16, 4096 < N <= 16384, K <= 4096) and the
-# strip kernel's shapes next to it (M = 3, 6) with row strides
+# The span kernel's region (M <= 16, 4096 < N <= 16384, K <= 4096) with row strides
 # past K, which the random draw above never reaches.
 SPAN_STRIDE_CASES = [(1, 2048, 8208, 8), (3, 4096, 8192, 40), (6, 352, 16384, 40), (16, 1024, 12288, 8),
                      (11, 4096, 14336, 40)]
