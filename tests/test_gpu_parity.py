@@ -464,3 +464,31 @@ def test_matmul_grouped_other_cases(dev):
     # N == 0: empty outputs, as for one weight.
     empty = [torch.zeros((K // 32, 0, 18), dtype=torch.uint8, device=dev) for _ in range(2)]
     assert [tuple(y.shape) for y in mo.matmul_ggml_q4_0_grouped(_acts(1, K, seed=5).to(dev), empty)] == [(1, 0)] * 2
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 8192), (3, 2048, 8208), (6, 1024, 12288), (12, 4096, 16384),
+                                   (4, 16384, 1024), (16, 8192, 4096), (1, 4096, 4096), (5, 4096, 4096),
+                                   (24, 2048, 1024), (40, 1024, 2048), (300, 2048, 512)])
+def test_matmul_capi_row_strides(dev, M, K, N):
+    """The C entry point with row strides past K and N on both sides (ldx = K + 40,
+    ldy = N + 24) across the decode and prefill kernels: outputs match the oracle
+    and the padding columns of Y keep what was there."""
+    from metalops_amd import _lib
+    print(f"capi strided M={M} K={K} N={N}", flush=True)
+    W = _weights(K, N, seed=M + K + 3 * N, outliers=True)
+    blocks = ref.quantize_llama_rule(W.numpy())
+    Xw = _acts(M, K + 40, seed=M + 5)
+    Xd = Xw.to(dev)
+    bd = torch.from_numpy(blocks).to(dev)
+    ldy = N + 24
+    Y = torch.full((M, ldy), 7.0, dtype=torch.float16, device=dev)
+    need = _lib.lib.mcq4_matmul_workspace_bytes(M, K, N)
+    ws = torch.zeros(max(need, 16), dtype=torch.uint8, device=dev)
+    st = _lib.lib.mcq4_matmul_q4_0_f16(Xd.data_ptr(), K + 40, bd.data_ptr(), Y.data_ptr(), ldy, M, K, N,
+                                       ws.data_ptr() if need else None, need,
+                                       torch.cuda.current_stream().cuda_stream)
+    assert st == 0, _lib.lib.mcq4_last_error()
+    torch.cuda.synchronize()
+    Yc = Y.float().cpu().numpy()
+    assert (Yc[:, N:] == 7.0).all()
+    _check_rows(Yc[:, :N], ref.matmul_f32(Xw[:, :K].contiguous().numpy(), blocks))
