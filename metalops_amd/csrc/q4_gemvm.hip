@@ -1,5 +1,8 @@
-// Small-batch (2 <= M <= 16) q4_0 GEMV/GEMM on gfx950: the M = 1 kernel's
-// structure (q4_gemv.hip) with a 16-row MFMA A operand.
+// Small-batch (2 <= M <= 32) q4_0 GEMV/GEMM on gfx950: the M = 1 kernel's
+// structure (q4_gemv.hip) with a 16-row MFMA A operand.  launch_gemvm first hands
+// M <= 16 to the span kernels of q4_gemv_span.hip where they fit (4096 < N <=
+// 16384 at K <= 4096; N <= 4096 with long K, split along K) and runs this strip
+// kernel for the rest.
 //
 //   * Column tile = 16 columns; item = one tile's batch of 8 K blocks (2304 bytes
 //     of strip rows), copied with three global_load_lds_dwordx4 into a 2-slot
