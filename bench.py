@@ -91,12 +91,13 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     p.add_argument("--part", choices=["all", "decode", "prefill", "configs", "copy", "int4-decode",
-                                      "int4-prefill", "probes"], default="all",
+                                      "int4-prefill", "probes", "prefill-splits"], default="all",
                    help="run one part only (for profiler passes); 'copy' runs a plain 256 MiB "
                         "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters; "
                         "'probes' runs the machine probes of libmcq4_bench.so (launch floor, "
                         "read patterns of the q4_0 layout, atomic and store-to-load latency, "
-                        "shader clock)")
+                        "shader clock); 'prefill-splits' times the few-tile prefill shapes "
+                        "(M = 512, N = 4096) over forced kernels and K splits")
     return p.parse_args()
 
 
@@ -183,6 +184,37 @@ def shape_bench(mo, torch, dev, M, K, N, pool_bytes=1 << 30, reps=20, outliers=F
     del ws
     torch.cuda.empty_cache()
     return t, copies, t_read
+
+
+def prefill_split_sweep(mo, torch, dev):
+    """The few-tile prefill shapes (M = 512, N = 4096: 32 tiles of 256 x 256, 64 of
+    128 x 256) under each prefill kernel forced with 1, 2, 4 and 8 K splits, and the
+    default plan: TFLOP/s per point, graph replays over rotated weight copies."""
+    from metalops_amd import _lib
+    keys = ("MCQ4_GEMM_PATH", "MCQ4_GEMM6_SPLIT")
+    saved = {k: os.environ.get(k) for k in keys}
+    out = []
+    try:
+        for M, K, N in ((512, 11008, 4096), (512, 4096, 4096)):
+            runs = [("default", None, None)] + [(f"gemm{p}", p, sp) for p in ("6", "7") for sp in (1, 2, 4, 8)]
+            for name, path, sp in runs:
+                for k in keys:
+                    os.environ.pop(k, None)
+                if path:
+                    os.environ["MCQ4_GEMM_PATH"] = path
+                    os.environ["MCQ4_GEMM6_SPLIT"] = str(sp)
+                _lib.reload_options()
+                t, _, _ = shape_bench(mo, torch, dev, M, K, N, reps=5)
+                out.append({"M": M, "K": K, "N": N, "kernel": name, "splits": sp, "us": round(t * 1e6, 2),
+                            "TFLOP/s": round(2 * M * N * K / t / 1e12, 1)})
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+        _lib.reload_options()
+    return out
 
 
 def config_points(mo, torch, dev):
@@ -795,6 +827,8 @@ def run_part(mo, torch, dev, args):
     elif args.part == "int4-prefill":
         print(json.dumps({"part": "int4-prefill", "configs": i4_prefill_bench(mo, torch, dev)}),
               flush=True)
+    elif args.part == "prefill-splits":
+        print(json.dumps({"part": "prefill-splits", "points": prefill_split_sweep(mo, torch, dev)}), flush=True)
     else:
         print(json.dumps({"part": "prefill", "configs": prefill_bench(mo, torch, dev)}), flush=True)
 
