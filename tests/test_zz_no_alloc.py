@@ -35,13 +35,14 @@ def _run_pair(dev, M, K, N, seed):
 
 
 @pytest.mark.parametrize("first,second", [
-    ((200, 11008, 1024), (16, 14336, 4096)),      # prefill split-K (16 MiB) then decode split-K
+    ((200, 11008, 1024), (16, 14336, 4096)),      # prefill split-K (16 MiB) then decode split-K (span split form)
     ((16, 14336, 4096), (8, 4096, 1040)),         # decode split-K then a smaller decode
     ((128, 11008, 1024), (130, 1024, 384)),       # prefill split-K then a small prefill
 ])
 def test_noalloc_matches_workspace_entry(dev, monkeypatch, first, second):
     from metalops_amd import _lib
-    for k in ("MCQ4_GEMVM_SPLIT", "MCQ4_GEMM6_SPLIT", "MCQ4_GEMM_PATH", "MCQ4_XCD_LOCAL", "MCQ4_SPLIT_FOREIGN"):
+    for k in ("MCQ4_GEMVM_SPLIT", "MCQ4_GEMM6_SPLIT", "MCQ4_GEMM_PATH", "MCQ4_XCD_LOCAL", "MCQ4_SPLIT_FOREIGN",
+              "MCQ4_GEMV_SPAN"):
         monkeypatch.delenv(k, raising=False)
     print(f"noalloc {first} then {second}", flush=True)
     assert _run_pair(dev, *first, seed=1) > 0        # the first call uses the scratch workspace
