@@ -331,13 +331,16 @@ def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
 
 
 @pytest.mark.parametrize("M,K,N,split", [(2048, 14336, 4096, "gemm2"), (300, 4096, 640, "gemm2"),
-                                         (1000, 2048, 1280, "gemm2"), (16, 14336, 4096, "gemvm2"),
+                                         (1000, 2048, 1280, "gemm2"), (512, 11008, 4096, "gemm4"),
+                                         (300, 4096, 640, "gemm3"), (384, 4096, 4096, "gemm4"),
+                                         (16, 14336, 4096, "gemvm2"),
                                          (9, 4096, 1040, "gemvm2"), (12, 11008, 8200, "gemvm4"),
                                          (16, 2048, 1032, "gemvm8")])
 def test_split_exchange_matches_reduce(dev, monkeypatch, M, K, N, split):
     """K split over workgroups: the in-kernel XCD-local sum (default) and the
     reduction kernel add the same partials in the same order (two splits of the
-    GEMM: p0 + p1, which commutes), so the outputs are identical bits."""
+    GEMM: p0 + p1, which commutes; three or four splits go to the reduction
+    kernel either way), so the outputs are identical bits."""
     print(f"split exchange {split} M={M} K={K} N={N}", flush=True)
     for k in ("MCQ4_GEMM_PATH", "MCQ4_XCD_LOCAL", "MCQ4_GEMM6_SPLIT", "MCQ4_GEMVM_SPLIT",
               "MCQ4_GEMV_PATH"):
