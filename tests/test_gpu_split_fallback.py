@@ -115,4 +115,3 @@ def test_split_recompute_path(dev, monkeypatch, name, env, case):
     # and the next default call is unaffected (counters left zero)
     Y2 = fn()
     assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
-
