@@ -67,9 +67,15 @@ constexpr int GS_RP = GS_RP_SET;
 #endif
 static_assert(16 * 64 * 4 <= GS_SLOT, "a wave's partials fit its slot");
 
-// Weight copies of an item of ng groups, and how many of them hold rows 0 .. RP(h+1)-1.
+// Weight copies of an item of ng groups, and how many of them hold rows 0 .. n-1.
 __host__ __device__ constexpr int gs_ncopy(int ng) { return (144 * ng + 63) / 64; }
-__host__ __device__ constexpr int gs_need(int ng, int h) { return (288 * ng * (GS_RP * h + GS_RP) + 1023) / 1024; }
+__host__ __device__ constexpr int gs_need_rows(int ng, int n) { return (288 * ng * n + 1023) / 1024; }
+// Row segments of an item, each processed once its copies have landed: GS_RP rows
+// at a time.  (Taking the last two rows one at a time, so that less math waits
+// for the last copy, measured the same.)
+constexpr int GS_NSEG = GS_B / GS_RP;
+__host__ __device__ constexpr int gs_seg_r0(int sg) { return GS_RP * sg; }
+__host__ __device__ constexpr int gs_seg_nr(int) { return GS_RP; }
 
 template <int N, typename F, int I = 0>
 __device__ __forceinline__ void static_for(F &&f) {
@@ -205,45 +211,51 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
             if constexpr (HOIST) negs[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], negc, z, 0, 0, 0);
         }
         const uint32_t base = lds_addr(slot);
+        const uint32_t vq0 = opaque_vgpr(base + qal), vq1 = opaque_vgpr(base + qal + 4),
+                       vd = opaque_vgpr(base + doff);
         // GS_RP K rows (all groups of the span) at a time, each set as soon as the
         // copies holding it have landed (the copies cover the item in row-major
         // order, so rows up to RP (h + 1) - 1 need the first gs_need(ng, h)).
-        auto pair = [&](auto NGc, int h) {
+        // Rows R0 .. R0 + NR - 1 (all groups of the span): their LDS reads first,
+        // then the unpacks and MFMAs, then the scaled sums.
+        auto proc = [&](auto NGc, auto R0c, auto NRc) {
             constexpr int NG = decltype(NGc)::value;
+            constexpr int R0 = decltype(R0c)::value, NR = decltype(NRc)::value;
             constexpr uint32_t rowb = 288u * NG;
-            uint32_t q0[GS_RP][NG], q1[GS_RP][NG];
-            _Float16 dh[GS_RP][NG];
+            uint32_t q0[NR][NG], q1[NR][NG];
+            _Float16 dh[NR][NG];
 #pragma unroll
-            for (int v = 0; v < GS_RP; ++v)
+            for (int v = 0; v < NR; ++v)
 #pragma unroll
                 for (int grp = 0; grp < NG; ++grp) {
-                    const uint32_t ra = base + (GS_RP * h + v) * rowb + grp * 288;
-                    const lds_u32 *qp = (const lds_u32 *)lds_ptr(ra + qal);
-                    q0[v][grp] = qp[0];
-                    q1[v][grp] = qp[1];
-                    dh[v][grp] = bitcast<_Float16>(*(const lds_u16 *)lds_ptr(ra + doff));
+                    // Immediate offsets from per-lane bases (one VGPR each for the two
+                    // words and the scale), so no address arithmetic per row.
+                    const uint32_t ro = (R0 + v) * rowb + grp * 288;
+                    q0[v][grp] = *(const lds_u32 *)(lds_ptr(vq0) + ro);
+                    q1[v][grp] = *(const lds_u32 *)(lds_ptr(vq1) + ro);
+                    dh[v][grp] = bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(vd) + ro));
                 }
-            float4_t ns[GS_RP];
+            float4_t ns[NR];
 #pragma unroll
-            for (int v = 0; v < GS_RP; ++v) {
-                if constexpr (HOIST) ns[v] = negs[GS_RP * h + v];
-                else ns[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[GS_RP * h + v], negc, z, 0, 0, 0);
+            for (int v = 0; v < NR; ++v) {
+                if constexpr (HOIST) ns[v] = negs[R0 + v];
+                else ns[v] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[R0 + v], negc, z, 0, 0, 0);
             }
-            float4_t r[GS_RP][NG];
+            float4_t r[NR][NG];
 #pragma unroll
-            for (int v = 0; v < GS_RP; ++v)
+            for (int v = 0; v < NR; ++v)
 #pragma unroll
                 for (int grp = 0; grp < NG; ++grp) {
                     const uint32_t w = __builtin_amdgcn_alignbit(q1[v][grp], q0[v][grp], qsh);
                     const uint32_t w8 = __builtin_amdgcn_alignbit(q1[v][grp], q0[v][grp], qsh + 8);
                     const uint4_t bq = {and_or(w, mlo, e1024), and_or(w, mhi, e64), and_or(w8, mlo, e1024),
                                         and_or(w8, mhi, e64)};
-                    r[v][grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[GS_RP * h + v], bitcast<half8_t>(bq),
-                                                                       ns[v], 0, 0, 0);
+                    r[v][grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[R0 + v], bitcast<half8_t>(bq), ns[v], 0,
+                                                                       0, 0);
                 }
 #pragma unroll
-            for (int v = 0; v < GS_RP; ++v)
-                if (GS_RP * h + v < rows) {
+            for (int v = 0; v < NR; ++v)
+                if (R0 + v < rows) {
 #pragma unroll
                     for (int grp = 0; grp < NG; ++grp)
 #pragma unroll
@@ -251,12 +263,14 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
                             acc[grp][i] += (float)dh[v][grp] * r[v][grp][i * IS];
                 }
         };
-        constexpr int NH = GS_B / GS_RP;
-        static_for<NH>([&](auto H) {
-            constexpr int h = decltype(H)::value;
-            if constexpr (h + 1 < NH) wait_vmcnt<NC - gs_need(NG, h)>();
+        // Segments of rows, each run as soon as the copies holding it have landed
+        // (the copies cover the item in row-major order).
+        static_for<GS_NSEG>([&](auto Sg) {
+            constexpr int sg = decltype(Sg)::value;
+            constexpr int r0 = gs_seg_r0(sg), nr = gs_seg_nr(sg);
+            if constexpr (sg + 1 < GS_NSEG) wait_vmcnt<NC - gs_need_rows(NG, r0 + nr)>();
             else wait_vmcnt<0>();
-            pair(NGc, h);
+            proc(NGc, std::integral_constant<int, r0>{}, std::integral_constant<int, nr>{});
         });
     };
     if (rows > 0) {
