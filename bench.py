@@ -188,21 +188,22 @@ def shape_bench(mo, torch, dev, M, K, N, pool_bytes=1 << 30, reps=20, outliers=F
 
 def prefill_split_sweep(mo, torch, dev):
     """The few-tile prefill shapes (M = 512, N = 4096: 32 tiles of 256 x 256, 64 of
-    128 x 256) under each prefill kernel forced with 1, 2, 4 and 8 K splits, and the
-    default plan: TFLOP/s per point, graph replays over rotated weight copies."""
+    128 x 256, 128 of 128 x 128) under each prefill kernel forced with 1, 2, 4 and 8
+    K splits (q4_gemm8: 1 and 2), and the default plan: TFLOP/s per point, graph replays over rotated weight copies."""
     from metalops_amd import _lib
-    keys = ("MCQ4_GEMM_PATH", "MCQ4_GEMM6_SPLIT")
+    keys = ("MCQ4_GEMM_PATH", "MCQ4_GEMM6_SPLIT", "MCQ4_GEMM8_SPLIT")
     saved = {k: os.environ.get(k) for k in keys}
     out = []
     try:
         for M, K, N in ((512, 11008, 4096), (512, 4096, 4096)):
-            runs = [("default", None, None)] + [(f"gemm{p}", p, sp) for p in ("6", "7") for sp in (1, 2, 4, 8)]
+            runs = [("default", None, None)] + [(f"gemm{p}", p, sp) for p in ("6", "7") for sp in (1, 2, 4, 8)] \
+                + [("gemm8", "8", sp) for sp in (1, 2)]
             for name, path, sp in runs:
                 for k in keys:
                     os.environ.pop(k, None)
                 if path:
                     os.environ["MCQ4_GEMM_PATH"] = path
-                    os.environ["MCQ4_GEMM6_SPLIT"] = str(sp)
+                    os.environ["MCQ4_GEMM8_SPLIT" if path == "8" else "MCQ4_GEMM6_SPLIT"] = str(sp)
                 _lib.reload_options()
                 t, _, _ = shape_bench(mo, torch, dev, M, K, N, reps=5)
                 out.append({"M": M, "K": K, "N": N, "kernel": name, "splits": sp, "us": round(t * 1e6, 2),

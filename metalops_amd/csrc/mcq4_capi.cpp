@@ -44,6 +44,7 @@ hipError_t i4_gemv_split_fallbacks(uint64_t *count, bool reset);
 hipError_t i4_gemv1_split_fallbacks(uint64_t *count, bool reset);
 hipError_t i4_gemm6_split_fallbacks(uint64_t *count, bool reset);
 hipError_t q4_gemv_span_split_fallbacks(uint64_t *count, bool reset);
+hipError_t q4_gemm8_split_fallbacks(uint64_t *count, bool reset);
 hipError_t launch_q4_xact(const void *X, int x_dt, int64_t ldx, const uint8_t *W, void *Y,
                           int64_t ldy, int64_t M, int64_t K, int64_t N, hipStream_t s);
 bool gemv_dma_supported(const _Float16 *X, const uint8_t *W, int64_t K, int64_t N);
@@ -74,13 +75,14 @@ constexpr int64_t kMaxDim = (int64_t)1 << 30;  // keeps 32-bit lane offsets safe
 bool aligned(const void *p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
 // Prefill kernel choice (M > 64).  When N % 128 == 0 and the pointers are
-// 16-byte aligned: the 256 x 256-tile GEMM (q4_gemm7) on grids that nearly fill
-// the CUs, else the 128 x 256-tile LDS-staged GEMM with two waves per SIMD
+// 16-byte aligned: the few-tile GEMM (q4_gemm8) when its plan is one round of
+// workgroups, the 256 x 256-tile GEMM (q4_gemm7) on grids that nearly fill the
+// CUs, else the 128 x 256-tile LDS-staged GEMM with two waves per SIMD
 // (q4_gemm6).  Otherwise the async-copy GEMM (q4_gemm2) when its alignment
 // needs hold and the output has at least 128 tiles of 128x256; otherwise the
-// register-staged split-K kernel.  MCQ4_GEMM_PATH=sync|async|6|7 forces one
+// register-staged split-K kernel.  MCQ4_GEMM_PATH=sync|async|6|7|8 forces one
 // kernel (tests).
-enum class Prefill { Sync, Async2, Staged6, Wide7 };
+enum class Prefill { Sync, Async2, Staged6, Wide7, Few8 };
 Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
                        int64_t N) {
     const bool ok2 = mcq4::gemm2_supported(X, ldx, W, K, N);
@@ -90,6 +92,7 @@ Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t
         if (env[0] == 'a' && ok2) return Prefill::Async2;
         if (env[0] == '6' && ok6) return Prefill::Staged6;
         if (env[0] == '7' && mcq4::gemm7_supported(X, ldx, W, M, K, N)) return Prefill::Wide7;
+        if (env[0] == '8' && mcq4::gemm8_supported(X, ldx, W, M, K, N)) return Prefill::Few8;
     }
     // The 256 x 256-tile GEMM (one wave per SIMD, half the dequant per MFMA)
     // wins once its grid nearly fills the 256 CUs, or with half of that on long
@@ -98,6 +101,18 @@ Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t
     // M=2048 4096x14336 244 / 213, 14336x4096 235 / 209, 4096x4096 71 / 80;
     // M=512 4096x128256 513 / 485, 11008x4096 57 / 61; M=1024 4096x14336
     // 117 / 111; M=256 4096x14336 46 / 47.
+    // The few-tile GEMM (128 x 128 tiles, eight waves, K split four ways
+    // inside the workgroup and at most twice across) wins when its grid is one
+    // round of 192..256 workgroups.  Measured (us, default / q4_gemm8): M=512
+    // 11008x4096 58.8 / 55.1, 14336x4096 76.1 / 68.3, 4096x4096 31.6 / 28.7;
+    // M=384 11008x4096 51.1 / 47.5; M=768 4096x4096 44.9 / 34.1; M=1024
+    // 4096x4096 50.3 / 40.2, 14336x4096 130.2 / 118.7; M=256 4096x14336
+    // 47.0 / 39.3.  Outside that range it loses (M=1536 4096x4096 64.9 / 71.6,
+    // M=256 11008x4096 37.8 / 42.2, M=512 4096x14336 70.5 / 73.2).
+    if (ok6 && mcq4::gemm8_supported(X, ldx, W, M, K, N)) {
+        const int g8 = mcq4::gemm8_workgroups(M, K, N);
+        if (g8 >= 192 && g8 <= 256) return Prefill::Few8;
+    }
     if (ok6 && mcq4::gemm7_supported(X, ldx, W, M, K, N)) {
         const int64_t t7 = ((M + 255) / 256) * ((N + 255) / 256);
         if (t7 >= 192 || (t7 >= 96 && K >= 8192)) return Prefill::Wide7;
@@ -240,7 +255,7 @@ size_t mcq4_matmul_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M <= 32) return mcq4::skinny_workspace_bytes(M, K, N);
     // The largest of the split-K kernels' needs: an upper bound for any prefill kernel.
     const size_t pre = std::max({mcq4::gemm_workspace_bytes(M, K, N), mcq4::gemm6_workspace_bytes(M, K, N),
-                                 mcq4::gemm7_workspace_bytes(M, K, N)});
+                                 mcq4::gemm7_workspace_bytes(M, K, N), mcq4::gemm8_workspace_bytes(M, K, N)});
     // 33..64 rows run either family, depending on the pointers' alignment.
     return M <= 64 ? std::max(pre, mcq4::skinny_workspace_bytes(M, K, N)) : pre;
 }
@@ -279,6 +294,7 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
         switch (prefill_kernel(x, ldx, W, M, K, N)) {
             case Prefill::Staged6: e = mcq4::launch_gemm6(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
             case Prefill::Wide7: e = mcq4::launch_gemm7(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
+            case Prefill::Few8: e = mcq4::launch_gemm8(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
             case Prefill::Async2: e = mcq4::launch_gemm2(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, st); break;
             default: e = mcq4::launch_gemm(x, ldx, W, y, ldy, (int)M, (int)K, (int)N, workspace, st); break;
         }
@@ -354,7 +370,8 @@ int mcq4_split_fallback_count(uint64_t *count, int reset) {
     *count = 0;
     hipError_t (*const readers[])(uint64_t *, bool) = {
         mcq4::q4_gemvm_split_fallbacks, mcq4::q4_gemm6_split_fallbacks, mcq4::i4_gemv_split_fallbacks,
-        mcq4::i4_gemv1_split_fallbacks, mcq4::i4_gemm6_split_fallbacks, mcq4::q4_gemv_span_split_fallbacks};
+        mcq4::i4_gemv1_split_fallbacks, mcq4::i4_gemm6_split_fallbacks, mcq4::q4_gemv_span_split_fallbacks,
+        mcq4::q4_gemm8_split_fallbacks};
     for (auto rd : readers)
         if (int st = hip_status(rd(count, reset != 0), "split fallback counter")) return st;
     return MCQ4_OK;

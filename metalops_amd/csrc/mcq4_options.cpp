@@ -16,8 +16,9 @@ namespace {
 const char *const kNames[] = {
     // q4_0 path
     "MCQ4_XCD_LOCAL",       // 0: split-K partials through memory / the reduction kernel
-    "MCQ4_GEMM_PATH",       // sync | async | 6 | 7: force one prefill kernel
+    "MCQ4_GEMM_PATH",       // sync | async | 6 | 7 | 8: force one prefill kernel
     "MCQ4_GEMM6_SPLIT",     // K splits of the prefill GEMM
+    "MCQ4_GEMM8_SPLIT",     // 1 | 2: K splits of the few-tile prefill GEMM
     "MCQ4_GEMV_PATH",       // off: M == 1 through the batched decode kernels
     "MCQ4_GEMV_SPAN",       // 0: no span kernels (strip kernels instead); 1: the split form wherever it fits
     "MCQ4_GEMVM_SPLIT",     // 1 | 2 | 4 | 8: K splits of the batched decode GEMV

@@ -33,4 +33,16 @@ size_t gemm6_workspace_bytes(int64_t M, int64_t K, int64_t N);
 hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
 
+// Few-tile prefill GEMM (q4_gemm8): 128 x 128 tiles, eight waves with K split
+// four ways inside the workgroup, at most two K splits across workgroups
+// summed through the XCD's L2 (partials [tiles][2][128*128] after the ticket
+// area).  Needs N % 128 == 0, 16-byte aligned W and activation rows, K >= 32.
+constexpr int G8_BM = 128;
+constexpr int G8_BN = 128;
+bool gemm8_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N);
+size_t gemm8_workspace_bytes(int64_t M, int64_t K, int64_t N);
+int gemm8_workgroups(int64_t M, int64_t K, int64_t N);   // tiles x K splits of its plan
+hipError_t launch_gemm8(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
+                        int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
+
 }  // namespace mcq4

@@ -38,7 +38,7 @@ def _replay_check(dev, fn, out_ref, reps=4):
 
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 4096), (1, 4096, 128256 // 16), (8, 4096, 2048),
                                    (16, 14336, 4096), (128, 4096, 1024), (512, 11008, 512), (384, 4096, 4096),
-                                   (2048, 4096, 14336), (2048, 14336, 4096)])
+                                   (512, 11008, 4096), (1024, 4096, 4096), (2048, 4096, 14336), (2048, 14336, 4096)])
 def test_q4_0_graph_replay(mo, dev, M, K, N):
     g = torch.Generator(device=dev).manual_seed(M + N)
     W = torch.randn(K, N, generator=g, device=dev) * 0.02

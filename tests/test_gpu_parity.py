@@ -250,6 +250,9 @@ PATHS = {
     "gemm7": {"MCQ4_GEMM_PATH": "7"},
     "gemm7_split2": {"MCQ4_GEMM_PATH": "7", "MCQ4_GEMM6_SPLIT": "2"},
     "gemm7_split3": {"MCQ4_GEMM_PATH": "7", "MCQ4_GEMM6_SPLIT": "3"},
+    "gemm8": {"MCQ4_GEMM_PATH": "8"},
+    "gemm8_split1": {"MCQ4_GEMM_PATH": "8", "MCQ4_GEMM8_SPLIT": "1"},
+    "gemm8_split2": {"MCQ4_GEMM_PATH": "8", "MCQ4_GEMM8_SPLIT": "2"},
     "gemv_span": {},
     "gemv_span_split": {"MCQ4_GEMV_SPAN": "1"},
     "gemv_span_split_off": {"MCQ4_GEMV_SPAN": "0"},
@@ -311,13 +314,20 @@ PATH_SHAPES = {
               (200, 32, 256), (130, 64, 384), (513, 96, 256), (2048, 11008, 512), (65, 4096, 4096)],
     "gemm7_split2": [(200, 352, 384), (300, 4096, 640), (512, 4096, 1024)],
     "gemm7_split3": [(300, 4096, 640), (129, 2048, 2304)],
+    # K blocks per split below, at and past one four-block stage (1, 3, 5, 7 blocks:
+    # phases idle in the last stage), and the plan's two splits.
+    "gemm8": [(129, 352, 128), (257, 1024, 384), (300, 2048, 512), (512, 4096, 768), (2048, 4096, 1024),
+              (200, 32, 256), (513, 96, 256), (100, 160, 128), (200, 224, 256), (512, 11008, 4096),
+              (2048, 11008, 512)],
+    "gemm8_split1": [(512, 4096, 768), (300, 2048, 512), (130, 4128, 256), (65, 1024, 128)],
+    "gemm8_split2": [(600, 1056, 640), (2048, 4096, 1024), (129, 1024, 2304)],
 }
 
 
 @pytest.mark.parametrize("path,M,K,N", [(p, *s) for p, shapes in PATH_SHAPES.items() for s in shapes])
 def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
     for k in ("MCQ4_DECODE_PATH", "MCQ4_GEMM_PATH", "MCQ4_GEMM2_BM", "MCQ4_GEMV_PATH",
-              "MCQ4_GEMM6_SPLIT", "MCQ4_GEMVM_SPLIT", "MCQ4_GEMVM_HOIST", "MCQ4_XCD_LOCAL",
+              "MCQ4_GEMM6_SPLIT", "MCQ4_GEMM8_SPLIT", "MCQ4_GEMVM_SPLIT", "MCQ4_GEMVM_HOIST", "MCQ4_XCD_LOCAL",
               "MCQ4_GEMV_SPAN"):
         monkeypatch.delenv(k, raising=False)
     for k, v in PATHS[path].items():
@@ -335,17 +345,23 @@ def test_matmul_each_kernel(dev, monkeypatch, path, M, K, N):
                                          (300, 4096, 640, "gemm3"), (384, 4096, 4096, "gemm4"),
                                          (16, 14336, 4096, "gemvm2"),
                                          (9, 4096, 1040, "gemvm2"), (12, 11008, 8200, "gemvm4"),
-                                         (16, 2048, 1032, "gemvm8")])
+                                         (16, 2048, 1032, "gemvm8"), (512, 11008, 4096, "few8"),
+                                         (600, 1056, 640, "few8")])
 def test_split_exchange_matches_reduce(dev, monkeypatch, M, K, N, split):
     """K split over workgroups: the in-kernel XCD-local sum (default) and the
     reduction kernel add the same partials in the same order (two splits of the
     GEMM: p0 + p1, which commutes; three or four splits go to the reduction
-    kernel either way), so the outputs are identical bits."""
+    kernel either way), so the outputs are identical bits.  The few-tile GEMM
+    (q4_gemm8, two splits) has no reduction-kernel form: its runs must repeat
+    bit for bit."""
     print(f"split exchange {split} M={M} K={K} N={N}", flush=True)
-    for k in ("MCQ4_GEMM_PATH", "MCQ4_XCD_LOCAL", "MCQ4_GEMM6_SPLIT", "MCQ4_GEMVM_SPLIT",
+    for k in ("MCQ4_GEMM_PATH", "MCQ4_XCD_LOCAL", "MCQ4_GEMM6_SPLIT", "MCQ4_GEMM8_SPLIT", "MCQ4_GEMVM_SPLIT",
               "MCQ4_GEMV_PATH"):
         monkeypatch.delenv(k, raising=False)
-    if split.startswith("gemm"):
+    if split == "few8":
+        monkeypatch.setenv("MCQ4_GEMM_PATH", "8")
+    elif split.startswith("gemm"):
+        monkeypatch.setenv("MCQ4_GEMM_PATH", "6")
         monkeypatch.setenv("MCQ4_GEMM6_SPLIT", split[-1])
     else:
         monkeypatch.setenv("MCQ4_GEMVM_SPLIT", split[-1])
@@ -357,10 +373,12 @@ def test_split_exchange_matches_reduce(dev, monkeypatch, M, K, N, split):
     X = torch.randn(M, K, generator=g).half().to(dev)
     Y = mo.matmul_ggml_q4_0(X, blocks)
     Y2 = mo.matmul_ggml_q4_0(X, blocks)
-    monkeypatch.setenv("MCQ4_XCD_LOCAL", "0")
-    Y0 = mo.matmul_ggml_q4_0(X, blocks)
     assert torch.isfinite(Y.float()).all()
     assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
+    if split == "few8":
+        return
+    monkeypatch.setenv("MCQ4_XCD_LOCAL", "0")
+    Y0 = mo.matmul_ggml_q4_0(X, blocks)
     assert torch.equal(Y.view(torch.int16), Y0.view(torch.int16))
 
 

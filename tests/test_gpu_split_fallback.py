@@ -77,6 +77,7 @@ CASES = [
     ("q4_gemvm_rows4_s4", {"MCQ4_GEMVM_SPLIT": "4"}, ("q4", 3, 4096, 1040)),
     ("q4_gemvm_rows8_s2", {"MCQ4_GEMVM_SPLIT": "2"}, ("q4", 7, 11008, 512)),
     ("q4_gemm6_s2", {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "2"}, ("q4", 300, 4096, 640)),
+    ("q4_gemm8_s2", {"MCQ4_GEMM_PATH": "8"}, ("q4", 300, 4096, 640)),
     # 64-column spans over K splits (q4_gemv_span.hip): 4, 5 and 4 splits, 16, 4 and 8 rows.
     ("q4_span_split_s4", {}, ("q4", 16, 14336, 4096)),
     ("q4_span_split_rows4_s5", {"MCQ4_GEMV_SPAN": "1"}, ("q4", 3, 2080, 2048)),
@@ -94,7 +95,7 @@ CASES = [
 def test_split_recompute_path(dev, monkeypatch, name, env, case):
     from metalops_amd import _lib
     print(f"split recompute {name} {case}", flush=True)
-    for k in ("MCQ4_GEMVM_SPLIT", "MCQ4_GEMM_PATH", "MCQ4_GEMM6_SPLIT", "MCQ4_I4_GEMV1", "MCQ4_XCD_LOCAL",
+    for k in ("MCQ4_GEMVM_SPLIT", "MCQ4_GEMM_PATH", "MCQ4_GEMM6_SPLIT", "MCQ4_GEMM8_SPLIT", "MCQ4_I4_GEMV1", "MCQ4_XCD_LOCAL",
               "MCQ4_SPLIT_FOREIGN", "MCQ4_I4_PATH", "MCQ4_I4_SPW1", "MCQ4_I4_GEMM7", "MCQ4_GEMV_SPAN"):
         monkeypatch.delenv(k, raising=False)
     for k, v in env.items():
