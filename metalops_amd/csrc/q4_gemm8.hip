@@ -82,8 +82,7 @@ q4_gemm8_kernel(Gemm6Args a) {
     constexpr int SUM_REGION = 64 * 16 * TN * 4;  // one wave's 32 x WN fp32 block
     constexpr int GROUP = A_LD + W_LD;            // vector-memory instructions per wave and stage
     constexpr int NMF = 2 * TM * TN;              // MFMAs per stage (32)
-    constexpr int NCH = 3 * 2 * TN;               // dequant chunks per stage (3 per 8-weight unit)
-    static_assert(2 * GROUP <= NMF && NCH <= NMF, "copies and dequant ride on the stage's MFMAs");
+    static_assert(2 * GROUP <= NMF, "copies ride on the stage's odd MFMAs");
     // Stage t's weights go out with stage t - G8_WD's activations, after them.
     // Copies still allowed in flight once the stage the next barrier admits has
     // landed (its activations and weights): with G8_WD > 0, the rest of the
@@ -181,10 +180,29 @@ q4_gemm8_kernel(Gemm6Args a) {
         const uint32_t base = lds_addr(sA + (s % G8_NS) * G8_A_SLOT);
         return *(const lds_half8 *)(lds_ptr(base + a_off[ks]) + i * 32 * G8_ROWB);
     };
+    // B operand (ks, j): column 32 j + lrow, K elements 16 ks + 8 lhi .. +8 of
+    // the block: qs bytes 2 + 8 ks + 4 lhi .. +4 of the column's 18-byte block,
+    // byte q_b + u of the dword pair at q_al.  Dequant of one B dword (elements
+    // 2u, 2u + 1 of the lane's eight): v_perm_b32 puts byte u into bytes 0 and
+    // 2, v_and_or_b32 keeps the low nibble in byte 0 and the high nibble in
+    // place in byte 2 and adds the exponent bytes 0x64 and 0x54, giving the
+    // fp16 pair {1024 + q0, 64 + q1} exactly; minus {1032, 72} (exact) gives
+    // q - 8, and one multiply by d the single rounding of the exact product --
+    // the reference's fp16 dequant value.  4 VALU per two weights.
     const int qoff0 = 18 * lrow + 2 + 4 * lhi;
     const int q_al = qoff0 & ~3;
-    const uint32_t q_sh = (uint32_t)(qoff0 & 3) * 8;
+    const int q_b = qoff0 & 3;
     const int d_off = 18 * lrow;
+    uint32_t bsel[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) bsel[u] = (uint32_t)(q_b + u) * 0x00010001u + 0x0C000C00u;
+    const uint32_t nib_mask = opaque_sgpr(0x00F0000Fu), exp_bits = opaque_vgpr(0x54006400u);
+    auto dq2 = [&](uint32_t hi_w, uint32_t lo_w, int u, half2_t d2) {
+#pragma clang fp contract(off)
+        const half2_t off = {(_Float16)1032.0f, (_Float16)72.0f};
+        const half2_t h = bitcast<half2_t>(and_or(__builtin_amdgcn_perm(hi_w, lo_w, bsel[u]), nib_mask, exp_bits));
+        return bitcast<uint32_t>((h - off) * d2);
+    };
     auto load_b = [&](int s, half8_t (&bv)[2][TN]) {
         const lds_u8 *Rs = lds_ptr(lds_addr(ring + (s % G8_RAW_N) * RAW_SLOT));
 #pragma unroll
@@ -196,8 +214,12 @@ q4_gemm8_kernel(Gemm6Args a) {
             const uint32_t dd = *(const lds_u16 *)(Rs + d_off + j * 32 * 18);
             const half2_t d2 = bitcast<half2_t>(__builtin_amdgcn_perm(dd, dd, 0x01000100u));
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-                bv[ks][j] = dequant8_nat(__builtin_amdgcn_alignbit(qd[2 * ks + 1], qd[2 * ks], q_sh), d2);
+            for (int ks = 0; ks < 2; ++ks) {
+                uint4_t r;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) r[u] = dq2(qd[2 * ks + 1], qd[2 * ks], u, d2);
+                bv[ks][j] = bitcast<half8_t>(r);
+            }
         }
     };
 
@@ -209,9 +231,14 @@ q4_gemm8_kernel(Gemm6Args a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    // One stage: the NMF MFMAs of (A, B).  After MFMA idx: dequant chunk idx of
-    // the next stage's B, the in-place reload of the A operand whose last use
-    // this was (stage s_next), and copy idx/2 of stage cs after every odd MFMA.
+    // One stage: the NMF MFMAs of (A, B), ordered ks, i, j.  The next stage's B
+    // is NMF dwords (d = 4 unit + u, unit = 2 j + ks): after MFMA idx the
+    // perm and and_or of dword idx - 1 and the subtract and multiply of dword
+    // idx - 2 (so neither waits on the raw words just read nor on its own
+    // first half), the rest after the last MFMA; also the in-place reload of
+    // the A operand whose last use this was (stage s_next), and copy idx/2 of
+    // stage cs after every odd MFMA.
+    static_assert(NMF == 8 * TN, "one B dword per MFMA");
     half8_t A[2][TM];
     auto stage = [&](int cs, const half8_t (&B)[2][TN], int s_next, half8_t (&Bn)[2][TN]) {
 #pragma clang fp contract(off)
@@ -224,11 +251,20 @@ q4_gemm8_kernel(Gemm6Args a) {
             for (int t = 0; t < 4; ++t) qd[j][t] = qp[t];
             dd[j] = *(const lds_u16 *)(Rs + d_off + j * 32 * 18);
         }
-        const half2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
-        const uint32_t C64 = 0x64646464u;
-        uint32_t lo[2 * TN], hi[2 * TN];
-        uint4_t uu[2 * TN];
+        const half2_t off = {(_Float16)1032.0f, (_Float16)72.0f};
         half2_t d2[TN];
+        uint32_t xw[NMF];
+        uint4_t bb[2 * TN];
+        auto first = [&](int d) {
+            const int unit = d >> 2, u = d & 3, uj = unit >> 1, uk = unit & 1;
+            if (u == 0 && uk == 0) d2[uj] = bitcast<half2_t>(__builtin_amdgcn_perm(dd[uj], dd[uj], 0x01000100u));
+            xw[d] = and_or(__builtin_amdgcn_perm(qd[uj][2 * uk + 1], qd[uj][2 * uk], bsel[u]), nib_mask, exp_bits);
+        };
+        auto second = [&](int d) {
+            const int unit = d >> 2, u = d & 3, uj = unit >> 1, uk = unit & 1;
+            bb[unit][u] = bitcast<uint32_t>((bitcast<half2_t>(xw[d]) - off) * d2[uj]);
+            if (u == 3) Bn[uk][uj] = bitcast<half8_t>(bb[unit]);
+        };
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int idx = 0; idx < NMF; ++idx) {
@@ -236,30 +272,13 @@ q4_gemm8_kernel(Gemm6Args a) {
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[ks][i], B[ks][j], acc[i][j], 0, 0, 0);
             if (j == TN - 1) A[ks][i] = read_a1(s_next, ks, i);
             if ((idx & 1) == 1 && (idx >> 1) < GROUP) issue_one(cs, idx >> 1);
-            if (idx < NCH) {
-                const int c = idx, unit = c / 3, part = c % 3, uj = unit >> 1, uk = unit & 1;
-                if (part == 0) {
-                    if (uk == 0) d2[uj] = bitcast<half2_t>(__builtin_amdgcn_perm(dd[uj], dd[uj], 0x01000100u));
-                    const uint32_t w = __builtin_amdgcn_alignbit(qd[uj][2 * uk + 1], qd[uj][2 * uk], q_sh);
-                    lo[unit] = w & 0x0F0F0F0Fu;
-                    hi[unit] = (w >> 4) & 0x0F0F0F0Fu;
-                } else if (part == 1) {
-                    const uint32_t e03 = __builtin_amdgcn_perm(hi[unit], lo[unit], 0x05010400u);
-                    const uint32_t e47 = __builtin_amdgcn_perm(hi[unit], lo[unit], 0x07030602u);
-                    uu[unit] = uint4_t{__builtin_amdgcn_perm(C64, e03, 0x04010400u),
-                                       __builtin_amdgcn_perm(C64, e03, 0x04030402u),
-                                       __builtin_amdgcn_perm(C64, e47, 0x04010400u),
-                                       __builtin_amdgcn_perm(C64, e47, 0x04030402u)};
-                } else {
-                    uint4_t r;
-#pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        r[t] = bitcast<uint32_t>((bitcast<half2_t>(uu[unit][t]) - off) * d2[uj]);
-                    Bn[uk][uj] = bitcast<half8_t>(r);
-                }
-            }
+            if (idx >= 2) second(idx - 2);
+            if (idx >= 1) first(idx - 1);
             __builtin_amdgcn_sched_barrier(0);
         }
+        second(NMF - 2);
+        first(NMF - 1);
+        second(NMF - 1);
     };
 
     // Prologue: the weights of stages 0 .. G8_WD-1, then activation stages
