@@ -86,7 +86,7 @@ enum class Prefill { Sync, Async2, Staged6, Wide7, Few8 };
 Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K,
                        int64_t N) {
     const bool ok2 = mcq4::gemm2_supported(X, ldx, W, K, N);
-    const bool ok6 = mcq4::gemm6_supported(X, ldx, W, K, N);
+    const bool ok6 = mcq4::gemm6_supported(X, ldx, W, M, K, N);
     if (const char *env = mcq4::opt("MCQ4_GEMM_PATH")) {
         if (env[0] == 's') return Prefill::Sync;
         if (env[0] == 'a' && ok2) return Prefill::Async2;
@@ -283,7 +283,7 @@ int mcq4_matmul_q4_0_f16(const void *X, int64_t ldx, const uint8_t *W, void *Y, 
     hipError_t e;
     // 33..64 rows: q4_gemm6 (flat ~31 us for any M <= 128 on 4096x14336) beats the
     // register-load decode kernel (40-77 us) wherever its alignment rules hold.
-    const bool skinny = M <= 32 || (M <= 64 && !mcq4::gemm6_supported((const _Float16 *)X, ldx, W, K, N));
+    const bool skinny = M <= 32 || (M <= 64 && !mcq4::gemm6_supported((const _Float16 *)X, ldx, W, M, K, N));
     if (skinny)
         e = mcq4::launch_skinny((const _Float16 *)X, ldx, W, (_Float16 *)Y, ldy, (int)M, (int)K,
                                 (int)N, workspace, (hipStream_t)stream);

@@ -77,43 +77,53 @@ q4_gemm6_kernel(Gemm6Args a) {
     uint8_t *const ring = smem + G6_NS * A_SLOT + wave * (G6_RAW_N * G6_RAW_SLOT);
 
     // A copy u of this wave: positions 64(wave*A_LD+u) + lane = row 8(wave*A_LD+u) + lane/8,
-    // chunk (lane ^ lane/8) & 7 (the same for every u).
+    // chunk (lane ^ lane/8) & 7 (the same for every u): K step a_t = chunk/4 of
+    // the stage, halves 8 (chunk % 4) .. +7 of it.  All copies are buffer loads
+    // into LDS whose lane offsets are fixed and whose stage offsets are scalars.
     const int a_c = (lane ^ (lane >> 3)) & 7;
     const int a_t = a_c >> 2;
     const int a_r0 = m0 + 8 * wave * A_LD + (lane >> 3);
-    const _Float16 *a_col = a.X + (int64_t)k_lo * QK + 8 * (a_c & 3);
+    const __amdgpu_buffer_rsrc_t a_rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.X, (short)0, (int)((int64_t)a.M * a.ldx * 2), 0x00020000);
+    uint32_t a_vo[A_LD];
+#pragma unroll
+    for (int u = 0; u < A_LD; ++u) {
+        const int m = min(a_r0 + 8 * u, a.M - 1);
+        a_vo[u] = ((uint32_t)m * (uint32_t)a.ldx + 8 * (a_c & 3)) * 2 + a_t * (QK * 2);
+    }
 
-    const int64_t row_bytes = (int64_t)a.N * BLOCK_BYTES;
-    const uint8_t *w_k = a.W + (int64_t)k_lo * row_bytes;
+    const uint32_t row_bytes = (uint32_t)a.N * BLOCK_BYTES;
     const bool wcols = n0 + wn * WN < a.N;
-    const uint8_t *w_seg = wcols ? w_k + (int64_t)(n0 + wn * WN) * BLOCK_BYTES : w_k;
+    const __amdgpu_buffer_rsrc_t w_rs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.W, (short)0, (int)0x7fffffff, 0x00020000);
+    const uint32_t w_so0 = (uint32_t)k_lo * row_bytes + (wcols ? (uint32_t)(n0 + wn * WN) * BLOCK_BYTES : 0u);
+    const uint32_t w_vo16 = 16 * lane, w_vo4 = 4 * min(lane, 31);
 
     // Copy ci (0 .. GROUP-1) of stage s_dst: A copies, then per step t the raw
     // bytes 0..1023 (16 per lane) and 1024..1151 (4 per lane for lanes 0..31;
     // lanes 32..63 re-read lane 31's dword into the slot's unused tail, so no
     // lane is masked and nothing past the segment is read).  LDS-DMA copies of
     // fewer than 4 bytes per lane still fill 4 bytes per lane, so 2-byte copies
-    // cannot pack the remainder.  Stages past the end re-copy the last stage.
+    // cannot pack the remainder.  Weight steps past the split's end re-copy its
+    // last step; activation steps past it are read (zero past the activations'
+    // last byte) but feed no MFMA.  The instruction's immediate offset would
+    // move the LDS destination too, so piece offsets go into the scalar offset.
     auto issue_one = [&](int s_dst, int ci) {
-        const int s_src = min(s_dst, nst - 1);
         if (ci < A_LD) {
             uint8_t *dst = sA + (s_dst % G6_NS) * A_SLOT + wave * (A_LD * 1024) + 1024 * ci;
-            const int64_t koff = (int64_t)min(2 * s_src + a_t, nk - 1) * QK;
-            const int m = min(a_r0 + 8 * ci, a.M - 1);
-            __builtin_amdgcn_global_load_lds(
-                (void *)(a_col + (int64_t)m * a.ldx + koff),
-                (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (__attribute__((address_space(3))) void *)dst, 16,
+                                                     a_vo[ci], (uint32_t)(k_lo + 2 * s_dst) * (QK * 2), 0, 0);
             return;
         }
         const int r = ci - A_LD, t = r >> 1;
-        const uint8_t *src = w_seg + (int64_t)min(2 * s_src + t, nk - 1) * row_bytes;
+        const uint32_t so = w_so0 + (uint32_t)min(2 * s_dst + t, nk - 1) * row_bytes;
         uint8_t *dst = ring + ((2 * s_dst + t) % G6_RAW_N) * G6_RAW_SLOT;
         if ((r & 1) == 0)
-            __builtin_amdgcn_global_load_lds((void *)(src + 16 * lane),
-                                             (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rs, (__attribute__((address_space(3))) void *)dst, 16, w_vo16,
+                                                     so, 0, 0);
         else
-            __builtin_amdgcn_global_load_lds((void *)(src + 1024 + 4 * min(lane, 31)),
-                                             (__attribute__((address_space(3))) void *)(dst + 1024), 4, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rs, (__attribute__((address_space(3))) void *)(dst + 1024), 4,
+                                                     w_vo4, so + 1024, 0, 0);
     };
     auto issue_stage = [&](int s_dst) {
 #pragma unroll
@@ -132,11 +142,26 @@ q4_gemm6_kernel(Gemm6Args a) {
         const uint32_t base = lds_addr(sA + (s % G6_NS) * A_SLOT);
         return *(const lds_half8 *)(lds_ptr(base + a_off[t][ks]) + i * 32 * G6_ROWB);
     };
+    // B operand (ks, j): column 32 j + lrow, K elements 16 ks + 8 lhi .. +8 of
+    // the block: qs bytes 2 + 8 ks + 4 lhi .. +4 of the column's 18-byte block,
+    // byte q_b + u of the dword pair at q_al.  Dequant of one B dword (elements
+    // 2u, 2u + 1 of the lane's eight): v_perm_b32 puts byte u into bytes 0 and
+    // 2, v_and_or_b32 keeps the low nibble in byte 0 and the high nibble in
+    // place in byte 2 and adds the exponent bytes 0x64 and 0x54, giving the
+    // fp16 pair {1024 + q0, 64 + q1} exactly; minus {1032, 72} (exact) gives
+    // q - 8, and one multiply by d the single rounding of the exact product --
+    // the reference's fp16 dequant value.  4 VALU per two weights.
     const int qoff0 = 18 * lrow + 2 + 4 * lhi;
     const int q_al = qoff0 & ~3;
-    const uint32_t q_sh = (uint32_t)(qoff0 & 3) * 8;
+    const int q_b = qoff0 & 3;
     const int d_off = 18 * lrow;
+    uint32_t bsel[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) bsel[u] = (uint32_t)(q_b + u) * 0x00010001u + 0x0C000C00u;
+    const uint32_t nib_mask = opaque_sgpr(0x00F0000Fu), exp_bits = opaque_vgpr(0x54006400u);
     auto load_b = [&](int k, half8_t (&bv)[2][TN]) {
+#pragma clang fp contract(off)
+        const half2_t off = {(_Float16)1032.0f, (_Float16)72.0f};
         const lds_u8 *Rs = lds_ptr(lds_addr(ring + (k % G6_RAW_N) * G6_RAW_SLOT));
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
@@ -147,8 +172,16 @@ q4_gemm6_kernel(Gemm6Args a) {
             const uint32_t dd = *(const lds_u16 *)(Rs + d_off + j * 32 * 18);
             const half2_t d2 = bitcast<half2_t>(__builtin_amdgcn_perm(dd, dd, 0x01000100u));
 #pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-                bv[ks][j] = dequant8_nat(__builtin_amdgcn_alignbit(qd[2 * ks + 1], qd[2 * ks], q_sh), d2);
+            for (int ks = 0; ks < 2; ++ks) {
+                uint4_t r;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const half2_t h = bitcast<half2_t>(
+                        and_or(__builtin_amdgcn_perm(qd[2 * ks + 1], qd[2 * ks], bsel[u]), nib_mask, exp_bits));
+                    r[u] = bitcast<uint32_t>((h - off) * d2);
+                }
+                bv[ks][j] = bitcast<half8_t>(r);
+            }
         }
     };
 
@@ -160,10 +193,14 @@ q4_gemm6_kernel(Gemm6Args a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    // One step: the NMF MFMAs of (A, B).  After MFMA idx: dequant chunk idx of
-    // the next B (12 chunks: 3 per 8-weight unit), the in-place reload of the A
-    // operand whose last use this was (next step's A: stage a_s, step a_t), and
-    // with copies, copy idx/2 of stage cs after every odd MFMA.
+    // One step: the NMF MFMAs of (A, B).  The next B is NMF dwords (d = 4 unit
+    // + u, unit = 2 j + ks): after MFMA idx the perm and and_or of dword idx - 1
+    // and the subtract and multiply of dword idx - 2 (so neither waits on the
+    // raw words just read nor on its own first half), the rest after the last
+    // MFMA; also the in-place reload of the A operand whose last use this was
+    // (next step's A: stage a_s, step a_t), and with copies, copy idx/2 of
+    // stage cs after every odd MFMA.
+    static_assert(NMF == 8 * TN, "one B dword per MFMA");
     half8_t A[2][TM];
     auto step = [&](auto with_copies, int cs, const half8_t (&B)[2][TN], int k_next,
                     half8_t (&Bn)[2][TN], int a_s, int a_t) {
@@ -177,11 +214,20 @@ q4_gemm6_kernel(Gemm6Args a) {
             for (int t = 0; t < 4; ++t) qd[j][t] = qp[t];
             dd[j] = *(const lds_u16 *)(Rs + d_off + j * 32 * 18);
         }
-        const half2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
-        const uint32_t C64 = 0x64646464u;
-        uint32_t lo[2 * TN], hi[2 * TN];
-        uint4_t uu[2 * TN];
+        const half2_t off = {(_Float16)1032.0f, (_Float16)72.0f};
         half2_t d2[TN];
+        uint32_t xw[NMF];
+        uint4_t bb[2 * TN];
+        auto first = [&](int d) {
+            const int unit = d >> 2, u = d & 3, uj = unit >> 1, uk = unit & 1;
+            if (u == 0 && uk == 0) d2[uj] = bitcast<half2_t>(__builtin_amdgcn_perm(dd[uj], dd[uj], 0x01000100u));
+            xw[d] = and_or(__builtin_amdgcn_perm(qd[uj][2 * uk + 1], qd[uj][2 * uk], bsel[u]), nib_mask, exp_bits);
+        };
+        auto second = [&](int d) {
+            const int unit = d >> 2, u = d & 3, uj = unit >> 1, uk = unit & 1;
+            bb[unit][u] = bitcast<uint32_t>((bitcast<half2_t>(xw[d]) - off) * d2[uj]);
+            if (u == 3) Bn[uk][uj] = bitcast<half8_t>(bb[unit]);
+        };
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int idx = 0; idx < NMF; ++idx) {
@@ -191,30 +237,13 @@ q4_gemm6_kernel(Gemm6Args a) {
             if constexpr (decltype(with_copies)::value) {
                 if ((idx & 1) == 1 && (idx >> 1) < GROUP) issue_one(cs, idx >> 1);
             }
-            if (idx < 3 * 2 * TN) {
-                const int c = idx, unit = c / 3, part = c % 3, uj = unit >> 1, uk = unit & 1;
-                if (part == 0) {
-                    if (uk == 0) d2[uj] = bitcast<half2_t>(__builtin_amdgcn_perm(dd[uj], dd[uj], 0x01000100u));
-                    const uint32_t w = __builtin_amdgcn_alignbit(qd[uj][2 * uk + 1], qd[uj][2 * uk], q_sh);
-                    lo[unit] = w & 0x0F0F0F0Fu;
-                    hi[unit] = (w >> 4) & 0x0F0F0F0Fu;
-                } else if (part == 1) {
-                    const uint32_t e03 = __builtin_amdgcn_perm(hi[unit], lo[unit], 0x05010400u);
-                    const uint32_t e47 = __builtin_amdgcn_perm(hi[unit], lo[unit], 0x07030602u);
-                    uu[unit] = uint4_t{__builtin_amdgcn_perm(C64, e03, 0x04010400u),
-                                       __builtin_amdgcn_perm(C64, e03, 0x04030402u),
-                                       __builtin_amdgcn_perm(C64, e47, 0x04010400u),
-                                       __builtin_amdgcn_perm(C64, e47, 0x04030402u)};
-                } else {
-                    uint4_t r;
-#pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        r[t] = bitcast<uint32_t>((bitcast<half2_t>(uu[unit][t]) - off) * d2[uj]);
-                    Bn[uk][uj] = bitcast<half8_t>(r);
-                }
-            }
+            if (idx >= 2) second(idx - 2);
+            if (idx >= 1) first(idx - 1);
             __builtin_amdgcn_sched_barrier(0);
         }
+        second(NMF - 2);
+        first(NMF - 1);
+        second(NMF - 1);
     };
 
     // Prologue: stages 0, 1, 2 in flight; stage 0 landed for every wave.
@@ -423,9 +452,10 @@ static int gemm6_splits(int64_t M, int64_t K, int64_t N) {
     return S;
 }
 
-bool gemm6_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N) {
+bool gemm6_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N) {
+    // Buffer loads: activations below 2^31 bytes, W below 2^31 bytes.
     return N % 128 == 0 && ((uintptr_t)W % 16) == 0 && ((uintptr_t)X % 16) == 0 && ldx % 8 == 0 &&
-           K >= QK;
+           K >= QK && M * ldx < ((int64_t)1 << 30) && (K / QK) * N * BLOCK_BYTES < ((int64_t)1 << 31);
 }
 
 size_t gemm6_workspace_bytes(int64_t M, int64_t K, int64_t N) {

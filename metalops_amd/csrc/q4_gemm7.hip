@@ -423,7 +423,7 @@ size_t gemm7_workspace_bytes(int64_t M, int64_t K, int64_t N) {
 // gemm6's shape rules, plus byte offsets that fit 31 bits (the copies address X
 // and W through buffer resources with 32-bit offsets and sizes).
 bool gemm7_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N) {
-    return gemm6_supported(X, ldx, W, K, N) && M * ldx * 2 < ((int64_t)1 << 31) &&
+    return gemm6_supported(X, ldx, W, M, K, N) && M * ldx * 2 < ((int64_t)1 << 31) &&
            (K / QK) * N * BLOCK_BYTES < ((int64_t)1 << 31);
 }
 

@@ -27,8 +27,9 @@ struct Gemm6Args {
     uint32_t foreign = 0;    // splits treated as run on another XCD (test switch)
 };
 
-// Needs N % 128 == 0, 16-byte aligned W and activation rows, K >= 32.
-bool gemm6_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t K, int64_t N);
+// Needs N % 128 == 0, 16-byte aligned W and activation rows, K >= 32, M * ldx <
+// 2^30 and W below 2^31 bytes (buffer loads).
+bool gemm6_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N);
 size_t gemm6_workspace_bytes(int64_t M, int64_t K, int64_t N);
 hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y,
                         int64_t ldy, int M, int K, int N, void *ws, hipStream_t s);
@@ -36,7 +37,7 @@ hipError_t launch_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
 // Few-tile prefill GEMM (q4_gemm8): 128 x 128 tiles, eight waves with K split
 // four ways inside the workgroup, at most two K splits across workgroups
 // summed through the XCD's L2 (partials [tiles][2][128*128] after the ticket
-// area).  Needs N % 128 == 0, 16-byte aligned W and activation rows, K >= 32.
+// area).  Needs what q4_gemm6 needs.
 constexpr int G8_BM = 128;
 constexpr int G8_BN = 128;
 bool gemm8_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M, int64_t K, int64_t N);
