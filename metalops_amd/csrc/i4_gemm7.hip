@@ -88,7 +88,9 @@ i4_gemm7_kernel(I4GemmArgs a) {
     const int a_c0 = (lane ^ (lane >> 4)) & 7, a_c1 = (lane ^ (4 + (lane >> 4))) & 7;
     const int x_row = (int)a.ldx * 2;
     const uint8_t *x_base = (const uint8_t *)(a.X + (int64_t)m0 * a.ldx + (int64_t)k_lo * 32);
-    const int x_bytes = (int)((int64_t)(a.M - m0) * x_row - (int64_t)k_lo * 32 * 2);
+    // Readable from x_base: up to the last row's K-th element (its row padding
+    // past K need not be allocated).
+    const int x_bytes = (int)((int64_t)(a.M - m0 - 1) * x_row + ((int64_t)a.nsteps - k_lo) * 32 * 2);
     const int vo_a0 = (64 * wave + (lane >> 3)) * x_row + 16 * (a_c0 & 3) + 64 * (a_c0 >> 2);
     const int vo_a1 = (64 * wave + (lane >> 3)) * x_row + 16 * (a_c1 & 3) + 64 * (a_c1 >> 2);
 

@@ -79,12 +79,16 @@ q4_gemm6_kernel(Gemm6Args a) {
     // A copy u of this wave: positions 64(wave*A_LD+u) + lane = row 8(wave*A_LD+u) + lane/8,
     // chunk (lane ^ lane/8) & 7 (the same for every u): K step a_t = chunk/4 of
     // the stage, halves 8 (chunk % 4) .. +7 of it.  All copies are buffer loads
-    // into LDS whose lane offsets are fixed and whose stage offsets are scalars.
+    // into LDS.  An activation copy's offset (lane part fixed, plus the stage's
+    // K offset) is a VGPR, so the resource's size -- the activations' last byte
+    // -- bounds it: the hardware's range check leaves out the scalar offset.
+    // A weight copy's K block is clamped to the split and its offset is a
+    // scalar.
     const int a_c = (lane ^ (lane >> 3)) & 7;
     const int a_t = a_c >> 2;
     const int a_r0 = m0 + 8 * wave * A_LD + (lane >> 3);
     const __amdgpu_buffer_rsrc_t a_rs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)a.X, (short)0, (int)((int64_t)a.M * a.ldx * 2), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.X, (short)0, (int)(((int64_t)(a.M - 1) * a.ldx + (int64_t)a.nb * QK) * 2), 0x00020000);
     uint32_t a_vo[A_LD];
 #pragma unroll
     for (int u = 0; u < A_LD; ++u) {
@@ -107,12 +111,13 @@ q4_gemm6_kernel(Gemm6Args a) {
     // cannot pack the remainder.  Weight steps past the split's end re-copy its
     // last step; activation steps past it are read (zero past the activations'
     // last byte) but feed no MFMA.  The instruction's immediate offset would
-    // move the LDS destination too, so piece offsets go into the scalar offset.
+    // move the LDS destination too, so the weights' piece offsets go into the
+    // scalar offset.
     auto issue_one = [&](int s_dst, int ci) {
         if (ci < A_LD) {
             uint8_t *dst = sA + (s_dst % G6_NS) * A_SLOT + wave * (A_LD * 1024) + 1024 * ci;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (__attribute__((address_space(3))) void *)dst, 16,
-                                                     a_vo[ci], (uint32_t)(k_lo + 2 * s_dst) * (QK * 2), 0, 0);
+                                                     a_vo[ci] + (uint32_t)(k_lo + 2 * s_dst) * (QK * 2), 0, 0, 0);
             return;
         }
         const int r = ci - A_LD, t = r >> 1;

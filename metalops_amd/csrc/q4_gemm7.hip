@@ -95,7 +95,9 @@ q4_gemm7_kernel(Gemm7Args a) {
     // Byte counts fit 31 bits (launch_gemm7 checks X and W).
     const int x_row = (int)a.ldx * 2;
     const uint8_t *x_base = (const uint8_t *)(a.X + (int64_t)m0 * a.ldx + (int64_t)k_lo * QK);
-    const int x_bytes = (int)((int64_t)(a.M - m0) * x_row - (int64_t)k_lo * QK * 2);   // readable from x_base
+    // Readable from x_base: up to the last row's K-th element (its row padding
+    // past K need not be allocated).
+    const int x_bytes = (int)((int64_t)(a.M - m0 - 1) * x_row + ((int64_t)a.nb - k_lo) * QK * 2);
     const int vo_a0 = (64 * wave + (lane >> 3)) * x_row + 16 * (a_c0 & 3) + 64 * (a_c0 >> 2);
     const int vo_a1 = (64 * wave + (lane >> 3)) * x_row + 16 * (a_c1 & 3) + 64 * (a_c1 >> 2);
 

@@ -18,8 +18,9 @@
 //     MFMAs.  The weights of stage t go out with the activations of stage
 //     t - G8_WD (G8_NS = 4 and G8_WD = -1: activations three stages ahead,
 //     weights two; 54.9 against 55.7 us for 3 and +2).
-//   * All copies are buffer loads into LDS with the lane's offset fixed and the
-//     stage's K offset in a scalar register: no address arithmetic per copy.
+//   * All copies are buffer loads into LDS: one add per activation copy (its
+//     VGPR offset, which the resource's size bounds), scalar offsets for the
+//     weights.
 //   * One barrier per stage; stage s + G8_NS's activations go out during stage s.
 //   * End: the four phases' accumulators are summed in LDS (reduce-scatter:
 //     wave (wn, ph) ends with rows 32 ph .. 32 ph + 31 of its columns), so the
@@ -118,13 +119,14 @@ q4_gemm8_kernel(Gemm6Args a) {
     // fills row 4 (A_LD wave + u) + l/16 (A_LD even) at position l % 16 with chunk
     // (l % 16) ^ (row & 7) = (l % 16) ^ (4 (u & 1) + l/16).  Chunk c is K block
     // 4s + c/4 of the stage, halves 8 (c % 4) .. +7 of it.  Buffer loads: the
-    // lane's byte offset is fixed, the stage's K offset is a scalar; K blocks
-    // past the split's end are read but used by no MFMA (the phases they
-    // belong to skip their last stage), and reads past the activations'
-    // last byte return zero.
+    // lane's byte offset plus the stage's K offset is the VGPR offset, which
+    // the hardware checks against the resource's size (the activations' last
+    // byte; the scalar offset is outside that check), so reads past the end
+    // return zero.  K blocks past the split's end are read but used by no MFMA
+    // (the phases they belong to skip their last stage).
     const int a_ce = (lane & 15) ^ (lane >> 4), a_co = a_ce ^ 4;
     const __amdgpu_buffer_rsrc_t a_rs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)a.X, (short)0, (int)((int64_t)a.M * a.ldx * 2), 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.X, (short)0, (int)(((int64_t)(a.M - 1) * a.ldx + (int64_t)a.nb * QK) * 2), 0x00020000);
     uint32_t a_vo[A_LD];
 #pragma unroll
     for (int u = 0; u < A_LD; ++u) {
@@ -150,8 +152,8 @@ q4_gemm8_kernel(Gemm6Args a) {
     // Weight K blocks past the split's end re-copy its last block.
     auto issue_a = [&](int s_dst, int u) {
         uint8_t *dst = sA + (s_dst % G8_NS) * G8_A_SLOT + (A_LD * wave + u) * 1024;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (__attribute__((address_space(3))) void *)dst, 16, a_vo[u],
-                                                 (uint32_t)(k_lo + G8_PH * s_dst) * (QK * 2), 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(a_rs, (__attribute__((address_space(3))) void *)dst, 16,
+                                                 a_vo[u] + (uint32_t)(k_lo + G8_PH * s_dst) * (QK * 2), 0, 0, 0);
     };
     auto issue_w = [&](int s_w, int r) {
         const uint32_t so = w_so0 + (uint32_t)min(G8_PH * s_w + ph, nk - 1) * row_bytes;
