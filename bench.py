@@ -91,7 +91,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0)
     p.add_argument("--no-graph", action="store_true", help="eager launches instead of a HIP graph")
     p.add_argument("--part", choices=["all", "decode", "prefill", "configs", "copy", "int4-decode",
-                                      "int4-prefill", "probes", "prefill-splits"], default="all",
+                                      "int4-prefill", "probes", "prefill-splits", "prefill-routing"],
+                   default="all",
                    help="run one part only (for profiler passes); 'copy' runs a plain 256 MiB "
                         "device copy that calibrates the FETCH_SIZE / WRITE_SIZE counters; "
                         "'probes' runs the machine probes of libmcq4_bench.so (launch floor, "
@@ -214,6 +215,42 @@ def prefill_split_sweep(mo, torch, dev):
                 os.environ.pop(k, None)
             else:
                 os.environ[k] = v
+        _lib.reload_options()
+    return out
+
+
+# Prefill shapes around the few-tile GEMM's routing rule (q4_gemm8 when its plan is one
+# round of 192..256 workgroups): inside the rule, and just outside it on either side.
+ROUTING_SHAPES = [(384, 4096, 4096), (384, 11008, 4096), (512, 4096, 4096), (512, 11008, 4096),
+                  (512, 14336, 4096), (768, 4096, 4096), (1024, 4096, 4096), (1024, 14336, 4096),
+                  (256, 4096, 14336), (256, 11008, 4096), (1536, 4096, 4096), (512, 4096, 14336),
+                  (1024, 4096, 11008), (2048, 4096, 4096), (768, 4096, 14336), (1280, 4096, 8192),
+                  (640, 4096, 11008)]
+
+
+def prefill_routing_sweep(mo, torch, dev):
+    """Each ROUTING_SHAPES point under the default plan and under each prefill kernel
+    forced (MCQ4_GEMM_PATH=6|7|8, each with its own split plan): microseconds per
+    launch, graph replays over rotated weight copies."""
+    from metalops_amd import _lib
+    saved = os.environ.get("MCQ4_GEMM_PATH")
+    out = []
+    try:
+        for M, K, N in ROUTING_SHAPES:
+            rec = {"M": M, "K": K, "N": N}
+            for name, path in (("default", None), ("gemm6", "6"), ("gemm7", "7"), ("gemm8", "8")):
+                os.environ.pop("MCQ4_GEMM_PATH", None)
+                if path:
+                    os.environ["MCQ4_GEMM_PATH"] = path
+                _lib.reload_options()
+                t, _, _ = shape_bench(mo, torch, dev, M, K, N, reps=5)
+                rec[name + "_us"] = round(t * 1e6, 2)
+            out.append(rec)
+            print(json.dumps(rec), file=sys.stderr, flush=True)
+    finally:
+        os.environ.pop("MCQ4_GEMM_PATH", None)
+        if saved is not None:
+            os.environ["MCQ4_GEMM_PATH"] = saved
         _lib.reload_options()
     return out
 
@@ -830,6 +867,8 @@ def run_part(mo, torch, dev, args):
               flush=True)
     elif args.part == "prefill-splits":
         print(json.dumps({"part": "prefill-splits", "points": prefill_split_sweep(mo, torch, dev)}), flush=True)
+    elif args.part == "prefill-routing":
+        print(json.dumps({"part": "prefill-routing", "points": prefill_routing_sweep(mo, torch, dev)}), flush=True)
     else:
         print(json.dumps({"part": "prefill", "configs": prefill_bench(mo, torch, dev)}), flush=True)
 

@@ -94,28 +94,28 @@ Prefill prefill_kernel(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t
         if (env[0] == '7' && mcq4::gemm7_supported(X, ldx, W, M, K, N)) return Prefill::Wide7;
         if (env[0] == '8' && mcq4::gemm8_supported(X, ldx, W, M, K, N)) return Prefill::Few8;
     }
-    // The 256 x 256-tile GEMM (one wave per SIMD, half the dequant per MFMA)
-    // wins once its grid nearly fills the 256 CUs, or with half of that on long
-    // K where two K splits and their reduction cost little; the 128 x 256-tile
-    // q4_gemm6 is faster on smaller grids.  Measured (us, q4_gemm6 / q4_gemm7):
-    // M=2048 4096x14336 244 / 213, 14336x4096 235 / 209, 4096x4096 71 / 80;
-    // M=512 4096x128256 513 / 485, 11008x4096 57 / 61; M=1024 4096x14336
-    // 117 / 111; M=256 4096x14336 46 / 47.
+    // Measured (us per launch, `python bench.py --part prefill-routing`, one box;
+    // default / q4_gemm6 / q4_gemm7 / q4_gemm8 forced):
+    //   M=512 11008x4096 55.8 / 59.5 / 64.1 / 56.5, 4096x4096 29.3 / 31.7 / 35.6 / 29.3
+    //   M=768 4096x4096 35.1 / 43.9 / 43.6 / 35.0; M=1024 4096x4096 40.8 / 50.2 / 53.2 / 41.0
+    //   M=256 4096x14336 39.7 / 46.7 / 49.1 / 39.7
+    //   M=1024 4096x11008 96.1 / 109.0 / 96.4 / 116.1; M=768 4096x14336 94.7 / 107.9 / 94.8 / 114.8
+    //   M=1280 4096x8192 92.2 / 106.2 / 92.4 / 111.6
+    //   M=640 4096x11008 69.9 / 69.1 / 85.8 / 75.7; M=1536 4096x4096 63.3 / 63.2 / 65.3 / 72.6
+    //   M=256 11008x4096 38.0 / 38.6 / 43.6 / 41.1; M=2048 4096x4096 75.0 / 75.1 / 81.0 / 81.5
     // The few-tile GEMM (128 x 128 tiles, eight waves, K split four ways
-    // inside the workgroup and at most twice across) wins when its grid is one
-    // round of 192..256 workgroups.  Measured (us, default / q4_gemm8): M=512
-    // 11008x4096 58.8 / 55.1, 14336x4096 76.1 / 68.3, 4096x4096 31.6 / 28.7;
-    // M=384 11008x4096 51.1 / 47.5; M=768 4096x4096 44.9 / 34.1; M=1024
-    // 4096x4096 50.3 / 40.2, 14336x4096 130.2 / 118.7; M=256 4096x14336
-    // 47.0 / 39.3.  Outside that range it loses (M=1536 4096x4096 64.9 / 71.6,
-    // M=256 11008x4096 37.8 / 42.2, M=512 4096x14336 70.5 / 73.2).
+    // inside the workgroup and at most twice across) wins when its plan is one
+    // round of 192..256 workgroups, and loses with more rounds or a half-empty
+    // grid.  The 256 x 256-tile GEMM (one wave per SIMD, half the dequant per
+    // MFMA) wins from 160 tiles, or from 96 on long K where two K splits and
+    // their reduction cost little; the 128 x 256-tile q4_gemm6 below that.
     if (ok6 && mcq4::gemm8_supported(X, ldx, W, M, K, N)) {
         const int g8 = mcq4::gemm8_workgroups(M, K, N);
         if (g8 >= 192 && g8 <= 256) return Prefill::Few8;
     }
     if (ok6 && mcq4::gemm7_supported(X, ldx, W, M, K, N)) {
         const int64_t t7 = ((M + 255) / 256) * ((N + 255) / 256);
-        if (t7 >= 192 || (t7 >= 96 && K >= 8192)) return Prefill::Wide7;
+        if (t7 >= 160 || (t7 >= 96 && K >= 8192)) return Prefill::Wide7;
     }
     if (ok6) return Prefill::Staged6;
     if (ok2 && ((M + 127) / 128) * ((N + 255) / 256) >= 128) return Prefill::Async2;
