@@ -123,7 +123,7 @@ i4_gemm_kernel(I4GemmArgs a) {
             __builtin_amdgcn_global_load_lds(
                 (void *)(src + (int64_t)8 * c * N),
                 (__attribute__((address_space(3))) void *)(dst + 1024 * c), 16, 0, 0);
-        const int64_t grp = (k_lo + k) / a.spg;
+        const int64_t grp = i4_group_of(k_lo + k, a.spg_magic, a.spg_ident);
         if (sz_lane)
             __builtin_amdgcn_global_load_lds(
                 (void *)(sz_src + grp * N * ESZ),
@@ -459,7 +459,7 @@ hipError_t launch_i4_gemm(const _Float16 *X, int64_t ldx, const uint8_t *P, cons
     const I4GCfg c = i4_gemm_config(M, K, N);
     I4GemmArgs a;
     a.X = X; a.ldx = ldx; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y; a.ldy = ldy;
-    a.M = M; a.nsteps = K / 32; a.N = N; a.spg = gs / 32;
+    a.M = M; a.nsteps = K / 32; a.N = N; a.spg = gs / 32; a.spg_magic = i4_spg_magic(a.spg); a.spg_ident = i4_spg_ident(a.spg);
     a.tiles_n = (N + I4G_BN - 1) / I4G_BN;
     a.tiles_m = (M + c.bm - 1) / c.bm;
     a.S = c.S;

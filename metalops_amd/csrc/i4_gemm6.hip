@@ -114,7 +114,7 @@ i4_gemm6_kernel(I4GemmArgs a) {
             __builtin_amdgcn_global_load_lds((void *)(w_k + (int64_t)step * 16 * N),
                                              (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
         } else {
-            const int64_t grp = (k_lo + step) / a.spg;
+            const int64_t grp = i4_group_of(k_lo + step, a.spg_magic, a.spg_ident);
             __builtin_amdgcn_global_load_lds((void *)(sz_base + grp * N * 2),
                                              (__attribute__((address_space(3))) void *)(dst + J6_RAW), 4, 0, 0);
         }
@@ -428,7 +428,7 @@ hipError_t launch_i4_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *P, con
     I4GemmArgs a;
     a.foreign = split_foreign_mask();
     a.X = X; a.ldx = ldx; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y; a.ldy = ldy;
-    a.M = M; a.nsteps = K / 32; a.N = N; a.spg = gs / 32;
+    a.M = M; a.nsteps = K / 32; a.N = N; a.spg = gs / 32; a.spg_magic = i4_spg_magic(a.spg); a.spg_ident = i4_spg_ident(a.spg);
     a.tiles_n = (N + I4G_BN - 1) / I4G_BN;
     a.tiles_m = (M + J6_BM - 1) / J6_BM;
     a.S = c.S;

@@ -54,6 +54,13 @@ __device__ __forceinline__ void j7_copy16(const uint8_t *base, int off, int byte
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16, voff, 0, 0, 0);
 }
 
+// One 16-byte-per-lane weight copy into LDS: P's bytes at the scalar offset
+// `so` (the K step, clamped to the split) plus the lane's fixed offset.
+__device__ __forceinline__ void j7_copy_w(const uint8_t *P, uint32_t so, uint8_t *dst, uint32_t voff) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)P, (short)0, 0x7fffffff, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16, voff, so, 0, 0);
+}
+
 template <int SZ, int ACT>
 __global__ void __launch_bounds__(256, 1)
 i4_gemm7_kernel(I4GemmArgs a) {
@@ -99,7 +106,10 @@ i4_gemm7_kernel(I4GemmArgs a) {
     // wave wholly past N (N % 256 == 128) copies column 0 instead.
     const int wcol0 = n0 + wave * J7_WN;
     const int wcol = wcol0 < N ? wcol0 : 0;
-    const uint8_t *w_k = a.P + (int64_t)k_lo * 16 * N + (int64_t)(lane >> 2) * N + wcol + 16 * (lane & 3);
+    // Byte offsets fit 31 bits (i4_gemm7_supported): the weights' K step is a
+    // scalar offset, a scale group a 32-bit scalar added to the lane's pointer.
+    const uint32_t w_vo = (uint32_t)(lane >> 2) * (uint32_t)N + 16 * (lane & 3);
+    const uint32_t w_so0 = (uint32_t)k_lo * 16 * (uint32_t)N + (uint32_t)wcol;
     const uint8_t *sz_base = (const uint8_t *)(lane < 32 ? a.scales : a.zeros) + (int64_t)wcol * 2 + 4 * (lane & 31);
 
     // Copy ci of a t = 0 step: ci = 0..7 the A rows 8 ci .. of this wave's 64 of
@@ -119,11 +129,10 @@ i4_gemm7_kernel(I4GemmArgs a) {
         const int step = min(2 * s_src + t, nk - 1);
         uint8_t *dst = ring + ((2 * s_r + t) & (J7_RAW_N - 1)) * J7_SLOT;
         if ((r & 1) == 0) {
-            __builtin_amdgcn_global_load_lds((void *)(w_k + (int64_t)step * 16 * N),
-                                             (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+            j7_copy_w(a.P, w_so0 + (uint32_t)step * 16 * (uint32_t)N, dst, w_vo);
         } else {
-            const int64_t grp = (k_lo + step) / a.spg;
-            __builtin_amdgcn_global_load_lds((void *)(sz_base + grp * N * 2),
+            const uint32_t grp = (uint32_t)i4_group_of(k_lo + step, a.spg_magic, a.spg_ident);
+            __builtin_amdgcn_global_load_lds((void *)(sz_base + grp * (uint32_t)(2 * N)),
                                              (__attribute__((address_space(3))) void *)(dst + J7_RAW), 4, 0, 0);
         }
     };
@@ -339,9 +348,10 @@ static int i4_gemm7_splits(int64_t M, int64_t K, int64_t N) {
     return S;
 }
 
-// i4_gemm6's shape rules, a grid that nearly fills the CUs (the rule q4_gemm7
-// uses: at least 192 tiles of 256 x 256, or 96 with K >= 8192), and byte
-// offsets of X that fit 31 bits (its copies use buffer resources).
+// i4_gemm6's shape rules, a grid that nearly fills the CUs (at least 192 tiles
+// of 256 x 256, or 96 with K >= 8192), and byte offsets of X, the packed
+// weights and the scales that fit 31 bits (its copies use buffer resources and
+// 32-bit scalar offsets).
 // MCQ4_I4_GEMM7=0 disables it.
 bool i4_gemm7_supported(int wb, int sz_dt, int64_t M, int64_t K, int64_t N, int64_t gs, const _Float16 *X,
                         int64_t ldx, const void *Y, int64_t ldy) {
@@ -349,7 +359,8 @@ bool i4_gemm7_supported(int wb, int sz_dt, int64_t M, int64_t K, int64_t N, int6
     const int64_t t = ((M + J7_BM - 1) / J7_BM) * ((N + I4G_BN - 1) / I4G_BN);
     return wb == 4 && (sz_dt == DT_F16 || sz_dt == DT_BF16) && N % 128 == 0 && K % 32 == 0 && gs % 32 == 0 &&
            ((uintptr_t)X % 16) == 0 && ldx % 8 == 0 && ((uintptr_t)Y % 4) == 0 && ldy % 2 == 0 &&
-           M * ldx * 2 < ((int64_t)1 << 31) && (t >= 192 || (t >= 96 && K >= 8192));
+           M * ldx * 2 < ((int64_t)1 << 31) && (K / 2) * N < ((int64_t)1 << 31) &&
+           ((K + gs - 1) / gs) * N * 2 < ((int64_t)1 << 31) && (t >= 192 || (t >= 96 && K >= 8192));
 }
 
 size_t i4_gemm7_workspace_bytes(int64_t M, int64_t K, int64_t N) {
@@ -390,7 +401,7 @@ hipError_t launch_i4_gemm7(const _Float16 *X, int64_t ldx, const uint8_t *P, con
                            int gs, int act, void *ws, hipStream_t s) {
     I4GemmArgs a;
     a.X = X; a.ldx = ldx; a.P = P; a.scales = scales; a.zeros = zeros; a.Y = Y; a.ldy = ldy;
-    a.M = M; a.nsteps = K / 32; a.N = N; a.spg = gs / 32;
+    a.M = M; a.nsteps = K / 32; a.N = N; a.spg = gs / 32; a.spg_magic = i4_spg_magic(a.spg); a.spg_ident = i4_spg_ident(a.spg);
     a.tiles_n = (N + I4G_BN - 1) / I4G_BN;
     a.tiles_m = (M + J7_BM - 1) / J7_BM;
     a.S = i4_gemm7_splits(M, K, N);
