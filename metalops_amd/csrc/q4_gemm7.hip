@@ -125,6 +125,7 @@ q4_gemm7_kernel(Gemm7Args a) {
     // per lane still fill 4 bytes per lane).  Stages past the end re-copy the
     // last stage, so every stage issues the same number of copies and the vmcnt
     // waits are exact.
+    const __amdgpu_buffer_rsrc_t w_rs = rsrc(w_base, 0, w_bytes);
     auto issue_one = [&](int s_a, int as_, int s_r, int ci) {
         if (ci < A_LD) {
             const int s_src = min(s_a, nst - 1);
@@ -136,14 +137,16 @@ q4_gemm7_kernel(Gemm7Args a) {
         }
         const int s_src = min(s_r, nst - 1);
         const int r = ci - A_LD, t = r >> 1;
-        const __amdgpu_buffer_rsrc_t rw = rsrc(w_base, min(2 * s_src + t, nk - 1) * row_bytes, w_bytes);
+        // The K block is clamped to the split, so the weights' offset can be the
+        // scalar one (outside the range check) of a single resource.
+        const uint32_t so = (uint32_t)(min(2 * s_src + t, nk - 1) * row_bytes);
         uint8_t *dst = ring + ((2 * s_r + t) & (G7_RAW_N - 1)) * G7_RAW_SLOT;
         if ((r & 1) == 0)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void *)dst, 16,
-                                                     vo_w0, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rs, (__attribute__((address_space(3))) void *)dst, 16,
+                                                     vo_w0, so, 0, 0);
         else
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (__attribute__((address_space(3))) void *)(dst + 1024),
-                                                     4, vo_w1, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rs, (__attribute__((address_space(3))) void *)(dst + 1024),
+                                                     4, vo_w1, so, 0, 0);
     };
 
     const int lrow = lane & 31, lhi = lane >> 5;
