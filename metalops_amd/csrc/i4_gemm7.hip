@@ -348,19 +348,22 @@ static int i4_gemm7_splits(int64_t M, int64_t K, int64_t N) {
     return S;
 }
 
-// i4_gemm6's shape rules, a grid that nearly fills the CUs (at least 192 tiles
-// of 256 x 256, or 96 with K >= 8192), and byte offsets of X, the packed
+// i4_gemm6's shape rules, a grid that nearly fills the CUs (at least 160 tiles
+// of 256 x 256, or 96 with K >= 8192; us, i4_gemm6 / this kernel: M=1024
+// 4096x11008 113.1 / 103.2, M=768 4096x14336 112.1 / 100.7, M=1280 4096x8192
+// 110.9 / 99.9, M=640 4096x11008 (129 tiles) 74.9 / 95.2), and byte offsets of X, the packed
 // weights and the scales that fit 31 bits (its copies use buffer resources and
 // 32-bit scalar offsets).
-// MCQ4_I4_GEMM7=0 disables it.
+// MCQ4_I4_GEMM7=0 disables it, =1 takes it whatever the grid (tests).
 bool i4_gemm7_supported(int wb, int sz_dt, int64_t M, int64_t K, int64_t N, int64_t gs, const _Float16 *X,
                         int64_t ldx, const void *Y, int64_t ldy) {
     if (opt_is("MCQ4_I4_GEMM7", '0')) return false;
+    const bool force = opt_is("MCQ4_I4_GEMM7", '1');
     const int64_t t = ((M + J7_BM - 1) / J7_BM) * ((N + I4G_BN - 1) / I4G_BN);
     return wb == 4 && (sz_dt == DT_F16 || sz_dt == DT_BF16) && N % 128 == 0 && K % 32 == 0 && gs % 32 == 0 &&
            ((uintptr_t)X % 16) == 0 && ldx % 8 == 0 && ((uintptr_t)Y % 4) == 0 && ldy % 2 == 0 &&
            M * ldx * 2 < ((int64_t)1 << 31) && (K / 2) * N < ((int64_t)1 << 31) &&
-           ((K + gs - 1) / gs) * N * 2 < ((int64_t)1 << 31) && (t >= 192 || (t >= 96 && K >= 8192));
+           ((K + gs - 1) / gs) * N * 2 < ((int64_t)1 << 31) && (force || t >= 160 || (t >= 96 && K >= 8192));
 }
 
 size_t i4_gemm7_workspace_bytes(int64_t M, int64_t K, int64_t N) {

@@ -32,7 +32,7 @@ const char *const kNames[] = {
     "MCQ4_I4_GEMV1",        // 0 | 1 | 4: async-copy decode GEMV routing
     "MCQ4_I4_SPW1",         // steps per wave of the async-copy decode GEMV
     "MCQ4_I4_GEMM6",        // 0: the barrier-free prefill kernel
-    "MCQ4_I4_GEMM7",        // 0: no 256 x 256-tile prefill kernel
+    "MCQ4_I4_GEMM7",        // 0: no 256 x 256-tile prefill kernel; 1: that kernel whatever the grid
 };
 constexpr int kN = sizeof(kNames) / sizeof(kNames[0]);
 

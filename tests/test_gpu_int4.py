@@ -270,7 +270,7 @@ def test_gemm6_split2_exchange_matches_reduce(mo, dev, monkeypatch, M, K, N, act
         _check_rows(Y.float().cpu().numpy(), base)
 
 
-# i4_gemm7 (256 x 256 tiles): grids of 192+ tiles, or 96+ with K >= 8192 (two
+# i4_gemm7 (256 x 256 tiles): grids of 160+ tiles, or 96+ with K >= 8192 (two
 # K splits summed by the reduction kernel); ragged M, N % 256 == 128 (waves past
 # N), group sizes 32..128, bf16 scales, fused activations.
 GEMM7_CASES = [
@@ -301,6 +301,20 @@ def test_gemm7(mo, dev, monkeypatch, M, K, N, gs, sz, act):
     monkeypatch.setenv("MCQ4_I4_GEMM7", "0")
     Y6 = f(X, packed, s, z, gs)
     _check_rows(Y6.float().cpu().numpy(), base)
+
+
+@pytest.mark.parametrize("M,K,N,gs", [(300, 1024, 768, 128), (129, 2048, 2560, 64), (1024, 4096, 2816, 128)])
+def test_gemm7_forced(mo, dev, monkeypatch, M, K, N, gs):
+    """i4_gemm7 taken below its grid rule (MCQ4_I4_GEMM7=1): ragged M, a handful
+    of tiles, N % 256 == 0 and == 128 (waves past N)."""
+    print(f"i4_gemm7 forced M={M} K={K} N={N} gs={gs}", flush=True)
+    for k in ("MCQ4_I4_GEMM6", "MCQ4_I4_PATH", "MCQ4_XCD_LOCAL"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("MCQ4_I4_GEMM7", "1")
+    w, packed, s, z = _quant(mo, dev, K, N, gs, R.F16, seed=M + N)
+    X = torch.randn(M, K, generator=torch.Generator().manual_seed(M + 1)).half().to(dev)
+    Y = mo.matmul_int4(X, packed, s, z, gs)
+    _check_rows(Y.float().cpu().numpy(), _ref(X, packed, s, z, gs))
 
 
 def _silu(y):
