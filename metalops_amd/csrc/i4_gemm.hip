@@ -427,7 +427,8 @@ static I4GCfg i4_gemm_config(int64_t M, int64_t K, int64_t N) {
     return c;
 }
 
-bool i4_gemm6_supported(int wb, int sz_dt, int64_t K, int64_t N, int64_t gs, const void *Y, int64_t ldy);
+bool i4_gemm6_supported(int wb, int sz_dt, int64_t M, int64_t K, int64_t N, int64_t gs, int64_t ldx, const void *Y,
+                        int64_t ldy);
 size_t i4_gemm6_workspace_bytes(int64_t M, int64_t K, int64_t N);
 hipError_t launch_i4_gemm6(const _Float16 *X, int64_t ldx, const uint8_t *P, const void *scales,
                            const void *zeros, int sz_dt, _Float16 *Y, int64_t ldy, int M, int K, int N,
@@ -454,7 +455,7 @@ hipError_t launch_i4_gemm(const _Float16 *X, int64_t ldx, const uint8_t *P, cons
                           int N, int gs, int act, void *ws, hipStream_t s, int wb) {
     if (i4_gemm7_supported(wb, sz_dt, M, K, N, gs, X, ldx, Y, ldy))
         return launch_i4_gemm7(X, ldx, P, scales, zeros, sz_dt, Y, ldy, M, K, N, gs, act, ws, s);
-    if (i4_gemm6_supported(wb, sz_dt, K, N, gs, Y, ldy))
+    if (i4_gemm6_supported(wb, sz_dt, M, K, N, gs, ldx, Y, ldy))
         return launch_i4_gemm6(X, ldx, P, scales, zeros, sz_dt, Y, ldy, M, K, N, gs, act, ws, s);
     const I4GCfg c = i4_gemm_config(M, K, N);
     I4GemmArgs a;

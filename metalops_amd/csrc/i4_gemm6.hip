@@ -48,6 +48,15 @@ constexpr int J6_RAW_N = 2 * J6_NS;             // ring slots per wave (steps)
 constexpr size_t J6_LDS = (size_t)J6_NS * J6_BM * J6_ROWB + (size_t)4 * J6_RAW_N * J6_SLOT;
 static_assert(2 * J6_LDS <= 160 * 1024, "two workgroups per CU");
 
+// One 16-byte-per-lane buffer copy into LDS from `base` (`bytes` readable) at
+// the VGPR offset voff plus the scalar offset soff.  (A plain function: the host
+// pass of a kernel template would instantiate the buffer builtins and drop the
+// kernel.)
+__device__ __forceinline__ void j6_copy16(const void *base, int bytes, uint32_t voff, uint32_t soff, uint8_t *dst) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, bytes, 0x00020000);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void *)dst, 16, voff, soff, 0, 0);
+}
+
 template <int SZ, int ACT>
 __global__ void __launch_bounds__(256, 2)
 i4_gemm6_kernel(I4GemmArgs a) {
@@ -83,15 +92,29 @@ i4_gemm6_kernel(I4GemmArgs a) {
     uint8_t *const sA = smem;
     uint8_t *const ring = smem + J6_NS * A_SLOT + wave * (J6_RAW_N * J6_SLOT);
 
-    // A copy u of this wave: row 8(wave*A_LD+u) + lane/8, chunk (lane ^ lane/8) & 7.
+    // A copy u of this wave: row 8(wave*A_LD+u) + lane/8, chunk (lane ^ lane/8) & 7
+    // (K step a_t of the stage, halves 8 (chunk % 4) .. +7 of it).  Buffer loads
+    // (byte offsets fit 31 bits, i4_gemm6_supported): an activation copy's stage
+    // offset goes into its VGPR offset, which the resource's size (the last
+    // row's K-th element) bounds -- the scalar offset is outside the hardware's
+    // range check; steps past the split are read but feed no MFMA.
     const int a_c = (lane ^ (lane >> 3)) & 7;
     const int a_t = a_c >> 2;
     const int a_r0 = m0 + 8 * wave * A_LD + (lane >> 3);
-    const _Float16 *a_col = a.X + (int64_t)k_lo * 32 + 8 * (a_c & 3);
+    const int x_bytes = (int)(((int64_t)(a.M - 1) * a.ldx + (int64_t)a.nsteps * 32) * 2);
+    uint32_t a_vo[A_LD];
+#pragma unroll
+    for (int u = 0; u < A_LD; ++u) {
+        const int m = min(a_r0 + 8 * u, a.M - 1);
+        a_vo[u] = ((uint32_t)m * (uint32_t)a.ldx + 8 * (a_c & 3)) * 2 + a_t * 64;
+    }
 
+    // Weights: the lane's fixed offset, the K step (clamped to the split) as the
+    // scalar offset; scale groups as a 32-bit scalar added to the lane's pointer.
     const int wcol0 = n0 + wn * WN;
     const int wcol = wcol0 < N ? wcol0 : 0;       // whole wave past N: copy column 0 instead
-    const uint8_t *w_k = a.P + (int64_t)k_lo * 16 * N + (int64_t)(lane >> 2) * N + wcol + 16 * (lane & 3);
+    const uint32_t w_vo = (uint32_t)(lane >> 2) * (uint32_t)N + (uint32_t)wcol + 16 * (lane & 3);
+    const uint32_t w_so0 = (uint32_t)k_lo * 16 * (uint32_t)N;
     const uint8_t *sz_base = (const uint8_t *)(lane < 32 ? a.scales : a.zeros) + (int64_t)wcol * 2 + 4 * (lane & 31);
 
     // Copy ci (0 .. GROUP-1) of stage s_dst: the A copies, then per step t the raw
@@ -100,22 +123,17 @@ i4_gemm6_kernel(I4GemmArgs a) {
         const int s_src = min(s_dst, nst - 1);
         if (ci < A_LD) {
             uint8_t *dst = sA + (s_dst % J6_NS) * A_SLOT + wave * (A_LD * 1024) + 1024 * ci;
-            const int64_t koff = (int64_t)min(2 * s_src + a_t, nk - 1) * 32;
-            const int m = min(a_r0 + 8 * ci, a.M - 1);
-            __builtin_amdgcn_global_load_lds(
-                (void *)(a_col + (int64_t)m * a.ldx + koff),
-                (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+            j6_copy16(a.X, x_bytes, a_vo[ci] + (uint32_t)(k_lo + 2 * s_src) * 64, 0, dst);
             return;
         }
         const int r = ci - A_LD, t = r >> 1;
         const int step = min(2 * s_src + t, nk - 1);
         uint8_t *dst = ring + ((2 * s_dst + t) % J6_RAW_N) * J6_SLOT;
         if ((r & 1) == 0) {
-            __builtin_amdgcn_global_load_lds((void *)(w_k + (int64_t)step * 16 * N),
-                                             (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+            j6_copy16(a.P, 0x7fffffff, w_vo, w_so0 + (uint32_t)step * 16 * (uint32_t)N, dst);
         } else {
-            const int64_t grp = i4_group_of(k_lo + step, a.spg_magic, a.spg_ident);
-            __builtin_amdgcn_global_load_lds((void *)(sz_base + grp * N * 2),
+            const uint32_t grp = (uint32_t)i4_group_of(k_lo + step, a.spg_magic, a.spg_ident);
+            __builtin_amdgcn_global_load_lds((void *)(sz_base + grp * (uint32_t)(2 * N)),
                                              (__attribute__((address_space(3))) void *)(dst + J6_RAW), 4, 0, 0);
         }
     };
@@ -381,10 +399,13 @@ static J6Cfg i4_gemm6_config(int64_t M, int64_t K, int64_t N) {
 // 4-bit weights with 16-bit scales/zeros, plus i4_gemm's shape rules (N % 128,
 // K % 32, group % 32, 16-byte aligned operands) and 4-byte aligned Y rows.
 // MCQ4_I4_GEMM6=0 disables it.
-bool i4_gemm6_supported(int wb, int sz_dt, int64_t K, int64_t N, int64_t gs, const void *Y, int64_t ldy) {
+bool i4_gemm6_supported(int wb, int sz_dt, int64_t M, int64_t K, int64_t N, int64_t gs, int64_t ldx, const void *Y,
+                        int64_t ldy) {
     if (opt_is("MCQ4_I4_GEMM6", '0')) return false;
+    // Buffer-load copies: activations and packed weights below 2^31 bytes.
     return wb == 4 && (sz_dt == DT_F16 || sz_dt == DT_BF16) && N % 128 == 0 && K % 32 == 0 && gs % 32 == 0 &&
-           ((uintptr_t)Y % 4) == 0 && ldy % 2 == 0;
+           ((uintptr_t)Y % 4) == 0 && ldy % 2 == 0 && M * ldx < ((int64_t)1 << 30) &&
+           (K / 2) * N < ((int64_t)1 << 31) && ((K + gs - 1) / gs) * N * 2 < ((int64_t)1 << 31);
 }
 
 size_t i4_gemm6_workspace_bytes(int64_t M, int64_t K, int64_t N) {
