@@ -489,7 +489,8 @@ def test_matmul_grouped_other_cases(dev):
 
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 8192), (3, 2048, 8208), (6, 1024, 12288), (12, 4096, 16384),
                                    (4, 16384, 1024), (16, 8192, 4096), (1, 4096, 4096), (5, 4096, 4096),
-                                   (24, 2048, 1024), (40, 1024, 2048), (300, 2048, 512)])
+                                   (24, 2048, 1024), (40, 1024, 2048), (300, 2048, 512), (512, 4096, 4096),
+                                   (1024, 2048, 4096), (256, 1024, 40960)])
 def test_matmul_capi_row_strides(dev, M, K, N):
     """The C entry point with row strides past K and N on both sides (ldx = K + 40,
     ldy = N + 24) across the decode and prefill kernels: outputs match the oracle
@@ -513,3 +514,34 @@ def test_matmul_capi_row_strides(dev, M, K, N):
     Yc = Y.float().cpu().numpy()
     assert (Yc[:, N:] == 7.0).all()
     _check_rows(Yc[:, :N], ref.matmul_f32(Xw[:, :K].contiguous().numpy(), blocks))
+
+
+@pytest.mark.parametrize("path", ["6", "7", "8"])
+@pytest.mark.parametrize("M,K,N", [(300, 1056, 1024), (129, 2080, 2304)])
+def test_prefill_tight_activation_storage(dev, monkeypatch, path, M, K, N):
+    """Prefill kernels on activations whose storage ends at the last row's K-th
+    element (row stride K + 40, no padding after the last row): the copies past a
+    split's K range must stay inside that storage (reads past it return zero and
+    feed no MFMA), and the outputs match the oracle."""
+    from metalops_amd import _lib
+    print(f"tight activations path={path} M={M} K={K} N={N}", flush=True)
+    for k in ("MCQ4_GEMM_PATH", "MCQ4_GEMM6_SPLIT", "MCQ4_GEMM8_SPLIT", "MCQ4_XCD_LOCAL"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("MCQ4_GEMM_PATH", path)
+    ldx = K + 40
+    W = _weights(K, N, seed=M + K + N, outliers=True)
+    blocks = ref.quantize_llama_rule(W.numpy())
+    X = _acts(M, K, seed=M + 9)
+    flat = torch.zeros((M - 1) * ldx + K, dtype=torch.float16)
+    flat.as_strided((M, K), (ldx, 1)).copy_(X)
+    Xd = flat.to(dev)
+    bd = torch.from_numpy(blocks).to(dev)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    need = _lib.lib.mcq4_matmul_workspace_bytes(M, K, N)
+    ws = torch.zeros(max(need, 16), dtype=torch.uint8, device=dev)
+    st = _lib.lib.mcq4_matmul_q4_0_f16(Xd.data_ptr(), ldx, bd.data_ptr(), Y.data_ptr(), N, M, K, N,
+                                       ws.data_ptr() if need else None, need,
+                                       torch.cuda.current_stream().cuda_stream)
+    assert st == 0, _lib.lib.mcq4_last_error()
+    torch.cuda.synchronize()
+    _check_rows(Y.float().cpu().numpy(), ref.matmul_f32(X.numpy(), blocks))
