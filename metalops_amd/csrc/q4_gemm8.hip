@@ -41,7 +41,7 @@ namespace mcq4 {
 
 MCQ4_SPLIT_FALLBACK_COUNTER(q4_gemm8_split_fallbacks)
 
-constexpr int G8_PH = 4;                          // K phases = waves per workgroup
+constexpr int G8_PH = 4;                          // K phases per workgroup
 #ifdef G8_NS_SET
 constexpr int G8_NS = G8_NS_SET;
 #else
@@ -66,7 +66,8 @@ constexpr int g8_raw_slot(int cw) { return cw == 1 ? 18 * G8_BN : 1280; }
 // + 16: the B operand reads of the last ring slot run up to 4 bytes past it.
 constexpr size_t g8_lds(int cw) {
     const size_t pipe = (size_t)G8_NS * G8_A_SLOT + (size_t)G8_PH * cw * G8_RAW_N * g8_raw_slot(cw) + 16;
-    const size_t sum = (size_t)2 * 3 * 64 * 64 * 4;   // [column group][two row blocks][3 sources] of 64 lanes x 64/cw floats x cw
+    // Phase sum: cw x 2 row blocks x 3 sources, each 64 lanes x 64 / cw floats.
+    const size_t sum = (size_t)2 * 3 * 64 * 64 * 4;
     return pipe > sum ? pipe : sum;
 }
 static_assert(g8_lds(1) <= 160 * 1024 && g8_lds(2) <= 160 * 1024, "LDS budget: one workgroup per CU");
@@ -82,7 +83,7 @@ q4_gemm8_kernel(Gemm6Args a) {
     constexpr int RAW_SLOT = g8_raw_slot(CW);
     constexpr int SUM_REGION = 64 * 16 * TN * 4;  // one wave's 32 x WN fp32 block
     constexpr int GROUP = A_LD + W_LD;            // vector-memory instructions per wave and stage
-    constexpr int NMF = 2 * TM * TN;              // MFMAs per stage (32)
+    constexpr int NMF = 2 * TM * TN;              // MFMAs per stage (16 at CW = 2)
     static_assert(2 * GROUP <= NMF, "copies ride on the stage's odd MFMAs");
     // Stage t's weights go out with stage t - G8_WD's activations, after them.
     // Copies still allowed in flight once the stage the next barrier admits has
