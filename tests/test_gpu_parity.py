@@ -420,6 +420,31 @@ def test_matmul_random_shapes(dev, M, K, N, pad):
     _check_rows(Y.float().cpu().numpy(), ref.matmul_f32(X.contiguous().numpy(), blocks))
 
 
+def _few_tile_cases(n, seed):
+    """Seeded random shapes for the few-tile GEMM forced (MCQ4_GEMM_PATH=8): M 65..700,
+    K any multiple of 32 up to 4096, N a multiple of 128 up to 2048, split plan 1 or 2."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(65, 701)), 32 * int(rng.integers(1, 129)), 128 * int(rng.integers(1, 17)),
+             int(rng.choice([8, 40])), str(rng.choice(["1", "2"]))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("M,K,N,pad,split", _few_tile_cases(16, 20261203))
+def test_matmul_few_tile_random(dev, monkeypatch, M, K, N, pad, split):
+    """q4_gemm8 on random shapes and strides (row stride K + pad) with one or two K
+    splits: against the oracle's fp32 product."""
+    print(f"few-tile random M={M} K={K} N={N} pad={pad} split={split}", flush=True)
+    for k in ("MCQ4_GEMM_PATH", "MCQ4_GEMM8_SPLIT", "MCQ4_XCD_LOCAL"):
+        monkeypatch.delenv(k, raising=False)
+    monkeypatch.setenv("MCQ4_GEMM_PATH", "8")
+    monkeypatch.setenv("MCQ4_GEMM8_SPLIT", split)
+    mo = _mo()
+    W = _weights(K, N, seed=M * 17 + K + N, outliers=True)
+    blocks = ref.quantize_llama_rule(W.numpy())
+    Xw = _acts(M, K + pad, seed=M + 2 * K + pad)
+    Y = mo.matmul_ggml_q4_0(Xw.to(dev)[:, :K], torch.from_numpy(blocks).to(dev))
+    _check_rows(Y.float().cpu().numpy(), ref.matmul_f32(Xw[:, :K].contiguous().numpy(), blocks))
+
+
 @pytest.mark.parametrize("K,N,count", [(4096, 11008, 2), (4096, 4096, 3), (352, 64, 4), (11008, 4096, 2),
                                        (4096, 32768, 2), (2080, 65536, 2), (32, 16, 2)])
 def test_matmul_grouped(dev, K, N, count):
