@@ -477,7 +477,8 @@ struct I1Cfg {
 // 9.6 us (the previous plan's 96 x 6 = 576 workgroups, two rounds of the 512
 // that fit two per CU: 10.6 us; 96 x 3: 12.1 us), gate/up 86 x 2 8.4 us (was
 // 9.8), down 32 x 8 8.6 us (was 32 x 15: 9.7), O 32 x 8 5.8 us (unchanged).
-// Deeper rings (6, 8 steps) were slower on every shape.  MCQ4_I4_SPW1 overrides
+// Deeper rings were slower on every shape: the decode layer 40.1 us with 2
+// slots, 40.8 with 3, 43.0 with 4, 46.9 with 6 (same box).  MCQ4_I4_SPW1 overrides
 // the steps per wave.
 static I1Cfg i4_gemv1_config(int64_t K, int64_t N, int64_t gs) {
     const int64_t nsteps = K / 32, spg = gs / 32, ntiles = N / I1_TC;
