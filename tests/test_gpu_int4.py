@@ -138,6 +138,8 @@ MM_CASES = [
     # prefill GEMM shapes (M > 16, N % 128 == 0)
     (17, 512, 256, 128), (64, 1024, 512, 64), (128, 4096, 1024, 128), (300, 2048, 768, 32),
     (512, 1024, 2048, 128), (33, 96, 128, 64),
+    # group sizes of 3 and 5 K steps (the scale group index by multiply-high)
+    (300, 1920, 768, 96), (129, 2080, 1024, 160),
     # general kernel (N % 128 != 0 with M > 16; N % 8 != 0)
     (40, 256, 200, 128), (3, 128, 21, 64),
 ]
@@ -303,7 +305,8 @@ def test_gemm7(mo, dev, monkeypatch, M, K, N, gs, sz, act):
     _check_rows(Y6.float().cpu().numpy(), base)
 
 
-@pytest.mark.parametrize("M,K,N,gs", [(300, 1024, 768, 128), (129, 2048, 2560, 64), (1024, 4096, 2816, 128)])
+@pytest.mark.parametrize("M,K,N,gs", [(300, 1024, 768, 128), (129, 2048, 2560, 64), (1024, 4096, 2816, 128),
+                                      (300, 1920, 768, 96), (257, 2080, 1280, 160)])
 def test_gemm7_forced(mo, dev, monkeypatch, M, K, N, gs):
     """i4_gemm7 taken below its grid rule (MCQ4_I4_GEMM7=1): ragged M, a handful
     of tiles, N % 256 == 0 and == 128 (waves past N)."""
