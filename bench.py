@@ -826,12 +826,20 @@ def probes(torch, dev):
     out["prefill_tile_scaling"] = tiles
 
     # 6. Shader clock under a dense MFMA load.
+    out["sclk_mfma_mhz"] = sclk_mfma_mhz(torch, dev)
+    return out
+
+
+def sclk_mfma_mhz(torch, dev):
+    """Median shader clock (MHz) of the waves of one dense-MFMA launch on every CU
+    (mcqb_measure_sclk: each wave's s_memtime cycles over its 100 MHz s_memrealtime
+    ticks).  The pool's boxes differ in it, and the decode and prefill figures with it."""
+    lib = bench_lib()
     tk = torch.zeros(4096, dtype=torch.int64, device=dev)
     bench_check(lib.mcqb_measure_sclk(tk.data_ptr(), 20000, None), "mcqb_measure_sclk")
     torch.cuda.synchronize()
     t2 = tk.view(-1, 2).double()
-    out["sclk_mfma_mhz"] = round(float((100.0 * t2[:, 0] / t2[:, 1]).median()), 0)
-    return out
+    return round(float((100.0 * t2[:, 0] / t2[:, 1]).median()), 0)
 
 
 def run_part(mo, torch, dev, args):
@@ -902,6 +910,7 @@ def main():
     pre_up = pre[0]
     pre_tflops = sum(2.0 * p["M"] * p["K"] * p["N"] for p in pre) / sum(p["ms"] / 1e3 for p in pre) / 1e12
     points = config_points(mo, torch, dev)
+    sclk = sclk_mfma_mhz(torch, dev)
 
     i4_dec = i4_decode_bench(mo, torch, dev, args)
     i4_t = i4_dec["seconds"] / i4_dec["steps"]
@@ -958,6 +967,9 @@ def main():
             "kernel": "read_probe_kernel (mcqb_read_probe: 16 KiB per 256-thread workgroup)",
             "value_over_ceiling": round(dec["read_ceiling_s"] / t_step, 4),
         },
+        # The box: shader clock under a dense MFMA load (the decode kernels' exposed
+        # math and the power-bound prefill scale with it; 1391-1530 MHz seen in the pool).
+        "machine": {"sclk_mfma_mhz": sclk},
         # The layer with gate and up in one launch (matmul_ggml_q4_0_grouped, no
         # reference counterpart): the same bytes in four launches.
         "grouped_gate_up": {
