@@ -32,13 +32,13 @@
 //     = s_j sum x (q - z) in fp32.  All 16 MFMA rows are the same activation
 //     row, so element 0 of each result is used.
 //   * Epilogue: the 8 waves' sums in wave order through LDS; with K split over
-//     workgroups, the splits are summed by the last-arriving workgroup of the
-//     tile in split order.  Default (XL): the grid's x extent is a multiple of
-//     8, so every split of a tile has the same linear id mod 8 and runs on one
-//     XCD; the partials go through that XCD's L2 (plain stores, L1-bypassing
-//     loads); the 64-bit ticket records each split's XCD, and a split found on
-//     another XCD is recomputed by the last arrival rather than read.  Otherwise agent-scope stores and loads, as
-//     in the general INT4 GEMV.  Store act(sum) as fp16.
+//     workgroups, the splits are summed in split order.  Default (XL): the
+//     grid's x extent is a multiple of 8, so every split of a tile has the same
+//     linear id mod 8 and runs on one XCD; the partials go through that XCD's L2
+//     (plain stores, L1-bypassing loads); split 0 sums them once each other
+//     split's flag shows its partial stored, and recomputes a split whose flag
+//     comes from another XCD or not in time.  Otherwise agent-scope stores and
+//     loads and a ticket, as in the general INT4 GEMV.  Store act(sum) as fp16.
 //
 // Int8 weights (WB = 8, W int8 [K][N], M <= 16): a step is 32 byte rows (4 KiB,
 // four copies), lane (c, g) reads byte rows 8g..8g+7, the K order is natural,
@@ -75,6 +75,8 @@ struct I4Gemv1Args {
     int M;                // activation rows (1 .. 16)
     int64_t ldx, ldy;     // row strides of X and Y (elements)
     float *part;          // [tiles][S][M][128] when S > 1
+    uint32_t *flags;      // XL: [tiles][S] split flags, behind the partials
+    uint32_t spin;        // XL: polls of a flag before its split is recomputed
     uint32_t *counters;   // [tiles]
     uint32_t foreign;     // splits treated as run on another XCD (test switch)
     const _Float16 *wn;   // NORM: RMSNorm weight [K] (X is the raw row)
@@ -129,6 +131,10 @@ i4_gemv1_kernel(I4Gemv1Args a) {
     const int N = a.N;
     const int col0 = t * I1_TC;
     const int s_begin = (sp * I1_W + wave) * a.spw;
+    // XL: the tile's split flags as this launch starts (lane q of wave 0: split q).
+    uint32_t fb = 0;
+    if (XL && a.S > 1 && wave == 0 && lane < a.S)
+        fb = __hip_atomic_load(a.flags + t * a.S + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int ns = max(0, min(a.spw, a.nsteps - s_begin));
 
     // [ring R x STEPB][x 1 KiB, M == 1 only][norm weights 1 KiB, NORM only][s/z slots]
@@ -385,38 +391,55 @@ i4_gemv1_kernel(I4Gemv1Args a) {
         }
     }
     if (a.S == 1) return;
-    // Split K: once this workgroup's partial is stored, one lane takes a ticket;
-    // the workgroup that draws the last sums every split's partial in split
-    // order.  XL: the partials were plain stores into this XCD's L2 (every split
-    // of the tile runs here; the 64-bit ticket records each split's XCD, and a
-    // split found elsewhere is recomputed, q4_common.h) and are read back
-    // through the L2.  Otherwise they went out
-    // write-through (agent-scope atomic stores) and come back with L2-bypassing
-    // loads.
+    // Split K.  XL: split 0 of the tile sums the partials (plain stores into
+    // this XCD's L2, read back through it) in split order.  Every other split,
+    // once its partial is stored, raises its flag: one word per (tile, split)
+    // behind the partials, written only by that split, which adds 8 to the value
+    // it read when the launch started and puts its XCD id in the low 3 bits.
+    // Split 0 read the same starting values, so it waits (a bounded number of
+    // polls, L1-bypassing loads) for each flag to reach start + 8; a flag that
+    // does not arrive in time, or arrives from another XCD, has its split
+    // recomputed from the inputs.  Nothing else writes the flags during a
+    // launch, so a flag can only hold its starting value or this launch's
+    // (whatever other kernels sharing the workspace left there before), and a
+    // slow split whose flag was given up on only moves its own count.
+    // Otherwise the partials go out write-through (agent-scope atomic stores),
+    // one lane takes a ticket, and the last to draw reads them back with
+    // L2-bypassing loads.
     wait_vmcnt<0>();
     __syncthreads();
     uint32_t *last_flag = (uint32_t *)smem;
     const float *base = a.part + (int64_t)t * a.S * nout;
     if constexpr (XL) {
-        // Ticket slots: 64-bit, 4096 per linear-id class mod 8 (one XCD each).
-        uint64_t *cnt = (uint64_t *)a.counters + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
         const uint32_t xcc = xcc_id();
-        if (tid == 0) {
-            const uint64_t inc = xcd_ticket_inc(xcc, sp);
-            const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const uint32_t local = xcd_ticket_local_mask(prev + inc, xcc, a.S) & ~a.foreign;
-            *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u : 0x10000u | local;
-            if ((prev & 0xFF) == (uint64_t)(a.S - 1)) {
-                // Every split has drawn: the slot is free for the next launch now,
-                // so its reset overlaps the sum instead of trailing it.
-                __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (sp != 0) {
+            if (wave == 0 && lane == sp)
+                __hip_atomic_store(a.flags + t * a.S + sp, (fb & ~7u) + 8u + xcc, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+            return;
+        }
+        if (wave == 0) {
+            const bool mine = lane >= 1 && lane < a.S;
+            const uint32_t want = (fb & ~7u) + 8u;
+            uint32_t v = 0;
+            bool seen = !mine;
+            for (uint32_t it = 0; it < a.spin; ++it) {
+                if (!seen) {
+                    v = __hip_atomic_load(a.flags + t * a.S + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    seen = (v & ~7u) == want;
+                }
+                if (__all(seen)) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            const uint64_t good = __ballot(mine && seen && (v & 7u) == xcc);
+            if (lane == 0) {
+                const uint32_t local = ((uint32_t)good | 1u) & ~a.foreign;
+                *last_flag = local;
                 if (local != (1u << a.S) - 1) note_split_fallback();
             }
         }
         __syncthreads();
-        const uint32_t lf = *last_flag;
-        if (!lf) return;
-        const uint32_t local = lf & 0xFFFF;        // splits whose partial is in this L2
+        const uint32_t local = *last_flag;         // splits whose partial is in this L2
         constexpr int KS = 32;                     // K per step (both weight widths)
         for (int v = tid; v < nout; v += I1_W * 64) {
             float sum = 0.f;
@@ -531,7 +554,8 @@ bool i4_gemv1_supported(int64_t M, int64_t K, int64_t N, int64_t gs, const void 
 size_t i4_gemv1_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs) {
     const I1Cfg c = i4_gemv1_config(K, N, gs);
     if (c.S == 1) return 0;
-    return COUNTER_BYTES + (size_t)(N / I1_TC) * c.S * std::max<int64_t>(M, 1) * I1_TC * sizeof(float);
+    return COUNTER_BYTES + (size_t)(N / I1_TC) * c.S * std::max<int64_t>(M, 1) * I1_TC * sizeof(float) +
+           (size_t)(N / I1_TC) * c.S * sizeof(uint32_t);
 }
 
 // The XCD-local exchange (default; MCQ4_XCD_LOCAL=0 selects the agent-scope
@@ -598,12 +622,14 @@ static hipError_t i1_setup(I4Gemv1Args &a, const _Float16 *X, int64_t ldx, const
     a.ngr_max = c.ngr_max;
     a.M = M; a.ldx = ldx; a.ldy = ldy;
     a.wave_bytes = (int)i1_wave_bytes(M, c, wb, norm);
-    a.part = nullptr; a.counters = nullptr; a.foreign = split_foreign_mask();
+    a.part = nullptr; a.flags = nullptr; a.counters = nullptr; a.foreign = split_foreign_mask();
+    a.spin = split_spin();
     a.wn = nullptr; a.eps = 0.f;
     if (c.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.counters = (uint32_t *)ws;
         a.part = (float *)((char *)ws + COUNTER_BYTES);
+        a.flags = (uint32_t *)(a.part + (int64_t)(N / I1_TC) * c.S * std::max(M, 1) * I1_TC);
     }
     if (i1_lds_bytes(M, a.wave_bytes) > 160 * 1024) return hipErrorInvalidValue;
     return hipSuccess;

@@ -2,6 +2,7 @@
 // publishes a new immutable snapshot through an atomic pointer; the old one is
 // kept alive (a few hundred bytes per reload) so that a launch running on
 // another thread never reads freed memory.
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <stdlib.h>
@@ -26,6 +27,7 @@ const char *const kNames[] = {
     "MCQ4_DECODE_PATH",     // direct: the register-load decode kernel
     "MCQ4_GEMM2_BM",        // 128 | 256: row tile of the fallback prefill kernel
     "MCQ4_SPLIT_FOREIGN",   // mask: split-K splits treated as run on another XCD (recompute path)
+    "MCQ4_SPLIT_SPIN",      // polls of a split flag before the split is recomputed (default 8192; 0: at once)
     // per-group INT4 / INT8 path
     "MCQ4_I4_PATH",         // generic: the general kernel for everything
     "MCQ4_I4_RMS_FUSE",     // 0: fused RMSNorm + INT4 at M = 1 runs as two kernels
@@ -74,6 +76,10 @@ const char *opt(const char *name) {
 uint32_t split_foreign_mask() {
     const char *v = opt("MCQ4_SPLIT_FOREIGN");
     return v ? (uint32_t)strtoul(v, nullptr, 0) : 0u;
+}
+uint32_t split_spin() {
+    const char *v = opt("MCQ4_SPLIT_SPIN");
+    return v ? (uint32_t)std::min<unsigned long>(strtoul(v, nullptr, 0), 1u << 20) : 8192u;
 }
 }  // namespace mcq4
 

@@ -17,4 +17,8 @@ inline bool opt_is(const char *name, char c) {
 // on another XCD (bit q = split q): MCQ4_SPLIT_FOREIGN, a test switch that
 // drives the recompute path on hardware where the placement always holds.
 uint32_t split_foreign_mask();
+// Polls of a split-K flag before the waiting workgroup recomputes that split
+// (MCQ4_SPLIT_SPIN, default 8192, at most 2^20; 0 drives the recompute path
+// for every other split).
+uint32_t split_spin();
 }  // namespace mcq4

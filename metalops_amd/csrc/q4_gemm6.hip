@@ -71,7 +71,6 @@ q4_gemm6_kernel(Gemm6Args a) {
     const int z = (int)blockIdx.z;
     const int k_lo = (int)((int64_t)a.nb * z / a.S);
     const int nk = (int)((int64_t)a.nb * (z + 1) / a.S) - k_lo;
-    const int nst = (nk + 1) >> 1;
 
     uint8_t *const sA = smem;
     uint8_t *const ring = smem + G6_NS * A_SLOT + wave * (G6_RAW_N * G6_RAW_SLOT);

@@ -96,7 +96,8 @@ def test_split_recompute_path(dev, monkeypatch, name, env, case):
     from metalops_amd import _lib
     print(f"split recompute {name} {case}", flush=True)
     for k in ("MCQ4_GEMVM_SPLIT", "MCQ4_GEMM_PATH", "MCQ4_GEMM6_SPLIT", "MCQ4_GEMM8_SPLIT", "MCQ4_I4_GEMV1", "MCQ4_XCD_LOCAL",
-              "MCQ4_SPLIT_FOREIGN", "MCQ4_I4_PATH", "MCQ4_I4_SPW1", "MCQ4_I4_GEMM7", "MCQ4_GEMV_SPAN"):
+              "MCQ4_SPLIT_FOREIGN", "MCQ4_I4_PATH", "MCQ4_I4_SPW1", "MCQ4_I4_GEMM7", "MCQ4_GEMV_SPAN",
+              "MCQ4_SPLIT_SPIN"):
         monkeypatch.delenv(k, raising=False)
     for k, v in env.items():
         monkeypatch.setenv(k, v)
@@ -116,3 +117,63 @@ def test_split_recompute_path(dev, monkeypatch, name, env, case):
     # and the next default call is unaffected (counters left zero)
     Y2 = fn()
     assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
+
+
+# Kernels whose XCD-local exchange waits on per-split flags (a bounded number of
+# polls, then the split is recomputed).
+FLAG_CASES = [
+    ("i4_gemv1", ("i4", 1, 4096, 4096, 128, 4)),
+    ("i4_gemv1_mr", ("i4", 8, 11008, 4096, 128, 4)),
+    ("i4_gemv1_rmsnorm", ("rms", 1, 4096, 4096, 128)),
+    ("i8_gemv1", ("i4", 4, 4096, 4096, 128, 8)),
+]
+
+
+@pytest.mark.parametrize("name,case", FLAG_CASES, ids=[c[0] for c in FLAG_CASES])
+def test_split_flag_timeout_recomputes(dev, monkeypatch, name, case):
+    """MCQ4_SPLIT_SPIN=0: the summing workgroup stops waiting at once and
+    recomputes every other split from the inputs.  The result keeps the oracle's
+    bar, the fallback counter counts the tiles, and the flags stay usable: the
+    next default call gives the first call's bits with no fallback."""
+    from metalops_amd import _lib
+    print(f"split flag timeout {name} {case}", flush=True)
+    for k in ("MCQ4_I4_GEMV1", "MCQ4_XCD_LOCAL", "MCQ4_SPLIT_FOREIGN", "MCQ4_SPLIT_SPIN", "MCQ4_I4_PATH",
+              "MCQ4_I4_SPW1"):
+        monkeypatch.delenv(k, raising=False)
+    build = {"i4": _i4_case, "rms": _rms_case}[case[0]]
+    fn, Yref = build(dev, *case[1:])
+    Y = fn()
+    torch.cuda.synchronize()
+    assert _lib.split_fallback_count(reset=True) == 0
+    monkeypatch.setenv("MCQ4_SPLIT_SPIN", "0")
+    Yt = fn()
+    torch.cuda.synchronize()
+    assert _lib.split_fallback_count(reset=True) > 0, "the recompute path did not run"
+    monkeypatch.delenv("MCQ4_SPLIT_SPIN")
+    _rows_close(Yt.float().cpu().numpy(), Yref)
+    Y2 = fn()
+    torch.cuda.synchronize()
+    assert _lib.split_fallback_count(reset=True) == 0
+    assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
+
+
+def test_split_flags_survive_other_kernels(dev, monkeypatch):
+    """The flags sit behind the INT4 decode kernel's partials in the shared
+    workspace, where other split-K kernels store their own partials between its
+    launches.  Each launch reads the flags' values when it starts, so whatever
+    was left there, every launch must give the same bits without a fallback."""
+    from metalops_amd import _lib
+    for k in ("MCQ4_I4_GEMV1", "MCQ4_XCD_LOCAL", "MCQ4_SPLIT_FOREIGN", "MCQ4_SPLIT_SPIN", "MCQ4_I4_PATH",
+              "MCQ4_I4_SPW1", "MCQ4_GEMV_SPAN", "MCQ4_GEMVM_SPLIT"):
+        monkeypatch.delenv(k, raising=False)
+    i4, _ = _i4_case(dev, 1, 4096, 4096, 128, 4)       # 32 tiles x 8 splits
+    q4, _ = _q4_case(dev, 16, 14336, 4096)              # 4 splits x 16 x 4096 fp32 partials
+    first = i4()
+    torch.cuda.synchronize()
+    _lib.split_fallback_count(reset=True)
+    for _ in range(5):
+        q4()
+        Y = i4()
+        torch.cuda.synchronize()
+        assert torch.equal(first.view(torch.int16), Y.view(torch.int16))
+    assert _lib.split_fallback_count(reset=True) == 0
