@@ -39,8 +39,9 @@
 // columns (1152-byte row pieces, the pattern a plain read serves ~20% faster than
 // strips) and one K range of up to 128 K blocks, the same one item per wave.  The
 // K splits of a tile share blockIdx.x and run on one XCD; their fp32 partials meet
-// in that XCD's L2 and the last to take the tile's ticket sums them in split
-// order (a split recorded on another XCD is recomputed from the inputs).
+// in that XCD's L2 and split 0 sums them in split order once each other split's
+// flag shows its partial stored (a split whose flag comes from another XCD, or
+// not in time, is recomputed from the inputs).
 #include <algorithm>
 #include <atomic>
 #include <type_traits>
@@ -96,7 +97,8 @@ struct GemvSpanArgs {
     // 8) and K splits (blockIdx.y) of bps K blocks each.
     int S = 1, bps = 0;
     float *part = nullptr;                   // [S][M][N] fp32 partials
-    uint64_t *tickets = nullptr;             // 64-bit tickets [8][4096] by blockIdx.x mod 8
+    uint32_t *flags = nullptr;               // split flags [tiles][S], behind the partials
+    uint32_t spin = 0;                       // polls of a flag before its split is recomputed
     uint32_t foreign = 0;                    // splits treated as run on another XCD (test switch)
 };
 
@@ -124,6 +126,7 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
     uint8_t *slot = smem + XS + wave * GS_SLOT;
 
     int g0, ng, kb0 = 0, kbe = nb;
+    uint32_t fb = 0;                         // SPLIT: the tile's split flags as the launch starts
     if constexpr (SPLIT) {
         // Tile t (64 columns) of the XCD-renumbered grid.x; split blockIdx.y owns
         // K blocks [sp bps, (sp + 1) bps).  Every split of a tile has the same
@@ -131,6 +134,8 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
         const int gx = (int)gridDim.x;
         const int t = ((int)blockIdx.x & 7) * (gx >> 3) + ((int)blockIdx.x >> 3);
         if (t >= (ngt >> 2)) return;                               // grid padding
+        if (wave == 0 && lane < a.S)
+            fb = __hip_atomic_load(a.flags + t * a.S + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         g0 = 4 * t;
         ng = 4;
         kb0 = (int)blockIdx.y * a.bps;
@@ -310,33 +315,53 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
         if constexpr (!SPLIT) Y[(int64_t)row * ldy + n] = (_Float16)s;
     }
     if constexpr (SPLIT) {
-        // This split's partial stays in the XCD's L2 (plain stores); once it is
-        // stored, one lane takes the tile's ticket and the workgroup that draws
-        // the last sums the S partials in split order -- its own from registers,
-        // the others through the L2, and any split that ran on another XCD
-        // (recorded in the ticket) recomputed from the inputs.
+        // Split 0 sums the S partials in split order: its own from registers, the
+        // others through the XCD's L2 (plain stores), each once that split's flag
+        // shows it stored.  A flag is one word per (tile, split) written only by
+        // that split, which adds 8 to the value it held when the launch started
+        // and puts its XCD id in the low 3 bits; split 0 read the same starting
+        // values and polls (at most a.spin times) for start + 8.  A split whose
+        // flag comes from another XCD, or not in time, is recomputed from the
+        // inputs.  Nothing else writes a flag during a launch, so whatever other
+        // kernels left in the words between launches, a flag holds its starting
+        // value or this launch's.
         const int N = ngt * 16, sp = (int)blockIdx.y, S = a.S;
-        if (live) a.part[((int64_t)sp * M + row) * N + n] = s;
-        wait_vmcnt<0>();
-        __syncthreads();
+        const int t = (int)(g0 >> 2);
         uint32_t *last_flag = (uint32_t *)smem;                    // the slots are idle from here
-        uint64_t *cnt = a.tickets + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
-        if (tid == 0) {
-            const uint32_t xcc = xcc_id();
-            const uint64_t inc = xcd_ticket_inc(xcc, sp);
-            const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const uint32_t local = xcd_ticket_local_mask(prev + inc, xcc, S) & ~a.foreign;
-            *last_flag = (prev & 0xFF) != (uint64_t)(S - 1) ? 0u : 0x10000u | local;
-            if ((prev & 0xFF) == (uint64_t)(S - 1)) {
-                // Every split has drawn: the slot is free for the next launch.
-                __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t xcc = xcc_id();
+        if (sp != 0) {
+            if (live) a.part[((int64_t)sp * M + row) * N + n] = s;
+            wait_vmcnt<0>();
+            __syncthreads();
+            if (wave == 0 && lane == sp)
+                __hip_atomic_store(a.flags + t * S + sp, (fb & ~7u) + 8u + xcc, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_WORKGROUP);
+            return;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const bool mine = lane >= 1 && lane < S;
+            const uint32_t want = (fb & ~7u) + 8u;
+            uint32_t v = 0;
+            bool seen = !mine;
+            for (uint32_t it = 0; it < a.spin; ++it) {
+                if (!seen) {
+                    v = __hip_atomic_load(a.flags + t * S + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    seen = (v & ~7u) == want;
+                }
+                if (__all(seen)) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            const uint64_t good = __ballot(mine && seen && (v & 7u) == xcc);
+            if (lane == 0) {
+                const uint32_t local = ((uint32_t)good | 1u) & ~a.foreign;
+                *last_flag = local;
                 if (local != (1u << S) - 1) note_split_fallback();
             }
         }
         __syncthreads();
-        const uint32_t lf = *last_flag;
-        if (!lf || !live) return;
-        const uint32_t local = lf & 0xFFFF;
+        if (!live) return;
+        const uint32_t local = *last_flag;
         float tot = 0.f;
         for (int q = 0; q < S; ++q) {
             float pv;
@@ -434,7 +459,7 @@ bool gemv_span_split_supported(const _Float16 *X, int64_t ldx, const uint8_t *W,
 size_t gemv_span_split_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M < 2 || M > 16 || N % 64 || N < 64 || N > 4096 || K < QK) return 0;
     const SpanSplitPlan p = span_split_plan(K, N);
-    return COUNTER_BYTES + (size_t)p.S * M * N * sizeof(float);
+    return COUNTER_BYTES + (size_t)p.S * M * N * sizeof(float) + (size_t)(N / 64) * p.S * sizeof(uint32_t);
 }
 
 hipError_t launch_gemv_span_split(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float16 *Y, int64_t ldy,
@@ -450,8 +475,9 @@ hipError_t launch_gemv_span_split(const _Float16 *X, int64_t ldx, const uint8_t 
     a.grow = (uint32_t)N * BLOCK_BYTES;
     a.S = p.S;
     a.bps = p.bps;
-    a.tickets = (uint64_t *)ws;
     a.part = (float *)((char *)ws + COUNTER_BYTES);
+    a.flags = (uint32_t *)(a.part + (int64_t)p.S * M * N);
+    a.spin = split_spin();
     a.foreign = split_foreign_mask();
     const dim3 grid(p.gx, p.S);
     // M <= 8: the 8-row instance (at M = 3, 4 on 14336 x 4096 the 4-row one ran

@@ -126,6 +126,8 @@ FLAG_CASES = [
     ("i4_gemv1_mr", ("i4", 8, 11008, 4096, 128, 4)),
     ("i4_gemv1_rmsnorm", ("rms", 1, 4096, 4096, 128)),
     ("i8_gemv1", ("i4", 4, 4096, 4096, 128, 8)),
+    ("q4_span_split_s4", ("q4", 16, 14336, 4096)),
+    ("q4_span_split_rows8", ("q4", 6, 11008, 4096)),
 ]
 
 
@@ -138,9 +140,9 @@ def test_split_flag_timeout_recomputes(dev, monkeypatch, name, case):
     from metalops_amd import _lib
     print(f"split flag timeout {name} {case}", flush=True)
     for k in ("MCQ4_I4_GEMV1", "MCQ4_XCD_LOCAL", "MCQ4_SPLIT_FOREIGN", "MCQ4_SPLIT_SPIN", "MCQ4_I4_PATH",
-              "MCQ4_I4_SPW1"):
+              "MCQ4_I4_SPW1", "MCQ4_GEMV_SPAN", "MCQ4_GEMVM_SPLIT"):
         monkeypatch.delenv(k, raising=False)
-    build = {"i4": _i4_case, "rms": _rms_case}[case[0]]
+    build = {"q4": _q4_case, "i4": _i4_case, "rms": _rms_case}[case[0]]
     fn, Yref = build(dev, *case[1:])
     Y = fn()
     torch.cuda.synchronize()
@@ -157,23 +159,39 @@ def test_split_flag_timeout_recomputes(dev, monkeypatch, name, case):
     assert torch.equal(Y.view(torch.int16), Y2.view(torch.int16))
 
 
-def test_split_flags_survive_other_kernels(dev, monkeypatch):
-    """The flags sit behind the INT4 decode kernel's partials in the shared
-    workspace, where other split-K kernels store their own partials between its
-    launches.  Each launch reads the flags' values when it starts, so whatever
-    was left there, every launch must give the same bits without a fallback."""
+# (kernel with flags, a split-K kernel whose partials cover those flag words)
+SURVIVE = [
+    # INT4 decode: 32 tiles x 8 splits, flags 128 KiB into the partial area; the
+    # span split form stores 1 MiB of partials there.
+    ("i4_gemv1", ("i4", 1, 4096, 4096, 128, 4), {}, ("q4", 16, 14336, 4096)),
+    # Span split form: flags 1 MiB in; gemm6 with two splits stores 2.3 MiB (9 tiles x 2 x 128 KiB).
+    ("q4_span_split", ("q4", 16, 14336, 4096), {"MCQ4_GEMM_PATH": "6", "MCQ4_GEMM6_SPLIT": "2"},
+     ("q4", 300, 4096, 640)),
+]
+
+
+@pytest.mark.parametrize("name,case,other_env,other", SURVIVE, ids=[c[0] for c in SURVIVE])
+def test_split_flags_survive_other_kernels(dev, monkeypatch, name, case, other_env, other):
+    """The flags sit behind a kernel's partials in the shared workspace, where
+    other split-K kernels store their own partials between its launches.  Each
+    launch reads the flags' values when it starts, so whatever was left there,
+    every launch must give the same bits without a fallback."""
     from metalops_amd import _lib
+    print(f"split flags survive {name} {case} {other}", flush=True)
     for k in ("MCQ4_I4_GEMV1", "MCQ4_XCD_LOCAL", "MCQ4_SPLIT_FOREIGN", "MCQ4_SPLIT_SPIN", "MCQ4_I4_PATH",
-              "MCQ4_I4_SPW1", "MCQ4_GEMV_SPAN", "MCQ4_GEMVM_SPLIT"):
+              "MCQ4_I4_SPW1", "MCQ4_GEMV_SPAN", "MCQ4_GEMVM_SPLIT", "MCQ4_GEMM_PATH", "MCQ4_GEMM6_SPLIT"):
         monkeypatch.delenv(k, raising=False)
-    i4, _ = _i4_case(dev, 1, 4096, 4096, 128, 4)       # 32 tiles x 8 splits
-    q4, _ = _q4_case(dev, 16, 14336, 4096)              # 4 splits x 16 x 4096 fp32 partials
-    first = i4()
+    for k, v in other_env.items():
+        monkeypatch.setenv(k, v)
+    build = {"q4": _q4_case, "i4": _i4_case}
+    fn, _ = build[case[0]](dev, *case[1:])
+    fo, _ = build[other[0]](dev, *other[1:])
+    first = fn()
     torch.cuda.synchronize()
     _lib.split_fallback_count(reset=True)
     for _ in range(5):
-        q4()
-        Y = i4()
+        fo()
+        Y = fn()
         torch.cuda.synchronize()
         assert torch.equal(first.view(torch.int16), Y.view(torch.int16))
     assert _lib.split_fallback_count(reset=True) == 0
