@@ -204,7 +204,14 @@ q4_gemv_dma_kernel(GemvArgs a) {
 
     const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
     const uint32_t qal = (uint32_t)(qoff & ~3), qsh = (uint32_t)(qoff & 3) * 8;
-    const uint32_t doff = (uint32_t)(c * BLOCK_BYTES);
+    // Only lanes g == 0 keep their sums (M == 1: every A row is the activation
+    // row), so their second word is taken where it holds the block's scale -- after
+    // the first for an even column (whose first word starts at the block), before it
+    // for an odd one (whose first word is the nibble bytes exactly) -- and the scale
+    // comes from the two words instead of a read of its own.  The B operand is
+    // unchanged: the second word only feeds byte 3 of w8, which the masks drop.
+    const uint32_t q1off = g == 0 && (c & 1) ? (uint32_t)(c * BLOCK_BYTES - 2) : qal + 4;
+    const uint32_t dsel = (c & 1) ? 0x0C0C0706u : 0x0C0C0100u;     // scale bytes of (q1, q0)
     // fp16 exponent words: 1024 + q for a low nibble (bits 0..3 of a half),
     // 64 + q for a high nibble left in place (bits 4..7: 64 * (1 + 16q/1024)).
     const uint32_t e1024 = opaque_vgpr(0x64006400u), e64 = opaque_vgpr(0x54005400u);
@@ -258,10 +265,9 @@ q4_gemv_dma_kernel(GemvArgs a) {
                 for (int u = 0; u < B; ++u)
 #pragma unroll
                     for (int grp = 0; grp < NG; ++grp) {
-                        const lds_u32 *qp = (const lds_u32 *)(lds_ptr(base + qal) + u * ROWB + grp * 288);
-                        q0[u][grp] = qp[0];
-                        q1[u][grp] = qp[1];
-                        dh[u][grp] = bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(base + doff) + u * ROWB + grp * 288));
+                        q0[u][grp] = *(const lds_u32 *)(lds_ptr(base + qal) + u * ROWB + grp * 288);
+                        q1[u][grp] = *(const lds_u32 *)(lds_ptr(base + q1off) + u * ROWB + grp * 288);
+                        dh[u][grp] = bitcast<_Float16>((uint16_t)__builtin_amdgcn_perm(q1[u][grp], q0[u][grp], dsel));
                     }
                 float4_t r[B][NG];
 #pragma unroll

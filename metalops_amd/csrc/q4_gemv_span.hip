@@ -155,6 +155,14 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
     const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
     const uint32_t qal = (uint32_t)(qoff & ~3), qsh = (uint32_t)(qoff & 3) * 8;
     const uint32_t doff = (uint32_t)(c * BLOCK_BYTES);
+    // M == 1: only lanes g == 0 keep their sums (every A row is the one activation
+    // row), so their second word is taken where it holds the block's scale -- after
+    // the first for an even column (whose first word starts at the block), before it
+    // for an odd one (whose first word is the nibble bytes exactly) -- and the scale
+    // comes from the two words instead of a read of its own.  The B operand is
+    // unchanged: the second word only feeds byte 3 of w8, which the masks drop.
+    const uint32_t q1off = GR == 1 && g == 0 && (c & 1) ? doff - 2 : qal + 4;
+    const uint32_t dsel = (c & 1) ? 0x0C0C0706u : 0x0C0C0100u;     // scale bytes of (q1, q0)
     const uint32_t e1024 = opaque_vgpr(0x64006400u), e64 = opaque_vgpr(0x54005400u);
     const uint32_t mlo = opaque_sgpr(0x000F000Fu), mhi = opaque_sgpr(0x00F000F0u);
     const uint32_t nlo = 0xE408E408u, nhi = 0xD480D480u;          // -1032, -72 pairs
@@ -216,7 +224,7 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
             if constexpr (HOIST) negs[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xq[u], negc, z, 0, 0, 0);
         }
         const uint32_t base = lds_addr(slot);
-        const uint32_t vq0 = opaque_vgpr(base + qal), vq1 = opaque_vgpr(base + qal + 4),
+        const uint32_t vq0 = opaque_vgpr(base + qal), vq1 = opaque_vgpr(base + q1off),
                        vd = opaque_vgpr(base + doff);
         // GS_RP K rows (all groups of the span) at a time, each set as soon as the
         // copies holding it have landed (the copies cover the item in row-major
@@ -238,7 +246,10 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
                     const uint32_t ro = (R0 + v) * rowb + grp * 288;
                     q0[v][grp] = *(const lds_u32 *)(lds_ptr(vq0) + ro);
                     q1[v][grp] = *(const lds_u32 *)(lds_ptr(vq1) + ro);
-                    dh[v][grp] = bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(vd) + ro));
+                    if constexpr (GR == 1)
+                        dh[v][grp] = bitcast<_Float16>((uint16_t)__builtin_amdgcn_perm(q1[v][grp], q0[v][grp], dsel));
+                    else
+                        dh[v][grp] = bitcast<_Float16>(*(const lds_u16 *)(lds_ptr(vd) + ro));
                 }
             float4_t ns[NR];
 #pragma unroll
