@@ -82,7 +82,10 @@ int mcq4_dequantize_q4_0(const uint8_t *blocks, int64_t K, int64_t N, void *out,
 /*
  * Workspace bytes mcq4_matmul_q4_0_f16 needs for this shape (0 = none).  The
  * workspace starts with a fixed 256 KiB area of per-tile arrival counters,
- * followed by fp32 split-K partials.  The counter area must be zero-filled
+ * followed by fp32 split-K partials and, for the kernels whose splits signal
+ * each other with per-split flag words, those words (any starting value: each
+ * call reads them as it starts and moves each by a fixed step).  The counter
+ * area must be zero-filled
  * before first use; every completed call leaves it zero again, so one zeroed
  * buffer can be reused for any later call whose requirement it covers.  Calls
  * that share a workspace must not overlap (use one workspace per stream).
