@@ -195,3 +195,50 @@ def test_split_flags_survive_other_kernels(dev, monkeypatch, name, case, other_e
         torch.cuda.synchronize()
         assert torch.equal(first.view(torch.int16), Y.view(torch.int16))
     assert _lib.split_fallback_count(reset=True) == 0
+
+
+@pytest.mark.parametrize("kind,M,K,N", [("i4", 1, 4096, 4096), ("i4", 8, 11008, 4096), ("q4", 16, 14336, 4096),
+                                        ("q4", 4, 11008, 4096)])
+def test_split_flags_any_start_value(dev, kind, M, K, N):
+    """Split flags need no initial value: a caller's workspace whose counter area
+    is zero and whose every other byte is 0xFF (each flag word 0xFFFFFFFF, so the
+    first step of 8 wraps past 2^32) gives the library's own workspace's bits on
+    every call, with no split recomputed."""
+    import metalops_amd as mo
+    from metalops_amd import _lib
+    print(f"split flags start value {kind} {M}x{K}x{N}", flush=True)
+    lib = _lib.lib
+    g = torch.Generator().manual_seed(M + K + N + 7)
+    X = torch.randn(M, K, generator=g).half().to(dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    if kind == "i4":
+        W = (torch.randn(K, N, generator=g) * 0.02).half().to(dev)
+        p, s, z = mo.quantize_int4(W, 128)
+        want = mo.matmul_int4(X, p, s, z, 128)
+        need = int(lib.mcq4_matmul_int4_workspace_bytes(M, K, N, 128, _lib.MCQ4_DTYPE_F16))
+
+        def call(Y, ws):
+            return lib.mcq4_matmul_int4(X.data_ptr(), _lib.MCQ4_DTYPE_F16, K, p.data_ptr(), s.data_ptr(),
+                                        z.data_ptr(), _lib.MCQ4_DTYPE_F16, Y.data_ptr(), N, M, K, N, 128,
+                                        ws.data_ptr(), ws.numel(), stream)
+    else:
+        W = torch.randn(K, N, generator=g) * 0.02
+        b = torch.from_numpy(R.quantize_llama_rule(W.numpy())).to(dev)
+        want = mo.matmul_ggml_q4_0(X, b)
+        need = int(lib.mcq4_matmul_workspace_bytes(M, K, N))
+
+        def call(Y, ws):
+            return lib.mcq4_matmul_q4_0_f16(X.data_ptr(), K, b.data_ptr(), Y.data_ptr(), N, M, K, N,
+                                            ws.data_ptr(), ws.numel(), stream)
+    counters = 256 * 1024
+    assert need > counters, "this shape splits K"
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=dev)
+    ws[:counters].zero_()
+    torch.cuda.synchronize()
+    _lib.split_fallback_count(reset=True)
+    for _ in range(3):
+        Y = torch.empty(M, N, dtype=torch.float16, device=dev)
+        assert call(Y, ws) == _lib.MCQ4_OK
+        torch.cuda.synchronize()
+        assert torch.equal(want.view(torch.int16), Y.view(torch.int16))
+    assert _lib.split_fallback_count(reset=True) == 0
