@@ -60,10 +60,11 @@ struct GemvMArgs {
     int M, nb, N, ntiles, nbt;
     int S, bps;          // K splits (grid.y) and batches per split
     float *part;         // [S][M][16 * ntiles] fp32 partials when S > 1 (after the counter area)
-    // S > 1 with the XCD-local exchange: grid.x padded to a multiple of 8 and the
-    // last split of each workgroup sums the partials (64-bit tickets [8][4096]
-    // by blockIdx.x mod 8 at the workspace start); null: the reduction kernel.
-    uint64_t *tickets;
+    // S > 1 with the XCD-local exchange: grid.x padded to a multiple of 8, split 0
+    // of each workgroup sums the partials once the other splits' flags ([grid.x][S]
+    // words behind the partials) show them stored; null: the reduction kernel.
+    uint32_t *flags;
+    uint32_t spin;       // polls of a flag before its split is recomputed
     uint32_t foreign;    // splits treated as run on another XCD (test switch)
 };
 
@@ -98,6 +99,11 @@ q4_gemvm_kernel(GemvMArgs a) {
     if (ntl <= 0) return;                         // grid padding (XCD-local exchange)
     // This split's batches [b0, b0 + nbs); wave w owns b0 + w, b0 + w + WAVES, ...
     const int sp = (int)blockIdx.y;
+    // XCD-local exchange: the workgroup's split flags as the launch starts (lane q
+    // of wave 0: split q).
+    uint32_t fb = 0;
+    if (a.S > 1 && a.flags && wave == 0 && lane < a.S)
+        fb = __hip_atomic_load(a.flags + wg * a.S + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int b0 = sp * a.bps;
     const int nbs = max(0, min(a.bps, a.nbt - b0));
     const int nbm = nbs > wave ? (nbs - wave + WAVES - 1) / WAVES : 0;
@@ -288,32 +294,49 @@ q4_gemvm_kernel(GemvMArgs a) {
             else a.part[((int64_t)sp * a.M + rr) * (16 * a.ntiles) + n] = s;
         }
     }
-    if (a.S == 1 || !a.tickets) return;
+    if (a.S == 1 || !a.flags) return;
     // Every split of this workgroup runs on this XCD (same blockIdx.x, grid.x a
-    // multiple of 8): the last to arrive sums the partials, in split order as the
-    // reduction kernel does, from the XCD's L2 (its own too with RB > 1: the LDS
-    // area holds only the last row block's wave sums).
+    // multiple of 8).  Split 0 sums the partials, in split order as the reduction
+    // kernel does, from the XCD's L2 (its own too with RB > 1: the LDS area holds
+    // only the last row block's wave sums), once each other split's flag shows
+    // its partial stored.  A flag is one word per (workgroup, split), written only
+    // by that split, which adds 8 to the value it held when the launch started and
+    // puts its XCD id in the low 3 bits; split 0 read the same starting values and
+    // polls (at most a.spin times).  A split whose flag comes from another XCD, or
+    // not in time, is recomputed from the inputs.
     wait_vmcnt<0>();
     __syncthreads();
-    uint64_t *cnt = a.tickets + ((int)blockIdx.x & 7) * 4096 + ((int)blockIdx.x >> 3);
     const uint32_t xcc = xcc_id();
     uint32_t *last_flag = (uint32_t *)smem;       // the ring is idle from here
-    if (tid == 0) {
-        const uint64_t inc = xcd_ticket_inc(xcc, sp);
-        const uint64_t prev = __hip_atomic_fetch_add(cnt, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t local = xcd_ticket_local_mask(prev + inc, xcc, a.S) & ~a.foreign;
-        *last_flag = (prev & 0xFF) != (uint64_t)(a.S - 1) ? 0u : 0x10000u | local;
-        if ((prev & 0xFF) == (uint64_t)(a.S - 1)) {
-            // Every split has drawn: the slot is free for the next launch now,
-            // so its reset overlaps the sum instead of trailing it.
-            __hip_atomic_store(cnt, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (sp != 0) {
+        if (wave == 0 && lane == sp)
+            __hip_atomic_store(a.flags + wg * a.S + sp, (fb & ~7u) + 8u + xcc, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+        return;
+    }
+    if (wave == 0) {
+        const bool mine = lane >= 1 && lane < a.S;
+        const uint32_t want = (fb & ~7u) + 8u;
+        uint32_t v = 0;
+        bool seen = !mine;
+        for (uint32_t it = 0; it < a.spin; ++it) {
+            if (!seen) {
+                v = __hip_atomic_load(a.flags + wg * a.S + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                seen = (v & ~7u) == want;
+            }
+            if (__all(seen)) break;
+            __builtin_amdgcn_s_sleep(1);
+        }
+        const uint64_t good = __ballot(mine && seen && (v & 7u) == xcc);
+        if (lane == 0) {
+            const uint32_t local = ((uint32_t)good | 1u) & ~a.foreign;
+            *last_flag = local;
             if (local != (1u << a.S) - 1) note_split_fallback();
         }
     }
     __syncthreads();
     const uint32_t lf = *last_flag;
-    if (!lf) return;
-    const uint32_t local = lf & 0xFFFF;            // splits whose partial is in this L2
+    const uint32_t local = lf;                     // splits whose partial is in this L2
     const int64_t pstride = (int64_t)a.M * 16 * a.ntiles;         // floats per split
     for (int v = tid; v < TPW * 256 * RB; v += WAVES * 64) {   // v = (rb, j, row, col)
         const int j = (v >> 8) % TPW, rr = 16 * (v / (256 * TPW)) + ((v >> 4) & 15), col = v & 15;
@@ -375,9 +398,9 @@ static hipError_t launch_gemvm_t(const GemvMArgs &a, int grid, hipStream_t s) {
         if (e != hipSuccess) return e;
         done.fetch_or(bit, std::memory_order_acq_rel);
     }
-    const int gx = a.tickets ? (grid + 7) / 8 * 8 : grid;
+    const int gx = a.flags ? (grid + 7) / 8 * 8 : grid;
     hipLaunchKernelGGL((q4_gemvm_kernel<WAVES, TPW, RB, GR, HOIST>), dim3(gx, a.S), dim3(WAVES * 64), lds, s, a);
-    if (a.S > 1 && !a.tickets) {
+    if (a.S > 1 && !a.flags) {
         const int64_t n = (int64_t)a.M * 16 * a.ntiles;
         hipLaunchKernelGGL(q4_gemvm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
     }
@@ -417,7 +440,7 @@ bool gemvm_supported(const _Float16 *X, int64_t ldx, const uint8_t *W, int64_t M
 // activation block (M x K halves) from L2, and at M >= 8 those loads -- one
 // line per row per instruction -- outnumber the weight copies.  Two tiles per
 // workgroup over half of K each keeps 256 workgroups and halves the activation
-// traffic; the fp32 partials are summed in split order by the last split of each
+// traffic; the fp32 partials are summed in split order by split 0 of each
 // workgroup (XCD-local exchange) or, with MCQ4_XCD_LOCAL=0, by a second kernel
 // (M=16 K=14336 N=4096: 15.6 us with the second kernel, was 18.7; M=8: 13.4,
 // was 14.3).  Up to 16 rows the split goes on until every wave has one batch
@@ -460,7 +483,9 @@ size_t gemvm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M < 2 || M > 32 || N < 16 || K < QK) return 0;
     const GmPlan p = gemvm_plan(M, K, N);
     // Partials follow the workspace's counter area, which other kernels rely on staying zero.
-    const size_t own = p.S > 1 ? COUNTER_BYTES + (size_t)p.S * M * (N / 16) * 16 * sizeof(float) : 0;
+    const size_t own = p.S > 1 ? COUNTER_BYTES + (size_t)p.S * M * (N / 16) * 16 * sizeof(float) +
+                                     (size_t)(p.grid + 7) / 8 * 8 * p.S * sizeof(uint32_t)
+                               : 0;
     return std::max(own, gemv_span_split_workspace_bytes(M, K, N));
 }
 
@@ -494,12 +519,14 @@ hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
     const GmPlan p = gemvm_plan(M, K, N);
     a.S = p.S; a.bps = p.bps;
     a.part = nullptr;
-    a.tickets = nullptr;
+    a.flags = nullptr;
+    a.spin = split_spin();
     a.foreign = split_foreign_mask();
     if (p.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.part = (float *)((char *)ws + COUNTER_BYTES);
-        if (!opt_is("MCQ4_XCD_LOCAL", '0') && p.S <= 8) a.tickets = (uint64_t *)ws;
+        if (!opt_is("MCQ4_XCD_LOCAL", '0') && p.S <= 8)
+            a.flags = (uint32_t *)(a.part + (int64_t)p.S * M * (N / 16) * 16);
     }
     // One batch per wave at most: the activations and -S once per wave
     // (MCQ4_GEMVM_HOIST=0 turns it off).

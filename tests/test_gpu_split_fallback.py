@@ -128,11 +128,14 @@ FLAG_CASES = [
     ("i8_gemv1", ("i4", 4, 4096, 4096, 128, 8)),
     ("q4_span_split_s4", ("q4", 16, 14336, 4096)),
     ("q4_span_split_rows8", ("q4", 6, 11008, 4096)),
+    ("q4_gemvm_rb2_s2", ("q4", 32, 14336, 4096)),
+    ("q4_gemvm_s8", ("q4", 12, 2048, 1032), {"MCQ4_GEMVM_SPLIT": "8"}),
 ]
 
 
-@pytest.mark.parametrize("name,case", FLAG_CASES, ids=[c[0] for c in FLAG_CASES])
-def test_split_flag_timeout_recomputes(dev, monkeypatch, name, case):
+@pytest.mark.parametrize("name,case,env", [(c[0], c[1], c[2] if len(c) > 2 else {}) for c in FLAG_CASES],
+                         ids=[c[0] for c in FLAG_CASES])
+def test_split_flag_timeout_recomputes(dev, monkeypatch, name, case, env):
     """MCQ4_SPLIT_SPIN=0: the summing workgroup stops waiting at once and
     recomputes every other split from the inputs.  The result keeps the oracle's
     bar, the fallback counter counts the tiles, and the flags stay usable: the
@@ -142,6 +145,8 @@ def test_split_flag_timeout_recomputes(dev, monkeypatch, name, case):
     for k in ("MCQ4_I4_GEMV1", "MCQ4_XCD_LOCAL", "MCQ4_SPLIT_FOREIGN", "MCQ4_SPLIT_SPIN", "MCQ4_I4_PATH",
               "MCQ4_I4_SPW1", "MCQ4_GEMV_SPAN", "MCQ4_GEMVM_SPLIT"):
         monkeypatch.delenv(k, raising=False)
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
     build = {"q4": _q4_case, "i4": _i4_case, "rms": _rms_case}[case[0]]
     fn, Yref = build(dev, *case[1:])
     Y = fn()
@@ -198,7 +203,7 @@ def test_split_flags_survive_other_kernels(dev, monkeypatch, name, case, other_e
 
 
 @pytest.mark.parametrize("kind,M,K,N", [("i4", 1, 4096, 4096), ("i4", 8, 11008, 4096), ("q4", 16, 14336, 4096),
-                                        ("q4", 4, 11008, 4096)])
+                                        ("q4", 4, 11008, 4096), ("q4", 32, 14336, 4096)])
 def test_split_flags_any_start_value(dev, kind, M, K, N):
     """Split flags need no initial value: a caller's workspace whose counter area
     is zero and whose every other byte is 0xFF (each flag word 0xFFFFFFFF, so the
