@@ -178,7 +178,9 @@ q4_skinny_kernel(SkinnyArgs a) {
         }
         __syncthreads();
     }
-    if (a.S == 1) return;
+    // Without counters the partials are summed by q4_skinny_reduce_kernel (the
+    // kernel boundary orders it after this one).
+    if (a.S == 1 || !a.counters) return;
 
     // ---- split-K: the last WG to arrive for this tile sums the partials ----
     __threadfence();
@@ -204,6 +206,24 @@ q4_skinny_kernel(SkinnyArgs a) {
         const int n = n0 + t * 16 + (l & 15);
         if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (_Float16)s;
     }
+}
+
+// Sums the S fp32 partials of the tiles from n_begin on in split order (the
+// fragment layout above: lane l of fragment (mt, t) holds rows 4 (l / 16) + i,
+// column l % 16) and stores fp16.
+__global__ void __launch_bounds__(256) q4_skinny_reduce_kernel(SkinnyArgs a, int MT, int NT) {
+    const int ncols = a.N - a.n_begin;
+    const int64_t v0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (v0 >= (int64_t)a.M * ncols) return;
+    const int m = (int)(v0 / ncols), nn = (int)(v0 % ncols);
+    const int tile = nn / (16 * NT), tn = nn % (16 * NT);
+    const int f = (m / 16) * NT + tn / 16;
+    const int v = (((m % 16) / 4) * 16 + tn % 16) * 4 + m % 4;
+    const int nfrag = MT * NT;
+    const float *p = a.partials + (int64_t)tile * a.S * (nfrag * 256) + f * 256 + v;
+    float s = 0.f;
+    for (int sp = 0; sp < a.S; ++sp) s += p[(int64_t)sp * nfrag * 256];
+    a.Y[(int64_t)m * a.ldy + a.n_begin + nn] = (_Float16)s;
 }
 
 // ---- launch configuration ---------------------------------------------------
@@ -258,10 +278,23 @@ SkinnyCfg skinny_config(int64_t M, int64_t K, int64_t N) {
 
 size_t gemvm_workspace_bytes(int64_t M, int64_t K, int64_t N);
 
+// Tail split: the columns past the last whole 16-column tile, which the other
+// decode kernels leave to this one (N % 16 != 0), are one or two tiles; walking
+// all of K in one workgroup took 8-22 us there (M = 1 11008 x 4104: 22.5 us
+// against ~7 for 4096 columns), so their K is split over up to 32 workgroups
+// whose fp32 partials a second kernel sums.
+constexpr int SK_TAIL_SMAX = 32;
+static int skinny_tail_splits(int64_t K) {
+    const int64_t nb = K / QK;
+    return nb >= 64 ? (int)std::min<int64_t>(SK_TAIL_SMAX, nb / 16) : 1;
+}
+
 // The larger of this kernel's split-K needs and the small-batch GEMV's.
 size_t skinny_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     const SkinnyCfg c = skinny_config(M, K, N);
     size_t need = 0;
+    if (N % 16 && skinny_tail_splits(K) > 1)
+        need = COUNTER_BYTES + (size_t)2 * skinny_tail_splits(K) * ((M + 15) / 16) * c.NT * 256 * sizeof(float);
     if (c.S > 1) {
         const int MT = (int)((M + 15) / 16);
         const int64_t tiles = (N + 16 * c.NT - 1) / (16 * c.NT);
@@ -301,7 +334,7 @@ hipError_t launch_skinny(const _Float16 *X, int64_t ldx, const uint8_t *W, _Floa
             e = launch_decode_lds(X, ldx, W, Y, ldy, M, K, N, &n_begin, s);
         if (e != hipSuccess || n_begin == N) return e;
     }
-    const SkinnyCfg c = skinny_config(M, K, N);
+    SkinnyCfg c = skinny_config(M, K, N);
     const int MT = (M + 15) / 16;
     const int64_t tiles = (N - n_begin + 16 * c.NT - 1) / (16 * c.NT);
     SkinnyArgs a;
@@ -312,6 +345,25 @@ hipError_t launch_skinny(const _Float16 *X, int64_t ldx, const uint8_t *W, _Floa
     if (c.S > 1) {
         a.counters = (uint32_t *)ws;
         a.partials = (float *)((char *)ws + COUNTER_BYTES);
+    }
+    const bool tail = n_begin > 0 && tiles <= 2 && ws && skinny_tail_splits(K) > 1;
+    if (tail) {
+        c.S = a.S = skinny_tail_splits(K);
+        c.WAVES = 8;
+        a.counters = nullptr;
+        a.partials = (float *)((char *)ws + COUNTER_BYTES);
+        hipError_t e;
+        switch (MT) {
+            case 1: e = launch_mt<1>(a, c, (int)tiles, s); break;
+            case 2: e = launch_mt<2>(a, c, (int)tiles, s); break;
+            case 3: e = launch_mt<3>(a, c, (int)tiles, s); break;
+            default: e = launch_mt<4>(a, c, (int)tiles, s); break;
+        }
+        if (e != hipSuccess) return e;
+        const int64_t nout = (int64_t)M * (N - n_begin);
+        hipLaunchKernelGGL(q4_skinny_reduce_kernel, dim3((unsigned)((nout + 255) / 256)), dim3(256), 0, s, a,
+                           MT > 4 ? 4 : MT, c.NT);
+        return hipGetLastError();
     }
     switch (MT) {
         case 1: return launch_mt<1>(a, c, (int)tiles, s);

@@ -257,6 +257,7 @@ PATHS = {
     "gemv_span_split": {"MCQ4_GEMV_SPAN": "1"},
     "gemv_span_split_off": {"MCQ4_GEMV_SPAN": "0"},
     "gemv_span_off": {"MCQ4_GEMV_SPAN": "0"},
+    "skinny_tail": {},
 }
 PATH_SHAPES = {
     "gemv_dma": [(1, 32, 16), (1, 352, 264), (1, 1024, 4104), (1, 11008, 512), (1, 4096, 65536),
@@ -282,6 +283,12 @@ PATH_SHAPES = {
                         (3, 11008, 4096), (7, 4096, 4096), (12, 4096, 2048), (16, 16384, 4096),
                         (5, 352, 1024), (9, 2080, 2048), (13, 1024, 64), (6, 4128, 3008)],
     "gemv_span_split_off": [(4, 14336, 4096), (16, 4096, 4096)],
+    # N % 16 != 0 with K >= 2048: the columns past the last whole 16-column tile, K
+    # split over workgroups whose partials a second kernel sums; after the M = 1
+    # strip kernel, the small-batch strip kernel (one and two row blocks) and, at
+    # N >= 8192, 32-column tail tiles.
+    "skinny_tail": [(1, 4096, 4104), (1, 11008, 4104), (1, 2048, 2056), (1, 4096, 32008), (3, 2048, 2056),
+                    (12, 11008, 8200), (20, 4096, 1032), (32, 14336, 520), (16, 4096, 8200)],
     "decode_lds_m1": [(1, 352, 264), (1, 4096, 1032)],
     "gemvm": [(2, 32, 16), (3, 352, 264), (4, 1024, 4104), (5, 11008, 512), (8, 4096, 14336),
               (11, 2048, 1040), (16, 14336, 4096), (16, 352, 8200)],
