@@ -79,6 +79,10 @@ struct GemvArgs {
     int tiles_per_w;
     int nb, N, ntiles, nbt;                  // N per weight; ntiles over all; nbt = batches per tile
     int xw;                                  // activation bytes per wave in LDS
+    // Columns of the last tile (one weight, TW = 16): 16, or 8 when N % 16 == 8;
+    // that tile's copies of the other chunks re-read its first chunk of the row,
+    // and only its first tail_cols outputs are stored.
+    int tail_cols = 16;
 };
 
 template <int R>
@@ -150,17 +154,23 @@ q4_gemv_dma_kernel(GemvArgs a) {
         wt[j] = w + (int64_t)lt * ROWB;
         yt[j] = y + lt * TW;
     }
+    // Chunks per row of the tile (CPR, or fewer for a partial last tile).
+    int tcpr[TPW];
+#pragma unroll
+    for (int j = 0; j < TPW; ++j)
+        tcpr[j] = !GROUP && TW == 16 && j < ntl && wg + j * G == ntiles - 1 ? a.tail_cols * BLOCK_BYTES / 16 : CPR;
     const int nbm = nbt > wave ? (nbt - wave + NW - 1) / NW : 0;  // my batches
     const int nmine = nbm * ntl;
 
     // Copy geometry per lane and copy i: strip chunk q = lane + 64 i of an item
     // (row q/CPR, 16-byte piece q%CPR); q >= 144 is masked off.
-    int crow[GV_LOADS];
+    int crow[GV_LOADS], cpc[GV_LOADS];
     uint32_t coff[GV_LOADS];
 #pragma unroll
     for (int i = 0; i < GV_LOADS; ++i) {
         const int q = lane + 64 * i;
         crow[i] = q < GV_WCH ? q / CPR : 0;
+        cpc[i] = q < GV_WCH ? q % CPR : 0;
         coff[i] = q < GV_WCH ? (uint32_t)(q / CPR) * grow + 16u * (uint32_t)(q % CPR) : 0u;
     }
     // Item (batch index m of this wave, tile j) into ring slot `slot`.
@@ -170,8 +180,10 @@ q4_gemv_dma_kernel(GemvArgs a) {
         const uint8_t *wb = wt[j] + (int64_t)row0 * grow;
 #pragma unroll
         for (int i = 0; i < GV_LOADS; ++i) {
-            // Rows past K re-copy row 0 (valid memory, never read back).
-            const uint32_t off = crow[i] < rows ? coff[i] : coff[i] - (uint32_t)crow[i] * grow;
+            // Rows past K re-copy row 0, and chunks past a partial tile's columns
+            // the row's first chunk (valid memory, never stored).
+            uint32_t off = crow[i] < rows ? coff[i] : coff[i] - (uint32_t)crow[i] * grow;
+            if (cpc[i] >= tcpr[j]) off -= 16u * (uint32_t)cpc[i];
             if (i < GV_LOADS - 1 || lane < GV_WCH - 64 * (GV_LOADS - 1))
                 __builtin_amdgcn_global_load_lds(
                     (void *)(wb + off),
@@ -317,7 +329,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
         float s = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; ++w) s += red[(j * NW + w) * TW + col];
-        yt[j][col] = (_Float16)s;
+        if (GROUP || TW != 16 || wg + j * G != ntiles - 1 || col < a.tail_cols) yt[j][col] = (_Float16)s;
     }
 }
 
@@ -410,10 +422,13 @@ hipError_t launch_gemv_dma_group(const _Float16 *X, const uint8_t *const *W, _Fl
         return launch_gemv_t<GV_RING, GV_TPW_MAX, 8, GV_WIDE>(a, grid, s);
     }
     constexpr int B = GV_ITEM / (16 * BLOCK_BYTES);
-    a.tiles_per_w = N / 16;
+    // One weight with N % 16 == 8: a last tile of 8 columns (the copies stay
+    // inside each row, N % 8 == 0 keeps its 144 bytes whole chunks).
+    a.tiles_per_w = count == 1 ? (N + 15) / 16 : N / 16;
+    a.tail_cols = count == 1 && N % 16 ? N % 16 : 16;
     a.ntiles = count * a.tiles_per_w;
     a.nbt = (a.nb + B - 1) / B;
-    *n_done = a.tiles_per_w * 16;
+    *n_done = count == 1 ? N : a.tiles_per_w * 16;
     // One 16-wave workgroup per CU and up to GV_TPW_MAX tiles each.  Larger N
     // (more than 1024 tiles) runs 8-wave workgroups of GV_TPW_MAX tiles, two per
     // CU, backfilled as they finish (16-column tiles at N = 128256: 56 vs 66 us

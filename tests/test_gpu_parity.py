@@ -287,7 +287,9 @@ PATH_SHAPES = {
     # split over workgroups whose partials a second kernel sums; after the M = 1
     # strip kernel, the small-batch strip kernel (one and two row blocks) and, at
     # N >= 8192, 32-column tail tiles.
-    "skinny_tail": [(1, 4096, 4104), (1, 11008, 4104), (1, 2048, 2056), (1, 4096, 32008), (3, 2048, 2056),
+    # (At M = 1 the strip kernel takes an 8-column last tile itself.)
+    "skinny_tail": [(1, 4096, 4104), (1, 11008, 4104), (1, 2048, 2056), (1, 4096, 32008), (1, 32, 24),
+                    (1, 4128, 40), (1, 352, 1048), (3, 2048, 2056),
                     (12, 11008, 8200), (20, 4096, 1032), (32, 14336, 520), (16, 4096, 8200)],
     "decode_lds_m1": [(1, 352, 264), (1, 4096, 1032)],
     "gemvm": [(2, 32, 16), (3, 352, 264), (4, 1024, 4104), (5, 11008, 512), (8, 4096, 14336),
