@@ -27,7 +27,7 @@ const char *const kNames[] = {
     "MCQ4_DECODE_PATH",     // direct: the register-load decode kernel
     "MCQ4_GEMM2_BM",        // 128 | 256: row tile of the fallback prefill kernel
     "MCQ4_SPLIT_FOREIGN",   // mask: split-K splits treated as run on another XCD (recompute path)
-    "MCQ4_SPLIT_SPIN",      // polls of a split flag before the split is recomputed (default 8192; 0: at once)
+    "MCQ4_SPLIT_SPIN",      // polls of a split flag before the split is recomputed (default 256; 0: at once)
     // per-group INT4 / INT8 path
     "MCQ4_I4_PATH",         // generic: the general kernel for everything
     "MCQ4_I4_RMS_FUSE",     // 0: fused RMSNorm + INT4 at M = 1 runs as two kernels
@@ -79,7 +79,7 @@ uint32_t split_foreign_mask() {
 }
 uint32_t split_spin() {
     const char *v = opt("MCQ4_SPLIT_SPIN");
-    return v ? (uint32_t)std::min<unsigned long>(strtoul(v, nullptr, 0), 1u << 20) : 8192u;
+    return v ? (uint32_t)std::min<unsigned long>(strtoul(v, nullptr, 0), 1u << 20) : 256u;
 }
 }  // namespace mcq4
 

@@ -18,7 +18,7 @@ inline bool opt_is(const char *name, char c) {
 // drives the recompute path on hardware where the placement always holds.
 uint32_t split_foreign_mask();
 // Polls of a split-K flag before the waiting workgroup recomputes that split
-// (MCQ4_SPLIT_SPIN, default 8192, at most 2^20; 0 drives the recompute path
+// (MCQ4_SPLIT_SPIN, default 256, at most 2^20; 0 drives the recompute path
 // for every other split).
 uint32_t split_spin();
 }  // namespace mcq4

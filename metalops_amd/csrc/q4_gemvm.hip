@@ -66,6 +66,9 @@ struct GemvMArgs {
     uint32_t *flags;
     uint32_t spin;       // polls of a flag before its split is recomputed
     uint32_t foreign;    // splits treated as run on another XCD (test switch)
+    // Columns of the last tile: 16, or 8 when N % 16 == 8 (its copies of chunks
+    // 9..17 of a row re-read chunks 0..8; outputs past N are not stored).
+    int tail_cols;
 };
 
 // RB row blocks of 16 activation rows (M <= 16 RB): each K-block row's B
@@ -111,11 +114,13 @@ q4_gemvm_kernel(GemvMArgs a) {
 
     int crow[3];
     uint32_t coff[3];
+    uint32_t past8 = 0;                           // bit i: copy i's chunk lies past a row's 9th
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int q = lane + 64 * i;
         crow[i] = q < GM_WCH ? q / 18 : 0;
         coff[i] = q < GM_WCH ? (uint32_t)(q / 18) * grow + 16u * (uint32_t)(q % 18) : 0u;
+        past8 |= (q < GM_WCH && q % 18 >= 9 ? 1u : 0u) << i;
     }
     const uint8_t *xrow[RB];
 #pragma unroll
@@ -134,9 +139,13 @@ q4_gemvm_kernel(GemvMArgs a) {
         const int row0 = (b0 + wave + WAVES * m) * GM_B;
         const int rows = min(GM_B, a.nb - row0);
         const uint8_t *wb = a.W + (int64_t)(wg + j * G) * GM_ROW + (int64_t)row0 * grow;
+        // An 8-column last tile: chunks 9..17 of a row re-read chunks 0..8 (the
+        // row's valid bytes; those columns are not stored).
+        const bool half = a.tail_cols < 16 && wg + j * G == a.ntiles - 1;
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
-            const uint32_t off = crow[i] < rows ? coff[i] : coff[i] - (uint32_t)crow[i] * grow;
+            uint32_t off = crow[i] < rows ? coff[i] : coff[i] - (uint32_t)crow[i] * grow;
+            if (half && ((past8 >> i) & 1)) off -= 144u;
             if (i < 2 || lane < GM_WCH - 128)
                 __builtin_amdgcn_global_load_lds(
                     (void *)(wb + off),
@@ -290,7 +299,9 @@ q4_gemvm_kernel(GemvMArgs a) {
 #pragma unroll
             for (int w = 0; w < WAVES; ++w) s += red[((j * WAVES + w) * 16 + (rr & 15)) * 16 + col];
             const int n = (wg + j * G) * 16 + col;
-            if (a.S == 1) a.Y[(int64_t)rr * a.ldy + n] = (_Float16)s;
+            if (a.S == 1) {
+                if (n < a.N) a.Y[(int64_t)rr * a.ldy + n] = (_Float16)s;
+            }
             else a.part[((int64_t)sp * a.M + rr) * (16 * a.ntiles) + n] = s;
         }
     }
@@ -340,13 +351,13 @@ q4_gemvm_kernel(GemvMArgs a) {
     const int64_t pstride = (int64_t)a.M * 16 * a.ntiles;         // floats per split
     for (int v = tid; v < TPW * 256 * RB; v += WAVES * 64) {   // v = (rb, j, row, col)
         const int j = (v >> 8) % TPW, rr = 16 * (v / (256 * TPW)) + ((v >> 4) & 15), col = v & 15;
-        if (j >= ntl || rr >= a.M) continue;
+        const int n = (wg + j * G) * 16 + col;
+        if (j >= ntl || rr >= a.M || n >= a.N) continue;          // (columns past N: none stored)
         float own = 0.f;
         if (RB == 1) {
 #pragma unroll
             for (int w = 0; w < WAVES; ++w) own += red[((j * WAVES + w) * 16 + rr) * 16 + col];
         }
-        const int n = (wg + j * G) * 16 + col;
         const float *base = a.part + (int64_t)rr * (16 * a.ntiles) + n;
         float pv[8];
 #pragma unroll
@@ -377,7 +388,7 @@ __global__ void __launch_bounds__(256) q4_gemvm_reduce_kernel(GemvMArgs a) {
     const int rr = (int)(v / nc), n = (int)(v % nc);
     float s = 0.f;
     for (int sp = 0; sp < a.S; ++sp) s += a.part[((int64_t)sp * a.M + rr) * nc + n];
-    a.Y[(int64_t)rr * a.ldy + n] = (_Float16)s;
+    if (n < a.N) a.Y[(int64_t)rr * a.ldy + n] = (_Float16)s;
 }
 
 static size_t gemvm_lds_bytes(int waves, int tpw) {
@@ -451,7 +462,7 @@ struct GmPlan {
     int waves, tpw, grid, S, bps;
 };
 static GmPlan gemvm_plan(int64_t M, int64_t K, int64_t N) {
-    const int ntiles = (int)(N / 16), nbt = (int)((K / QK + GM_B - 1) / GM_B);
+    const int ntiles = (int)((N + 15) / 16), nbt = (int)((K / QK + GM_B - 1) / GM_B);
     int waves = 16;
     // Two row blocks: 8-wave workgroups, one per CU (their registers fill the SIMDs).
     if (M > 16) waves = 8;
@@ -483,7 +494,7 @@ size_t gemvm_workspace_bytes(int64_t M, int64_t K, int64_t N) {
     if (M < 2 || M > 32 || N < 16 || K < QK) return 0;
     const GmPlan p = gemvm_plan(M, K, N);
     // Partials follow the workspace's counter area, which other kernels rely on staying zero.
-    const size_t own = p.S > 1 ? COUNTER_BYTES + (size_t)p.S * M * (N / 16) * 16 * sizeof(float) +
+    const size_t own = p.S > 1 ? COUNTER_BYTES + (size_t)p.S * M * ((N + 15) / 16) * 16 * sizeof(float) +
                                      (size_t)(p.grid + 7) / 8 * 8 * p.S * sizeof(uint32_t)
                                : 0;
     return std::max(own, gemv_span_split_workspace_bytes(M, K, N));
@@ -513,9 +524,10 @@ hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
     GemvMArgs a;
     a.X = X; a.ldx = ldx; a.W = W; a.Y = Y; a.ldy = ldy;
     a.M = M; a.nb = K / QK; a.N = N;
-    a.ntiles = N / 16;
+    a.ntiles = (N + 15) / 16;
+    a.tail_cols = N % 16 ? N % 16 : 16;
     a.nbt = (a.nb + GM_B - 1) / GM_B;
-    *n_done = a.ntiles * 16;
+    *n_done = N;
     const GmPlan p = gemvm_plan(M, K, N);
     a.S = p.S; a.bps = p.bps;
     a.part = nullptr;
@@ -525,8 +537,11 @@ hipError_t launch_gemvm(const _Float16 *X, int64_t ldx, const uint8_t *W, _Float
     if (p.S > 1) {
         if (!ws) return hipErrorInvalidValue;
         a.part = (float *)((char *)ws + COUNTER_BYTES);
-        if (!opt_is("MCQ4_XCD_LOCAL", '0') && p.S <= 8)
-            a.flags = (uint32_t *)(a.part + (int64_t)p.S * M * (N / 16) * 16);
+        // Split 0 waits for the other splits' flags, so the exchange needs every
+        // workgroup resident at once (one per CU); a larger grid (only a forced
+        // MCQ4_GEMVM_SPLIT makes one) sums in the reduction kernel instead.
+        if (!opt_is("MCQ4_XCD_LOCAL", '0') && p.S <= 8 && (p.grid + 7) / 8 * 8 * p.S <= 256)
+            a.flags = (uint32_t *)(a.part + (int64_t)p.S * M * a.ntiles * 16);
     }
     // One batch per wave at most: the activations and -S once per wave
     // (MCQ4_GEMVM_HOIST=0 turns it off).
