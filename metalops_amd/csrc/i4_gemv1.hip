@@ -559,9 +559,13 @@ size_t i4_gemv1_workspace_bytes(int64_t M, int64_t K, int64_t N, int64_t gs) {
 }
 
 // The XCD-local exchange (default; MCQ4_XCD_LOCAL=0 selects the agent-scope
-// one) needs K split and at most 4096 tiles per class of the padded grid.
+// one) needs K split, at most 4096 tiles per class of the padded grid, and the
+// whole grid resident at once (split 0 waits for the other splits' flags): at
+// most 256 workgroups.  Longer K on wide N can split further (K = 16384 at
+// N = 32768: 1024 workgroups); those shapes take the agent-scope exchange,
+// whose last arrival waits on nobody.
 static bool use_xcd_local(int ntiles, int S) {
-    return !opt_is("MCQ4_XCD_LOCAL", '0') && S > 1 && (ntiles + 7) / 8 <= 4096;
+    return !opt_is("MCQ4_XCD_LOCAL", '0') && S > 1 && (ntiles + 7) / 8 <= 4096 && (ntiles + 7) / 8 * 8 * S <= 256;
 }
 
 template <int SZ, int ACT, bool XL, int RB, int WB, bool NORM = false>
