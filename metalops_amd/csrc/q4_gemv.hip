@@ -121,6 +121,12 @@ q4_gemv_dma_kernel(GemvArgs a) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 15, g = lane >> 4;
+    // MFMA lane rows g = 0..3 take K quarters kq = 0, 2, 1, 3 of each block (the
+    // activations to match): a 32-lane half then reads quarters {0, 2} or {1, 3}
+    // of the 16 columns' nibbles, whose words fall on the 32 LDS banks with fewer
+    // conflicts than {0, 1} / {2, 3} (M = 1: 9 against 11 cycles per four
+    // half-wave reads, M >= 2: 8 against 12).
+    const int kq = ((g & 1) << 1) | (g >> 1);
 
     // LDS: [NW waves x activations][NW waves x R slots][partials when SEPRED]
     uint8_t *xs = smem + wave * xw;
@@ -214,7 +220,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
     const int npro = min(R - 1, nmine);
     for (int k = 0; k < npro; ++k) issue_next();
 
-    const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
+    const int qoff = c * BLOCK_BYTES + 2 + 4 * kq;
     const uint32_t qal = (uint32_t)(qoff & ~3), qsh = (uint32_t)(qoff & 3) * 8;
     // Only lanes g == 0 keep their sums (M == 1: every A row is the activation
     // row), so their second word is taken where it holds the block's scale -- after
@@ -253,7 +259,7 @@ q4_gemv_dma_kernel(GemvArgs a) {
                     // they were copied before any weights, so at most the items in
                     // flight (this one included) are newer.
                     gv_wait<R + 1>(min(R, nmine - k));
-                    const uint32_t xa = lds_addr(xs + m * (B * 64) + 16 * g);
+                    const uint32_t xa = lds_addr(xs + m * (B * 64) + 16 * kq);
 #pragma unroll
                     for (int u = 0; u < B; ++u) {
                         const uint4_t x = bitcast<uint4_t>(*(const lds_half8 *)(lds_ptr(xa) + u * 64));

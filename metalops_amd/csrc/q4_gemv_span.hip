@@ -120,6 +120,12 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 15, g = lane >> 4;
+    // MFMA lane rows g = 0..3 take K quarters kq = 0, 2, 1, 3 of each block (the
+    // activations to match): a 32-lane half then reads quarters {0, 2} or {1, 3}
+    // of the 16 columns' nibbles, whose words fall on the 32 LDS banks with fewer
+    // conflicts than {0, 1} / {2, 3} (M = 1: 9 against 11 cycles per four
+    // half-wave reads, M >= 2: 8 against 12).
+    const int kq = ((g & 1) << 1) | (g >> 1);
 
     constexpr int XS = GR == 1 ? GS_XS : 0;
     uint8_t *xs = smem + wave * (GS_B * 64);
@@ -152,7 +158,7 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
     const int rows = max(0, min(GS_B, kbe - row0));                // 0: no item for this wave
     const uint8_t *wb = W + (int64_t)g0 * 288 + (int64_t)row0 * grow;
 
-    const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
+    const int qoff = c * BLOCK_BYTES + 2 + 4 * kq;
     const uint32_t qal = (uint32_t)(qoff & ~3), qsh = (uint32_t)(qoff & 3) * 8;
     const uint32_t doff = (uint32_t)(c * BLOCK_BYTES);
     // M == 1: only lanes g == 0 keep their sums (every A row is the one activation
@@ -192,7 +198,7 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
         } else {
             // Lane (c, g): activation row min(c / (16 / GR), M - 1), elements 8g..8g+7
             // of each K block of the batch (blocks past K clamp to the last one).
-            const uint8_t *xrow = (const uint8_t *)X + (int64_t)min(c / (16 / GR), M - 1) * ldx * 2 + 16 * g;
+            const uint8_t *xrow = (const uint8_t *)X + (int64_t)min(c / (16 / GR), M - 1) * ldx * 2 + 16 * kq;
 #pragma unroll
             for (int u = 0; u < GS_B; ++u) xr[u] = *(const uint4_t *)(xrow + (int64_t)min(row0 + u, nb - 1) * 64);
         }
@@ -210,7 +216,7 @@ q4_gemv_span_kernel(GemvSpanArgs a) {
         wait_vmcnt<NC>();
         half8_t xq[GS_B];
         float4_t negs[HOIST ? GS_B : 1];
-        const uint32_t xa = lds_addr(xs + 16 * g);
+        const uint32_t xa = lds_addr(xs + 16 * kq);
 #pragma unroll
         for (int u = 0; u < GS_B; ++u) {
             uint4_t x;

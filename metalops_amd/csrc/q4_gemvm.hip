@@ -85,6 +85,12 @@ q4_gemvm_kernel(GemvMArgs a) {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 15, g = lane >> 4;
+    // MFMA lane rows g = 0..3 take K quarters kq = 0, 2, 1, 3 of each block (the
+    // activations to match): a 32-lane half then reads quarters {0, 2} or {1, 3}
+    // of the 16 columns' nibbles, whose words fall on the 32 LDS banks with fewer
+    // conflicts than {0, 1} / {2, 3} (M = 1: 9 against 11 cycles per four
+    // half-wave reads, M >= 2: 8 against 12).
+    const int kq = ((g & 1) << 1) | (g >> 1);
     const uint32_t grow = (uint32_t)a.N * BLOCK_BYTES;
 
     // LDS: [WAVES x 2 slots][partials: TPW x WAVES x 16 rows x 16 columns]
@@ -125,7 +131,7 @@ q4_gemvm_kernel(GemvMArgs a) {
     const uint8_t *xrow[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
-        xrow[rb] = (const uint8_t *)a.X + (int64_t)min(16 * rb + c / (16 / GR), a.M - 1) * a.ldx * 2 + 16 * g;
+        xrow[rb] = (const uint8_t *)a.X + (int64_t)min(16 * rb + c / (16 / GR), a.M - 1) * a.ldx * 2 + 16 * kq;
     uint4_t xr[RB][GM_B];
     auto load_x = [&](int m) {
         const int row0 = (b0 + wave + WAVES * m) * GM_B;
@@ -166,7 +172,7 @@ q4_gemvm_kernel(GemvMArgs a) {
     }
     if (nmine > 0) issue_next();
 
-    const int qoff = c * BLOCK_BYTES + 2 + 4 * g;
+    const int qoff = c * BLOCK_BYTES + 2 + 4 * kq;
     const uint32_t qal = (uint32_t)(qoff & ~3), qsh = (uint32_t)(qoff & 3) * 8;
     const uint32_t doff = (uint32_t)(c * BLOCK_BYTES);
     // fp16 exponent words: 1024 + q for a low nibble, 64 + q for a high nibble
